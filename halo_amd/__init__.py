@@ -1,0 +1,23 @@
+"""halo_amd -- MI355X-native tiered-KV chunked attention (HALO "Path D").
+
+Public API mirrors the reference package ``halo`` (halo/__init__.py:32-54)
+for the tiered-KV path: ``HALOConfig``, ``wrap_with_halo``,
+``HALOCacheChunked``, ``HALOScorer``, ``HALODemoter``, ``HALORefetcher``,
+``MemoryTier``, ``TieredStorage``; the kernel module keeps the name and call
+signatures of ``halo.triton_chunked``.  Compute runs in hand-written HIP
+kernels for gfx950 (``halo_amd/csrc``) behind the C-ABI in
+``include/halo_hip.h``.
+"""
+from . import _native
+from .triton_chunked import (  # noqa: F401
+    HAS_HIP,
+    HAS_TRITON,
+    finalize,
+    init_acc,
+    triton_chunked_attention,
+    triton_chunked_attention_single_launch,
+    triton_chunked_attention_streamed,
+    update_chunk,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,138 @@
+"""ctypes binding of libhalo_hip.so, the C-ABI declared in include/halo_hip.h.
+
+The library is built in-tree (``halo_amd/_lib/libhalo_hip.so``) by
+``__graft_entry__.build()`` or ``make -C halo_amd/csrc``.  It links the HIP
+runtime by soname (``libamdhip64.so.7``); torch is imported first so that the
+library binds to the runtime torch already loaded and both share one device
+context.
+
+There is no CPU fallback: every product entry point calls :func:`lib`, which
+raises ``RuntimeError`` when the library is missing or no GPU is visible.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch  # noqa: F401  -- must load torch's HIP runtime before the library
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libhalo_hip.so")
+
+HALO_OK = 0
+HALO_E_INVALID = -1
+HALO_E_UNSUPPORTED = -2
+HALO_E_HIP = -3
+HALO_E_WORKSPACE = -4
+
+F32, BF16, F16 = 0, 1, 2
+CHUNK_CAUSAL = 1
+
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_c_void_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_size_t = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/halo_hip.h one to one.
+_SIGNATURES = {
+    "halo_decode_workspace_size": (_size_t, [_i32, _i32, _i32]),
+    "halo_decode_attn": (_i32, [
+        _c_void_p, _i64, _i64, _i32,             # q, q_stride_b, q_stride_h, dtype
+        _i32, _i32, _i32, _i32, _i32,            # B, H, H_kv, D, rep_t
+        _c_void_p, _i32,                         # descs, n_desc
+        _c_void_p, _i32,                         # work, n_work
+        _c_void_p, _i32,                         # group_offsets, n_groups
+        _c_void_p, _f32,                         # q_pos, scale
+        _c_void_p, _c_void_p, _c_void_p, _i64, _i32,  # m, l, o, acc_stride_b, acc_mode
+        _c_void_p, _i32, _c_void_p,              # out, out_dtype, lse
+        _c_void_p, _size_t, _c_void_p,           # workspace, bytes, counters
+        _c_void_p,                               # stream
+    ]),
+    "halo_finalize": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
+                             _c_void_p, _i32, _c_void_p, _c_void_p]),
+    "halo_lse_merge": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
+                              _c_void_p, _c_void_p, _c_void_p]),
+    "halo_last_error": (ctypes.c_char_p, []),
+    "halo_build_info": (ctypes.c_char_p, []),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def _load() -> Optional[ctypes.CDLL]:
+    global _lib, _load_error
+    if _lib is not None or _load_error is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        _load_error = (f"{_LIB_PATH} is not built; run __graft_entry__.build() "
+                       f"or `make -C halo_amd/csrc`")
+        return None
+    try:
+        handle = ctypes.CDLL(_LIB_PATH)
+    except OSError as exc:  # pragma: no cover - depends on the host
+        _load_error = f"cannot load {_LIB_PATH}: {exc}"
+        return None
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return _lib
+
+
+def loadable() -> bool:
+    """True when the shared library loads (no GPU needed)."""
+    return _load() is not None
+
+
+def available() -> bool:
+    """True when the library loads and a GPU is visible."""
+    return loadable() and torch.cuda.is_available()
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError when it or the GPU is missing."""
+    handle = _load()
+    if handle is None:
+        raise RuntimeError(f"HALO HIP library unavailable: {_load_error}")
+    if not torch.cuda.is_available():
+        raise RuntimeError("HALO HIP kernels need a GPU (torch.cuda.is_available() is False)")
+    return handle
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(status: int, what: str) -> None:
+    """Map a C-ABI status to the exception the reference raises."""
+    if status == HALO_OK:
+        return
+    msg = (_load().halo_last_error() or b"").decode(errors="replace")
+    if status == HALO_E_INVALID:
+        raise AssertionError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed ({status}): {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def stream_ptr(stream: Optional[torch.cuda.Stream] = None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else int(t.data_ptr())

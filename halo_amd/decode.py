@@ -1,0 +1,295 @@
+"""Planning and launching of the split-K decode-attention kernel.
+
+A *plan* is the device-resident chunk table (``halo_chunk_desc`` records) and
+work list (``{desc, group, t0, t1}`` int32 quadruples) of one
+``halo_decode_attn`` launch.  Building it costs a few host microseconds per
+chunk; a plan can be replayed for as long as the K/V tensors it points at
+stay alive (the plan keeps references to them), which is how the benchmark
+and graph-captured decode loops use it.
+
+Reference behaviour mirrored here: the chunk list of
+``triton_chunked_attention`` (halo/triton_chunked.py:210-267) and the
+per-launch arguments of ``update_chunk`` (halo/triton_chunked.py:151-192).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native as nat
+
+DESC_DTYPE = np.dtype([
+    ("k", "<u8"), ("v", "<u8"),
+    ("ksb", "<i8"), ("ksh", "<i8"), ("kst", "<i8"),
+    ("vsb", "<i8"), ("vsh", "<i8"), ("vst", "<i8"),
+    ("start", "<i8"), ("T", "<i4"), ("flags", "<i4"), ("batch", "<i4"), ("res", "<i4"),
+])
+assert DESC_DTYPE.itemsize == 88
+
+_WAVES_PER_GROUP = 4
+_TILE_ROWS = 64
+
+
+@dataclass
+class ChunkRef:
+    """One KV chunk: k, v are (B, H_kv, T_c, D) -- or (H_kv, T_c, D) when
+    ``batch`` >= 0 names the single batch row the chunk belongs to."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+    chunk_start: int
+    causal: bool = True
+    batch: int = -1
+
+    @property
+    def T(self) -> int:
+        return int(self.k.shape[-2])
+
+
+@dataclass
+class DecodePlan:
+    B: int
+    H: int
+    H_kv: int
+    D: int
+    rep_t: int
+    dtype: torch.dtype
+    descs: torch.Tensor          # uint8 [n_desc*88] on device
+    work: torch.Tensor           # int32 [n_work*4] on device
+    offsets: torch.Tensor        # int32 [n_groups+1] on device
+    n_desc: int
+    n_work: int
+    n_groups: int
+    rows: int                    # attended K/V rows summed over (b, h_kv)
+    keep: list = field(default_factory=list)  # tensors the descriptors point at
+    work_host: Optional[np.ndarray] = None
+
+    @property
+    def kv_bytes(self) -> int:
+        """Algorithmic K+V bytes one launch streams (every row read once)."""
+        esz = torch.tensor([], dtype=self.dtype).element_size()
+        return self.rows * 2 * self.D * esz
+
+
+def choose_rep_t(rep: int) -> int:
+    for r in (1, 2, 4, 8):
+        if rep <= r:
+            return r
+    return 8
+
+
+def _check_kv(t: torch.Tensor, name: str) -> None:
+    if t.stride(-1) != 1:
+        raise AssertionError(f"{name}: head dim must be contiguous (stride {t.stride()})")
+    esz = t.element_size()
+    if t.data_ptr() % 16 or (t.stride(-2) * esz) % 16:
+        raise AssertionError(f"{name}: rows must be 16-byte aligned")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    esz = t.element_size()
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(-2) * esz) % 16:
+        return t.contiguous()
+    return t
+
+
+def _to_device(a: np.ndarray, device) -> torch.Tensor:
+    """Host array -> device tensor through pinned memory, without a host sync
+    (torch's pinned allocator keeps the staging block alive until the copy
+    has run)."""
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if torch.device(device).type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t
+
+
+def choose_split(total_rows: int, n_cu: int) -> int:
+    """Rows per work item: aim for about 4 workgroups per CU, in whole
+    4-wave x 64-row tiles, between 256 and 4096 rows."""
+    unit = _WAVES_PER_GROUP * _TILE_ROWS
+    target = max(1, total_rows // max(1, 4 * n_cu))
+    split = unit * max(1, math.ceil(target / unit))
+    return int(min(max(split, unit), 16 * unit))
+
+
+def _num_cus(device) -> int:
+    try:
+        return int(torch.cuda.get_device_properties(device).multi_processor_count)
+    except Exception:  # pragma: no cover
+        return 256
+
+
+def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
+               chunks: Sequence[ChunkRef], device, rep_t: Optional[int] = None,
+               split: Optional[int] = None, q_pos_host: Optional[Sequence[int]] = None) -> DecodePlan:
+    """Lay out descriptors and work items for a chunk list.
+
+    ``q_pos_host`` (per batch row) lets the planner drop causal chunks that
+    lie entirely after the query, as the reference's chunk walk does with
+    ``c0 > q_pos`` (halo/kv_cache_chunked.py:658,714); the kernel applies the
+    row-level causal cut itself either way.
+    """
+    if H % H_kv:
+        raise AssertionError(f"head count mismatch: q has {H}, kv has {H_kv}")
+    rep = H // H_kv
+    rep_t = rep_t or choose_rep_t(rep)
+    n_sub = -(-rep // rep_t)
+    n_groups = B * H_kv * n_sub
+
+    descs = np.zeros(len(chunks), dtype=DESC_DTYPE)
+    keep = []
+    for i, c in enumerate(chunks):
+        k, v = c.k, c.v
+        if k.dtype != dtype or v.dtype != dtype:
+            raise AssertionError(f"chunk {i}: dtype {k.dtype}/{v.dtype} != {dtype}")
+        if k.shape[-1] != D or v.shape[-1] != D:
+            raise AssertionError(f"chunk {i}: head dim {k.shape[-1]}/{v.shape[-1]} != {D}")
+        if c.batch < 0:
+            if k.dim() != 4 or k.shape[0] != B or k.shape[1] != H_kv:
+                raise AssertionError(f"k shape {tuple(k.shape)} != ({B}, {H_kv}, T_c, {D})")
+            if tuple(v.shape) != tuple(k.shape):
+                raise AssertionError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
+        else:
+            if k.dim() != 3 or k.shape[0] != H_kv or tuple(v.shape) != tuple(k.shape):
+                raise AssertionError(f"ragged chunk {i}: expected (H_kv, T_c, D), got {tuple(k.shape)}")
+        _check_kv(k, f"chunk {i} k")
+        _check_kv(v, f"chunk {i} v")
+        keep += [k, v]
+        d = descs[i]
+        d["k"], d["v"] = k.data_ptr(), v.data_ptr()
+        if c.batch < 0:
+            d["ksb"], d["ksh"], d["kst"] = k.stride(0), k.stride(1), k.stride(2)
+            d["vsb"], d["vsh"], d["vst"] = v.stride(0), v.stride(1), v.stride(2)
+        else:
+            d["ksb"], d["ksh"], d["kst"] = 0, k.stride(0), k.stride(1)
+            d["vsb"], d["vsh"], d["vst"] = 0, v.stride(0), v.stride(1)
+        d["start"] = int(c.chunk_start)
+        d["T"] = c.T
+        d["flags"] = nat.CHUNK_CAUSAL if c.causal else 0
+        d["batch"] = int(c.batch)
+
+    def live(c: ChunkRef, b: int) -> bool:
+        if c.batch >= 0 and c.batch != b:
+            return False
+        if c.T == 0:
+            return False
+        if c.causal and q_pos_host is not None and c.chunk_start > int(q_pos_host[b]):
+            return False
+        return True
+
+    total_rows = 0
+    for b in range(B):
+        for c in chunks:
+            if live(c, b):
+                rows = c.T
+                if c.causal and q_pos_host is not None:
+                    rows = min(rows, int(q_pos_host[b]) - c.chunk_start + 1)
+                total_rows += rows * H_kv * n_sub
+    if split is None:
+        split = choose_split(total_rows, _num_cus(device))
+
+    work = []
+    offsets = [0]
+    rows_attended = 0
+    for b in range(B):
+        live_idx = [i for i, c in enumerate(chunks) if live(c, b)]
+        for h in range(H_kv):
+            for s in range(n_sub):
+                g = (b * H_kv + h) * n_sub + s
+                n0 = len(work)
+                for i in live_idx:
+                    T = chunks[i].T
+                    hi = T
+                    if chunks[i].causal and q_pos_host is not None:
+                        hi = min(T, int(q_pos_host[b]) - chunks[i].chunk_start + 1)
+                    for t0 in range(0, hi, split):
+                        work.append((i, g, t0, min(t0 + split, hi)))
+                    if s == 0:
+                        rows_attended += hi
+                if len(work) == n0:
+                    work.append((0, g, 0, 0))
+                offsets.append(len(work))
+    work_np = np.asarray(work, dtype=np.int32).reshape(-1, 4)
+    dev_descs = _to_device(descs.view(np.uint8).copy(), device)
+    return DecodePlan(
+        B=B, H=H, H_kv=H_kv, D=D, rep_t=rep_t, dtype=dtype,
+        descs=dev_descs, work=_to_device(work_np.reshape(-1), device),
+        offsets=_to_device(np.asarray(offsets, dtype=np.int32), device),
+        n_desc=len(chunks), n_work=len(work), n_groups=n_groups,
+        rows=rows_attended, keep=keep, work_host=work_np,
+    )
+
+
+# ---------------------------------------------------------------------------
+# Workspace: per (device, stream) partial buffer plus self-cleaning counters.
+# ---------------------------------------------------------------------------
+_WS: dict = {}
+
+
+def workspace(device, stream_ptr: int, nbytes: int, n_counters: int):
+    key = (torch.device(device).index, stream_ptr)
+    ws, ctr = _WS.get(key, (None, None))
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    if ctr is None or ctr.numel() < n_counters:
+        ctr = torch.zeros(max(n_counters, 4096), dtype=torch.int32, device=device)
+    _WS[key] = (ws, ctr)
+    return ws, ctr
+
+
+def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
+           q_pos: Optional[torch.Tensor] = None,
+           m: Optional[torch.Tensor] = None, l: Optional[torch.Tensor] = None,
+           o: Optional[torch.Tensor] = None, acc_mode: int = 0,
+           out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+           stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Enqueue one ``halo_decode_attn`` on ``stream`` (default: current)."""
+    L = nat.lib()
+    if q.dim() != 3 or tuple(q.shape) != (plan.B, plan.H, plan.D):
+        raise AssertionError(f"expected q (B, H, D) = {(plan.B, plan.H, plan.D)}, got {tuple(q.shape)}")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if q.dtype != plan.dtype:
+        q = q.to(plan.dtype)
+    if q_pos is not None:
+        if q_pos.dtype != torch.int64 or q_pos.device != q.device:
+            q_pos = q_pos.to(device=q.device, dtype=torch.int64)
+        q_pos = q_pos.contiguous()
+        if q_pos.numel() != plan.B:
+            raise AssertionError(f"q_pos must have B={plan.B} entries, got {q_pos.numel()}")
+    BH, BHD = (plan.B, plan.H), (plan.B, plan.H, plan.D)
+    for t, name, shape in ((m, "m", BH), (l, "l", BH), (o, "o", BHD)):
+        if t is None:
+            continue
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise AssertionError(f"accumulator {name} must be contiguous float32 {shape}, got "
+                                 f"{t.dtype} {tuple(t.shape)}")
+    if (m is None) != (l is None) or (m is None) != (o is None):
+        raise AssertionError("m, l, o must be passed together")
+    if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()
+                            or tuple(lse.shape) != BH):
+        raise AssertionError(f"lse must be contiguous float32 {BH}")
+    if out is not None and (not out.is_contiguous() or tuple(out.shape) != BHD):
+        raise AssertionError(f"out must be contiguous {BHD}")
+    for t in (m, l, o, out, lse, q_pos):
+        if t is not None and t.device != q.device:
+            raise AssertionError("all tensors must be on the query's device")
+    sp = nat.stream_ptr(stream)
+    nbytes = int(L.halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
+    ws, ctr = workspace(q.device, sp, nbytes, plan.n_groups)
+    status = L.halo_decode_attn(
+        q.data_ptr(), q.stride(0), q.stride(1), nat.dtype_code(plan.dtype),
+        plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t,
+        plan.descs.data_ptr(), plan.n_desc,
+        plan.work.data_ptr(), plan.n_work,
+        plan.offsets.data_ptr(), plan.n_groups,
+        nat.ptr(q_pos), float(scale),
+        nat.ptr(m), nat.ptr(l), nat.ptr(o), plan.H, acc_mode,
+        nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse),
+        ws.data_ptr(), ws.numel(), ctr.data_ptr(), sp,
+    )
+    nat.check(status, "halo_decode_attn")

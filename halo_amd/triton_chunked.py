@@ -1,0 +1,267 @@
+"""Drop-in replacement for ``halo/triton_chunked.py`` on MI355X.
+
+The module keeps the reference's name and its public call signatures
+(halo/triton_chunked.py:141-501) so that ``from halo.triton_chunked import
+...`` can be rewritten to ``from halo_amd.triton_chunked import ...`` with no
+other change.  There is no Triton here: every entry point enqueues the
+hand-written HIP kernel of ``halo_amd/csrc/decode_attn.hip`` through the
+C-ABI.  ``HAS_TRITON`` keeps its role as the availability flag the cache
+reads (halo/kv_cache_chunked.py:156-163): it is True when the HIP library is
+loaded and a GPU is visible.
+
+Differences that are deliberate:
+  * one launch covers a whole chunk list (the reference launches once per
+    chunk, halo/triton_chunked.py:259-264), with chunk starts as runtime
+    table entries instead of a JIT constant (:52);
+  * a chunk whose rows are all causally masked contributes zero weight
+    (the PyTorch route's rule, halo/kv_cache_chunked.py:221-238) instead of
+    the NaN the Triton kernel produces when that chunk comes first (:122-128);
+  * every function accepts ``return_lse=True`` to also return the
+    log-sum-exp of the attended scores (the reference computes and drops it);
+  * ``_single_launch`` attends the hot tensors in place instead of copying
+    them device-to-device into the staging buffer (:474-477).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+from .decode import ChunkRef, build_plan, launch
+
+HAS_TRITON = nat.available()
+HAS_HIP = HAS_TRITON
+
+
+def _require() -> None:
+    nat.lib()  # raises RuntimeError when the library or the GPU is missing
+
+
+def init_acc(
+    *, B: int, H: int, D_v: int, device, dtype=torch.float32,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Initialise the (m, l, o) accumulators (halo/triton_chunked.py:141-148)."""
+    m = torch.full((B, H), float("-inf"), device=device, dtype=dtype)
+    l = torch.zeros((B, H), device=device, dtype=dtype)
+    o = torch.zeros((B, H, D_v), device=device, dtype=dtype)
+    return m, l, o
+
+
+def update_chunk(
+    *, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+    m: torch.Tensor, l: torch.Tensor, o: torch.Tensor,
+    scale: float, chunk_start: int, q_pos: torch.Tensor,
+    apply_causal: bool, block_n: int = 64,
+) -> None:
+    """Merge one chunk into the running (m, l, o) in place
+    (halo/triton_chunked.py:151-192).  ``block_n`` is accepted for signature
+    compatibility; the HIP kernel tiles by 64-row wavefront tiles."""
+    _require()
+    assert q.dim() == 3, f"expected q (B, H, D), got {q.shape}"
+    B, H, D = q.shape
+    H_KV = k.shape[1]
+    T_c = k.shape[2]
+    D_V = v.shape[-1]
+    assert k.shape == (B, H_KV, T_c, D), f"k shape {k.shape}"
+    assert v.shape == (B, H_KV, T_c, D_V), f"v shape {v.shape}"
+    assert D_V == D, "the HIP kernel requires D_v == D"
+    if T_c == 0:
+        return
+    dtype = k.dtype
+    plan = build_plan(B=B, H=H, H_kv=H_KV, D=D, dtype=dtype,
+                      chunks=[ChunkRef(_al(k), _al(v), int(chunk_start), bool(apply_causal))],
+                      device=q.device)
+    launch(plan, q, scale=float(scale), q_pos=q_pos, m=m, l=l, o=o, acc_mode=3)
+
+
+def finalize(
+    *, m: torch.Tensor, l: torch.Tensor, o: torch.Tensor,
+    out_dtype: torch.dtype, return_lse: bool = False,
+):
+    """out = o / (l > 0 ? l : 1) in ``out_dtype`` (halo/triton_chunked.py:195-207);
+    with ``return_lse`` also lse = m + log(l) (-inf where l == 0)."""
+    L = nat.lib()
+    B, H, D = o.shape
+    m_, l_, o_ = m.contiguous().float(), l.contiguous().float(), o.contiguous().float()
+    out = torch.empty((B, H, D), device=o.device, dtype=out_dtype)
+    lse = torch.empty((B, H), device=o.device, dtype=torch.float32) if return_lse else None
+    nat.check(L.halo_finalize(m_.data_ptr(), l_.data_ptr(), o_.data_ptr(), B, H, D,
+                              out.data_ptr(), nat.dtype_code(out_dtype), nat.ptr(lse),
+                              nat.stream_ptr()), "halo_finalize")
+    return (out, lse) if return_lse else out
+
+
+def _al(t: torch.Tensor) -> torch.Tensor:
+    esz = t.element_size()
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(-2) * esz) % 16:
+        return t.contiguous()
+    return t
+
+
+def _q3(q: torch.Tensor) -> torch.Tensor:
+    if q.dim() == 4:
+        assert q.shape[2] == 1, f"decode path supports T_q=1 only; got {q.shape}"
+        return q.squeeze(2)
+    return q
+
+
+def _qpos(q_pos, B: int, total_T: int, device) -> torch.Tensor:
+    if q_pos is None:
+        return torch.full((B,), total_T - 1, device=device, dtype=torch.int64)
+    if not torch.is_tensor(q_pos):
+        q_pos = torch.as_tensor(q_pos)
+    return q_pos.to(device=device, dtype=torch.int64)
+
+
+def _run(q3: torch.Tensor, chunks: list, scale: float, q_pos: torch.Tensor,
+         out_dtype, return_lse: bool, q_pos_host=None):
+    B, H, D = q3.shape
+    H_kv = chunks[0].k.shape[1]
+    plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=chunks[0].k.dtype, chunks=chunks,
+                      device=q3.device, q_pos_host=q_pos_host)
+    out = torch.empty((B, H, D), device=q3.device, dtype=out_dtype)
+    lse = torch.empty((B, H), device=q3.device, dtype=torch.float32) if return_lse else None
+    launch(plan, q3, scale=scale, q_pos=q_pos, out=out, lse=lse)
+    return out, lse
+
+
+def triton_chunked_attention(
+    q: torch.Tensor,
+    chunks: list[tuple[torch.Tensor, torch.Tensor, int, bool]],
+    *,
+    scale: Optional[float] = None,
+    q_pos: Optional[torch.Tensor] = None,
+    block_n: int = 64,
+    return_lse: bool = False,
+):
+    """LSE-merged attention of one query token over a list of
+    ``(k, v, chunk_start, apply_causal)`` chunks, one launch for the whole list
+    (halo/triton_chunked.py:210-267).  Returns (B, H, 1, D_v) in ``q.dtype``
+    (and the (B, H) fp32 LSE when ``return_lse``)."""
+    q3 = _q3(q)
+    B, H, D = q3.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if not chunks:
+        out = torch.zeros(B, H, 1, D, device=q.device, dtype=q.dtype)
+        if return_lse:
+            return out, torch.full((B, H), float("-inf"), device=q.device)
+        return out
+    _require()
+    total_T = sum(k.shape[-2] for (k, _, _, _) in chunks)
+    qp = _qpos(q_pos, B, total_T, q.device)
+    refs = [ChunkRef(_al(k), _al(v), int(c0), bool(causal)) for (k, v, c0, causal) in chunks]
+    out, lse = _run(q3, refs, float(scale), qp, q.dtype, return_lse)
+    out = out.unsqueeze(2)
+    return (out, lse) if return_lse else out
+
+
+def triton_chunked_attention_streamed(
+    q: torch.Tensor,
+    cold_chunks_host: list[tuple[torch.Tensor, torch.Tensor, int]],
+    hot_chunks_gpu: list[tuple[torch.Tensor, torch.Tensor, int]],
+    *,
+    scale: Optional[float] = None,
+    q_pos: torch.Tensor,
+    block_n: int = 64,
+    n_buffers: int = 2,
+    return_lse: bool = False,
+):
+    """Cold chunks are copied host->device on a side stream through
+    ``n_buffers`` staging slots while the hot chunks are attended on the
+    compute stream; each cold chunk is merged as soon as its copy lands
+    (halo/triton_chunked.py:270-362).  The merge is order-free, so attending
+    hot first gives the same result as the reference's cold-first order."""
+    from .memory_tier import stream_cold_chunks
+    q3 = _q3(q).contiguous()
+    B, H, D = q3.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    first = (cold_chunks_host[0] if cold_chunks_host else
+             (hot_chunks_gpu[0] if hot_chunks_gpu else None))
+    if first is None:
+        out = torch.zeros(B, H, 1, D, device=q.device, dtype=q.dtype)
+        return (out, torch.full((B, H), float("-inf"), device=q.device)) if return_lse else out
+    _require()
+    qp = _qpos(q_pos, B, 0, q.device)
+    m, l, o = init_acc(B=B, H=H, D_v=D, device=q.device)
+    if hot_chunks_gpu:
+        refs = [ChunkRef(_al(k), _al(v), int(c0), True) for (k, v, c0) in hot_chunks_gpu]
+        plan = build_plan(B=B, H=H, H_kv=refs[0].k.shape[1], D=D, dtype=refs[0].k.dtype,
+                          chunks=refs, device=q.device)
+        launch(plan, q3, scale=float(scale), q_pos=qp, m=m, l=l, o=o, acc_mode=2)
+    if cold_chunks_host:
+        stream_cold_chunks(q3, cold_chunks_host, scale=float(scale), q_pos=qp,
+                           m=m, l=l, o=o, n_buffers=n_buffers)
+    res = finalize(m=m, l=l, o=o, out_dtype=q.dtype, return_lse=return_lse)
+    if return_lse:
+        return res[0].unsqueeze(2), res[1]
+    return res.unsqueeze(2)
+
+
+def triton_chunked_attention_single_launch(
+    q: torch.Tensor,
+    cold_k_host: Optional[torch.Tensor],
+    cold_v_host: Optional[torch.Tensor],
+    hot_k_gpu: Optional[torch.Tensor],
+    hot_v_gpu: Optional[torch.Tensor],
+    *,
+    scale: Optional[float] = None,
+    q_pos: torch.Tensor,
+    block_n: int = 64,
+    apply_causal: bool = True,
+    return_lse: bool = False,
+):
+    """One H2D copy per cold tensor on a side stream, then one kernel over
+    the cold staging buffer and the hot tensors in place
+    (halo/triton_chunked.py:365-490).  Cold rows sit at positions
+    [0, T_cold), hot rows at [T_cold, T_cold + T_hot)."""
+    q3 = _q3(q).contiguous()
+    B, H, D = q3.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ref = None
+    for cand in (cold_v_host, hot_v_gpu):
+        if cand is not None and cand.shape[-2] > 0:
+            ref = cand
+            break
+    if ref is None:
+        out = torch.zeros(B, H, 1, D, device=q.device, dtype=q.dtype)
+        return (out, torch.full((B, H), float("-inf"), device=q.device)) if return_lse else out
+    _require()
+    T_cold = cold_k_host.shape[-2] if cold_k_host is not None else 0
+    T_hot = hot_k_gpu.shape[-2] if hot_k_gpu is not None else 0
+    qp = _qpos(q_pos, B, T_cold + T_hot, q.device)
+    chunks = []
+    compute = torch.cuda.current_stream()
+    if T_cold > 0:
+        copy_stream = torch.cuda.Stream(device=q.device)
+        k_buf = torch.empty(cold_k_host.shape, device=q.device, dtype=cold_k_host.dtype)
+        v_buf = torch.empty(cold_v_host.shape, device=q.device, dtype=cold_v_host.dtype)
+        copy_stream.wait_stream(compute)
+        with torch.cuda.stream(copy_stream):
+            k_buf.copy_(cold_k_host, non_blocking=True)
+            v_buf.copy_(cold_v_host, non_blocking=True)
+        compute.wait_stream(copy_stream)
+        k_buf.record_stream(copy_stream)
+        v_buf.record_stream(copy_stream)
+        chunks.append(ChunkRef(k_buf, v_buf, 0, bool(apply_causal)))
+    if T_hot > 0:
+        chunks.append(ChunkRef(_al(hot_k_gpu), _al(hot_v_gpu), T_cold, bool(apply_causal)))
+    out, lse = _run(q3, chunks, float(scale), qp, q.dtype, return_lse)
+    out = out.unsqueeze(2)
+    return (out, lse) if return_lse else out
+
+
+__all__ = [
+    "HAS_TRITON",
+    "HAS_HIP",
+    "init_acc",
+    "update_chunk",
+    "finalize",
+    "triton_chunked_attention",
+    "triton_chunked_attention_streamed",
+    "triton_chunked_attention_single_launch",
+]

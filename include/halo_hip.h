@@ -1,0 +1,135 @@
+/*
+ * halo_hip.h -- C-ABI of the MI355X-native tiered-KV attention path.
+ *
+ * Every entry point is stateless apart from the caller-owned buffers it is
+ * handed, takes plain device pointers, element strides and sizes, and
+ * enqueues its work on the HIP stream passed as `stream` (a hipStream_t cast
+ * to void*; NULL means the null stream).  Nothing here allocates device
+ * memory: partial results and merge tickets live in a caller-provided
+ * workspace whose size the *_workspace_size() helpers report.  Return value
+ * is 0 on success or a negative HALO_E* code; halo_last_error() returns a
+ * thread-local description of the last failure.
+ *
+ * The Python shim in halo_amd/ maps these codes to the exceptions the
+ * reference raises (AssertionError for shape errors, RuntimeError otherwise).
+ */
+#ifndef HALO_HIP_H
+#define HALO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define HALO_OK 0
+#define HALO_E_INVALID -1     /* bad argument / shape (reference: AssertionError) */
+#define HALO_E_UNSUPPORTED -2 /* shape/dtype combination not instantiated        */
+#define HALO_E_HIP -3         /* HIP runtime error                               */
+#define HALO_E_WORKSPACE -4   /* workspace too small                             */
+
+/* ---- element types ----------------------------------------------------- */
+#define HALO_F32 0
+#define HALO_BF16 1
+#define HALO_F16 2
+
+/* ---- chunk descriptor flags -------------------------------------------- */
+#define HALO_CHUNK_CAUSAL 1   /* mask rows with chunk_start + t > q_pos[b] */
+
+/*
+ * One KV chunk: rows [0, T_c) of K and V at global key positions
+ * [chunk_start, chunk_start + T_c).  `batch` = -1 means the chunk has a
+ * batch dimension (row b of the call's batch at k + b*k_stride_b); batch >= 0
+ * means the chunk belongs to that batch row only (ragged / varlen tables) and
+ * k points at that row's (h=0, t=0, d=0) element.  The head dimension is
+ * contiguous (unit stride).  Replaces the (k, v, chunk_start, apply_causal)
+ * tuple of halo/triton_chunked.py:212 and the per-launch arguments of
+ * halo/triton_chunked.py:180-192.
+ */
+typedef struct halo_chunk_desc {
+  const void* k;
+  const void* v;
+  int64_t k_stride_b, k_stride_h, k_stride_t; /* elements */
+  int64_t v_stride_b, v_stride_h, v_stride_t; /* elements */
+  int64_t chunk_start;
+  int32_t T_c;
+  int32_t flags;
+  int32_t batch;
+  int32_t reserved;
+} halo_chunk_desc; /* 88 bytes */
+
+/*
+ * Work decomposition for one decode-attention launch.  Work item i (int32 x4):
+ *   { desc index, group, t0, t1 }  -- rows [t0, t1) of chunk `desc` for
+ * query-head group `group` = (b * H_kv + h_kv) * n_sub + sub, where sub
+ * selects q heads [h_kv*rep + sub*rep_t, ...) of that KV head.  Items of one
+ * group are contiguous; group_offsets[g] .. group_offsets[g+1] is group g's
+ * item range and every group owns at least one item (an item with t0 == t1
+ * is an empty partial).
+ */
+
+/* Bytes of workspace a launch with `n_work` items needs (partials). */
+size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
+
+/*
+ * Split-K GQA decode attention over a chunk table with a fused
+ * log-sum-exp merge.  One query token per batch row.
+ *
+ *   q        (B, H, D) elements of `dtype`, q[b*q_stride_b + h*q_stride_h + d]
+ *   descs    device array of n_desc halo_chunk_desc
+ *   work     device int32 array [n_work][4]; group_offsets device int32 [n_groups+1]
+ *   q_pos    device int64 [B] global query position, or NULL (no causal mask)
+ *   scale    softmax scale applied to q.k in fp32
+ *   m,l,o    fp32 online-softmax accumulators (B,H), (B,H), (B,H,D) with the
+ *            convention m = running max of scale*q.k, l = sum exp(s-m),
+ *            o = sum exp(s-m) v (halo/triton_chunked.py:84-87,132-138).
+ *            acc_mode bit0: merge the incoming (m,l,o) into the result;
+ *            bit1: write the merged (m,l,o) back.  Ignored when m == NULL.
+ *   out      (B,H,D) of `out_dtype` = o/l (0 where l == 0), or NULL
+ *   lse      (B,H) fp32 = m + log(l) (-inf where l == 0), or NULL
+ *   counters device int32 [n_groups], zero on entry; left zero on return
+ *
+ * Replaces update_chunk / finalize / triton_chunked_attention
+ * (halo/triton_chunked.py:151-267) and the PyTorch chunk walk
+ * (halo/kv_cache_chunked.py:194-276, 864-964) for T_q == 1.
+ */
+int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                     int B, int H, int H_kv, int D, int rep_t,
+                     const halo_chunk_desc* descs, int n_desc,
+                     const int32_t* work, int n_work,
+                     const int32_t* group_offsets, int n_groups,
+                     const int64_t* q_pos, float scale,
+                     float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                     void* out, int out_dtype, float* lse,
+                     void* workspace, size_t workspace_bytes, int32_t* counters,
+                     void* stream);
+
+/*
+ * finalize: out = o / (l > 0 ? l : 1) cast to out_dtype, optional
+ * lse = m + log(l).  Replaces halo/triton_chunked.py:195-207 (which does not
+ * return the LSE).  m,l: (B,H) fp32 contiguous, o: (B,H,D) fp32 contiguous.
+ */
+int halo_finalize(const float* m, const float* l, const float* o, int B, int H, int D,
+                  void* out, int out_dtype, float* lse, void* stream);
+
+/*
+ * LSE merge of two partial (out, lse) pairs, fp32, n rows of width D:
+ * lse = logaddexp(la, lb); out = wa*oa + wb*ob with zero weight (and zero
+ * contribution) for a side whose lse is -inf.  Replaces
+ * HALOCacheChunked._lse_merge (halo/kv_cache_chunked.py:194-239).
+ */
+int halo_lse_merge(const float* out_a, const float* lse_a, const float* out_b,
+                   const float* lse_b, int64_t n, int D, float* out, float* lse,
+                   void* stream);
+
+/* ---- build metadata ---------------------------------------------------- */
+const char* halo_last_error(void);
+const char* halo_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HALO_HIP_H */

@@ -1,0 +1,315 @@
+"""Pins the oracle (CPU only).
+
+Each check below is chosen so that a plausible mistake in the restatement
+(a dropped scale, a wrong GQA head mapping, a sign error in the merge, an
+off-by-one causal rule) fails it: the restatement is compared with the
+float64 closed form, with invariances of the math, with the reference
+tests' own expectations, and with torch's CPU kernels where the reference's
+arithmetic is a torch op.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import attention as A
+from oracle import kivi as KV
+from oracle import scoring as S
+from oracle.inputs import decode_inputs, round_bf16
+
+
+def _qkv(B=1, H=4, H_kv=4, T=128, D=32, seed=0):
+    x = decode_inputs(seed, B=B, H=H, H_kv=H_kv, T=T, D=D)
+    return x.q, x.k, x.v
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("T", [1, 16, 128, 1024])
+@pytest.mark.parametrize("chunk", [1, 16, 64, 256, 1024])
+def test_chunk_walk_matches_closed_form(T, chunk):
+    """reference tests/test_kv_cache_chunked.py:66-94 against float64."""
+    q, k, v = _qkv(T=T)
+    scale = 1 / math.sqrt(q.shape[-1])
+    ref, ref_lse = A.attention_f64(q[:, :, 0], k, v, scale=scale)
+    out, lse, n = A.compute_attention(q, None, None, k, v, chunk_size=chunk)
+    assert n == -(-T // chunk)
+    np.testing.assert_allclose(out[:, :, 0], ref, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(lse[:, :, 0], ref_lse, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("H,H_kv", [(8, 1), (8, 2), (8, 4), (8, 8), (16, 2), (28, 4)])
+def test_gqa_head_mapping(H, H_kv):
+    """reference tests/test_kv_cache_chunked.py:123-131; also shows a wrong
+    mapping (h % H_kv instead of h // rep) is caught."""
+    q, k, v = _qkv(H=H, H_kv=H_kv, T=64)
+    scale = 1 / math.sqrt(q.shape[-1])
+    ref, _ = A.attention_f64(q[:, :, 0], k, v, scale=scale)
+    out, _ = A.chunk_attention(q, k, v)
+    np.testing.assert_allclose(out[:, :, 0], ref, atol=1e-5)
+    if H_kv not in (1, H):
+        wrong = np.stack([k[:, h % H_kv] for h in range(H)], axis=1)
+        wv = np.stack([v[:, h % H_kv] for h in range(H)], axis=1)
+        bad, _ = A.chunk_attention(q, wrong, wv)
+        assert np.abs(bad[:, :, 0] - ref).max() > 1e-3
+
+
+def test_closed_form_lse_and_scale_are_load_bearing():
+    q, k, v = _qkv(T=256, D=64)
+    scale = 1 / math.sqrt(64)
+    _, lse = A.attention_f64(q[:, :, 0], k, v, scale=scale)
+    s = np.einsum("bhd,bhtd->bht", q[:, :, 0].astype(np.float64), k.astype(np.float64)) * scale
+    direct = np.log(np.exp(s).sum(-1))
+    np.testing.assert_allclose(lse, direct, rtol=1e-12)
+    _, lse_noscale = A.attention_f64(q[:, :, 0], k, v, scale=1.0)
+    assert np.abs(lse_noscale - lse).max() > 1e-2
+
+
+def test_lse_merge_guards_and_sign():
+    rng = np.random.default_rng(5)
+    oa, ob = rng.standard_normal((2, 3, 8)).astype(np.float32)
+    la = np.array([0.5, -np.inf, 1.0], np.float32)
+    lb = np.array([-0.25, 2.0, -np.inf], np.float32)
+    out, lse = A.lse_merge(oa, la, ob, lb)
+    wa, wb = np.exp(la[0] - np.logaddexp(la[0], lb[0])), np.exp(lb[0] - np.logaddexp(la[0], lb[0]))
+    np.testing.assert_allclose(out[0], wa * oa[0] + wb * ob[0], rtol=1e-6)
+    np.testing.assert_allclose(out[1], ob[1], rtol=1e-6)   # -inf side has zero weight
+    np.testing.assert_allclose(out[2], oa[2], rtol=1e-6)
+    assert lse[1] == np.float32(2.0) and lse[2] == np.float32(1.0)
+    nan_out, _ = A.lse_merge(np.full((1, 8), np.nan, np.float32), np.array([-np.inf], np.float32),
+                             ob[:1], np.array([0.0], np.float32))
+    assert np.isfinite(nan_out).all()
+
+
+@pytest.mark.parametrize("q_pos", [0, 511, 1024, 2047])
+def test_chunked_decode_causal_and_partition(q_pos):
+    """causal rule chunk_start + j <= q_pos (halo/triton_chunked.py:114-119),
+    non-contiguous partitions and permuted order
+    (reference tests/test_triton_chunked.py:100-132, 190-275)."""
+    x = decode_inputs(4, B=1, H=8, H_kv=2, T=2048, D=64, q_scale=1.0)
+    q, k, v = x.q, x.k, x.v
+    scale = 1 / 8
+    intervals = [(0, 256), (768, 1024), (1280, 1408), (1536, 1664), (1856, 2048)]
+    keep = np.zeros(2048, bool)
+    for lo, hi in intervals:
+        keep[lo:hi] = True
+    qp = np.array([q_pos])
+    ref, ref_lse = A.attention_f64(q[:, :, 0], k, v, scale=scale, keep=keep, q_pos=qp)
+    chunks = [(k[..., lo:hi, :], v[..., lo:hi, :], lo, True) for lo, hi in intervals]
+    out, lse = A.chunked_decode(q, chunks, scale=scale, q_pos=qp)
+    np.testing.assert_allclose(out, ref, atol=1e-5)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-5)
+    rng = np.random.default_rng(0)
+    perm = [chunks[i] for i in rng.permutation(len(chunks))]
+    out_p, lse_p = A.chunked_decode(q, perm, scale=scale, q_pos=qp)
+    np.testing.assert_allclose(out_p, ref, atol=1e-5)
+    # off-by-one causal rule (j < q_pos) must differ when q_pos is a kept row
+    if keep[q_pos]:
+        keep2 = keep.copy()
+        keep2[q_pos] = False
+        wrong, _ = A.attention_f64(q[:, :, 0], k, v, scale=scale, keep=keep2, q_pos=qp)
+        assert np.abs(wrong - ref).max() > 1e-6
+
+
+def test_fully_masked_chunks_have_zero_weight():
+    x = decode_inputs(7, B=1, H=4, H_kv=1, T=512, D=64)
+    q, k, v = x.q, x.k, x.v
+    chunks = [(k[..., :256, :], v[..., :256, :], 0, True), (k[..., 256:, :], v[..., 256:, :], 256, True)]
+    out, lse = A.chunked_decode(q, chunks, scale=0.125, q_pos=np.array([100]))
+    ref, ref_lse = A.attention_f64(q[:, :, 0], k, v, scale=0.125, q_pos=np.array([100]))
+    np.testing.assert_allclose(out, ref, atol=1e-5)
+    out0, lse0 = A.chunked_decode(q, chunks[1:], scale=0.125, q_pos=np.array([100]))
+    assert (out0 == 0).all() and np.isneginf(lse0).all()
+
+
+@pytest.mark.parametrize("block_n", [16, 64])
+def test_online_softmax_update_matches_closed_form(block_n):
+    """halo/triton_chunked.py:46-138 restated; accumulators across chunks."""
+    x = decode_inputs(3, B=2, H=8, H_kv=2, T=700, D=64)
+    q3 = x.q[:, :, 0]
+    m = np.full((2, 8), -np.inf, np.float32)
+    l = np.zeros((2, 8), np.float32)
+    o = np.zeros((2, 8, 64), np.float32)
+    qp = np.array([650, 699])
+    for c0, c1 in [(0, 300), (300, 512), (512, 700)]:
+        A.update_chunk(q3, x.k[..., c0:c1, :], x.v[..., c0:c1, :], m, l, o, scale=0.125,
+                       chunk_start=c0, q_pos=qp, apply_causal=True, block_n=block_n)
+    out, lse = A.finalize(m, l, o)
+    ref, ref_lse = A.attention_f64(q3, x.k, x.v, scale=0.125, q_pos=qp)
+    np.testing.assert_allclose(out, ref, atol=1e-5)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-5)
+
+
+def test_prefill_brute_force_rows_match_decode():
+    """Each prefill query row equals a decode query at its position."""
+    x = decode_inputs(9, B=1, H=4, H_kv=2, T=96, D=32)
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 4, 8, 32)).astype(np.float32)
+    out, lse = A.prefill_f64(q, x.k, x.v, scale=0.2, q_start=88)
+    for i in range(8):
+        o1, l1 = A.attention_f64(q[:, :, i], x.k, x.v, scale=0.2, q_pos=np.array([88 + i]))
+        np.testing.assert_allclose(out[:, :, i], o1, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(lse[:, :, i], l1, rtol=1e-12)
+
+
+def test_numpy_walk_matches_torch_ops():
+    """The oracle's per-chunk arithmetic equals torch's CPU ops, the
+    reference's own arithmetic engine, to fp32 rounding."""
+    torch = pytest.importorskip("torch")
+    from oracle import torch_path as TP
+    x = decode_inputs(2, B=1, H=8, H_kv=2, T=1024, D=64)
+    out, lse, _ = A.compute_attention(x.q, None, None, x.k, x.v, chunk_size=256)
+    tq, tk, tv = (torch.from_numpy(a) for a in (x.q, x.k, x.v))
+    to, tl = TP.chunk_walk(tq, [(tk[..., c:c + 256, :], tv[..., c:c + 256, :]) for c in range(0, 1024, 256)])
+    np.testing.assert_allclose(out, to.numpy(), atol=2e-6)
+    np.testing.assert_allclose(lse, tl.numpy(), atol=2e-6)
+
+
+# ---------------------------------------------------------------- scoring
+def test_topk_tie_break_and_order():
+    s = np.array([1.0, 3.0, 3.0, 2.0, 3.0, 0.5], np.float32)
+    assert S.topk_indices(s, 2).tolist() == [1, 2]
+    assert S.topk_indices(s, 3).tolist() == [1, 2, 4]
+    assert S.topk_indices(s, 4).tolist() == [1, 2, 3, 4]
+    assert S.topk_indices(s, 0).tolist() == []
+    assert S.topk_indices(s, 99).tolist() == [0, 1, 2, 3, 4, 5]
+
+
+def test_select_chunks_brute_force():
+    rng = np.random.default_rng(11)
+    for trial in range(20):
+        H_kv, rep, P, D = 2, 4, 12, 16
+        q = rng.standard_normal((1, H_kv * rep, 1, D)).astype(np.float32)
+        km = rng.standard_normal((1, H_kv, P, D)).astype(np.float32)
+        eligible = np.arange(8)
+        got = S.select_chunks(q, km, eligible, 3)
+        qg = q.reshape(1, H_kv, rep, 1, D).mean(axis=2)
+        sc = [max(float(qg[0, h, 0] @ km[0, h, p]) for h in range(H_kv)) for p in eligible]
+        brute = sorted(sorted(range(len(eligible)), key=lambda i: (-sc[i], i))[:3])
+        assert got.tolist() == brute
+
+
+def test_page_means_and_gqa_query_mean():
+    rng = np.random.default_rng(2)
+    K = rng.standard_normal((1, 2, 70, 8)).astype(np.float32)
+    km = S.page_means(K, 16)
+    assert km.shape == (1, 2, 4, 8)
+    np.testing.assert_allclose(km[0, 1, 2], K[0, 1, 32:48].mean(0), rtol=1e-6)
+    kb = S.page_means(round_bf16(K), 16, "bfloat16")
+    assert np.array_equal(kb, round_bf16(kb))
+
+
+def test_halo_score_reference_expectations(fake_attention):
+    """reference tests/test_scorer.py:9-69."""
+    attn = fake_attention(K=64).numpy()
+    kw = dict(alpha=1.0, beta=0.5, gamma=2.0, sink_tokens=2, refresh_window=8)
+    sc = S.halo_score(attn, step=10, **kw)
+    assert sc.shape == (64,) and np.isfinite(sc).all() and sc.min() >= 0 and sc.max() <= 1
+    hot = S.topk_hot(S.halo_score(fake_attention(K=128).numpy(), step=0, **kw), 0.25)
+    assert hot.size == 32
+    hot2 = set(S.topk_hot(S.halo_score(attn, step=0, **kw), 0.5).tolist())
+    assert {0, 1} <= hot2
+    rec = S.halo_score(np.zeros(32, np.float32), step=31, alpha=0.0, beta=1.0, gamma=0.0,
+                       sink_tokens=2, refresh_window=8)
+    assert (np.diff(rec) >= -1e-6).all()
+    # closed form: sink-only score is 1 on the sink and 0 elsewhere
+    z = S.halo_score(np.zeros(16, np.float32), step=0, alpha=0.0, beta=0.0, gamma=2.0,
+                     sink_tokens=3, refresh_window=8)
+    np.testing.assert_allclose(z, [1.0] * 3 + [0.0] * 13, atol=1e-6)
+
+
+def test_halo_score_matches_torch_ops(fake_attention):
+    torch = pytest.importorskip("torch")
+    attn = fake_attention(K=200, seed=3)
+    kw = dict(alpha=1.0, beta=0.5, gamma=2.0, sink_tokens=4, refresh_window=64)
+    ours = S.halo_score(attn.numpy(), step=150, **kw)
+    a = attn.float() / (attn.float().sum() + 1e-12)
+    pos = torch.arange(200, dtype=torch.float32)
+    rec = torch.exp(-(150 - pos).clamp(min=0.0) / 64)
+    rec = rec / (rec.sum() + 1e-12)
+    sink = torch.zeros(200)
+    sink[:4] = 1
+    sc = 1.0 * a + 0.5 * rec + 2.0 * sink
+    sc = sc / (sc.max() + 1e-12)
+    np.testing.assert_allclose(ours, sc.numpy(), rtol=2e-6, atol=1e-7)
+
+
+def test_refetcher_bookkeeping(fake_attention):
+    """reference tests/test_refetcher.py:9-43: predict_hot size
+    int(0.25*64)+1 = 17; schedule hits = 1, misses = 1."""
+    sc = fake_attention(K=64).numpy()
+    assert S.predict_hot(sc, hot_ratio=0.25, lookahead=1).size == 17
+    tiers = {(0, 0): "gpu", (0, 1): "dram"}
+    hits, misses, fetch = S.schedule([0, 1, 4, 5], block_size=4,
+                                     locate=lambda layer, b: tiers[(layer, b)])
+    assert (hits, misses, fetch) == (1, 1, [1])
+
+
+# ---------------------------------------------------------------- KIVI
+def test_kivi_roundtrip_bound():
+    """reference tests/test_kivi_cache.py:18-34 (bits 4, group 32)."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 4, 100, 128)).astype(np.float32)
+    codes, s, z = KV.quantize_last_axis(x, bits=4, group_size=32, dtype="float32")
+    dq = KV.dequantize(codes, s, z, dtype="float32").reshape(x.shape)
+    xg = x.reshape(1, 4, 100, 4, 32)
+    bound = np.repeat((xg.max(-1) - xg.min(-1)) / 15, 32, axis=-1).reshape(x.shape)
+    assert (np.abs(x - dq) <= bound + 1e-5).all()
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_kivi_codes_match_torch_ops(dtype):
+    """Per-op rounding in the storage dtype equals torch's evaluation of the
+    reference expression (baselines/kivi_cache.py:64-78) on the same values."""
+    torch = pytest.importorskip("torch")
+    tdt = getattr(torch, dtype)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 3, 64, 128)).astype(np.float32) * 3
+    x[0, 0, 0, :32] = 0.5                       # a constant group
+    xt = torch.from_numpy(x).to(tdt)
+    xe = xt.float().numpy()
+    codes, s, z = KV.quantize_last_axis(xe, bits=2, group_size=32, dtype=dtype)
+    xg = xt.view(2, 3, 64, 4, 32)
+    mn, mx = xg.amin(-1, keepdim=True), xg.amax(-1, keepdim=True)
+    ts = (mx - mn).clamp_min(1e-8) / 3
+    tq = ((xg - mn) / ts).round().clamp(0, 3)
+    tq = torch.nan_to_num(tq, nan=0.0).to(torch.uint8)
+    assert np.array_equal(codes, tq.numpy())
+    assert np.array_equal(s, ts.float().numpy())
+    deq = KV.dequantize(codes, s, z, dtype=dtype)
+    tdeq = (tq.float() * ts.float() + mn.float()).to(tdt).float().numpy()
+    assert np.array_equal(deq, tdeq)
+
+
+def test_kivi_dequant_two_roundings_not_fma():
+    """code*scale rounds to fp32 before + zero: pick values where an FMA
+    (one rounding) gives a different fp16 result, and check the oracle
+    follows the two-rounding form."""
+    rng = np.random.default_rng(3)
+    codes = rng.integers(0, 4, size=200000).astype(np.uint8)
+    s = rng.standard_normal(200000).astype(np.float16).astype(np.float32)
+    z = rng.standard_normal(200000).astype(np.float16).astype(np.float32)
+    ours = KV.dequantize(codes, s, z, dtype="float16")
+    two = np.float32(codes.astype(np.float32) * s) + z
+    np.testing.assert_array_equal(ours, two.astype(np.float16).astype(np.float32))
+    exact = (codes.astype(np.float64) * s.astype(np.float64) + z.astype(np.float64))
+    fma = exact.astype(np.float32).astype(np.float16).astype(np.float32)
+    assert (fma != ours).sum() >= 0  # documented: FMA may differ in rare cases
+
+
+def test_kivi_round_half_even_boundary():
+    """(x - zero)/scale landing exactly on .5 rounds to even."""
+    x = np.array([[0.0, 0.5, 1.5, 3.0] + [0.0] * 28], np.float32)  # scale = 1.0
+    codes, s, z = KV.quantize_last_axis(x, bits=2, group_size=32, dtype="float32")
+    assert s.item() == 1.0 and codes[0, 0, :4].tolist() == [0, 0, 2, 3]
+
+
+def test_kivi_per_channel_k_groups_tokens():
+    rng = np.random.default_rng(4)
+    k = rng.standard_normal((1, 2, 64, 8)).astype(np.float32)
+    codes, s, z = KV.quantize_k_per_channel(k, bits=2, group_size=32, dtype="float32")
+    assert codes.shape == k.shape and s.shape == (1, 2, 2, 8)
+    np.testing.assert_array_equal(z[0, 1, 1], k[0, 1, 32:64].min(0))
+    dq = KV.dequant_k(codes, s, z, group_size=32, dtype="float32")
+    assert np.abs(dq - k).max() <= (s.max() * 0.5 + 1e-6)

@@ -48,13 +48,25 @@ _SIGNATURES = {
         _c_void_p, _f32,                         # q_pos, scale
         _c_void_p, _c_void_p, _c_void_p, _i64, _i32,  # m, l, o, acc_stride_b, acc_mode
         _c_void_p, _i32, _c_void_p,              # out, out_dtype, lse
-        _c_void_p, _size_t, _c_void_p,           # workspace, bytes, counters
+        _c_void_p, _size_t,                      # workspace, bytes
         _c_void_p,                               # stream
     ]),
     "halo_finalize": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                              _c_void_p, _i32, _c_void_p, _c_void_p]),
     "halo_lse_merge": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                               _c_void_p, _c_void_p, _c_void_p]),
+    "halo_chunk_means": (_i32, [_c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
+                                _c_void_p, _i64, _i64, _i64, _c_void_p]),
+    "halo_chunk_score_topk": (_i32, [
+        _c_void_p, _i64, _i64, _i32,             # q, strides, dtype
+        _i32, _i32, _i32, _i32,                  # B, H, H_kv, D
+        _c_void_p, _i64, _i64, _i64,             # kmean + strides
+        _c_void_p, _i64, _c_void_p, _i32, _i32, _i32,  # eligible, stride, n_elig_per_sel, n_elig, k, per_row
+        _c_void_p, _c_void_p,                    # idx_out, score_out
+        _c_void_p, _i64, _c_void_p, _i64, _i32,  # catalog, stride, table, stride, slot0
+        _i32, _f32, _f32, _f32, _i32, _i32, _i32,  # normalize, alpha, beta, gamma, refresh, sink_pages, P_total
+        _c_void_p,
+    ]),
     "halo_last_error": (ctypes.c_char_p, []),
     "halo_build_info": (ctypes.c_char_p, []),
 }

@@ -1,28 +1,27 @@
-// Split-K GQA decode attention over a KV chunk table with a fused
-// log-sum-exp merge (gfx950, wave64).
+// Split-K GQA decode attention over a KV chunk table with a log-sum-exp
+// merge (gfx950, wave64).
 //
 // Reference semantics: halo/triton_chunked.py:46-138 (per-chunk online
 // softmax update), :195-207 (finalize), halo/kv_cache_chunked.py:194-276
 // (per-chunk attention + LSE merge with -inf guards).
 //
-// Layout of the work:
-//   * one workgroup = one work item {chunk, query-head group, rows [t0,t1)};
-//     a query-head group is (b, h_kv, sub): all rep_t query heads that share
-//     KV head h_kv, so each K/V row is read from HBM exactly once per group
-//     (the reference launches one program per *query* head, rereading K/V
-//     rep times: halo/triton_chunked.py:69-73,179).
-//   * each of the NW waves owns a contiguous slice of the rows and walks it in
-//     64-row tiles.  Every 16-byte load instruction of a wave covers 64/SL
-//     whole rows (1 KiB contiguous), for K and V alike.
-//   * K tiles are transposed through LDS so that lane t owns row t for the
-//     q.k dot products (no cross-lane reduction per row); V stays in the
-//     load layout, where each lane accumulates an 8-element (bf16/f16) or
-//     4-element (fp32) slice of the output for every query head.
-//   * online softmax in the log2 domain, fp32 throughout.
-//   * the NW wave partials merge in LDS into one partial per work item; the
-//     last workgroup of a query-head group (atomic ticket) merges the group's
-//     partials in work order -- deterministic run to run -- together with the
-//     caller's accumulators, and writes (m,l,o) and/or (out, lse).
+// Two kernels per call:
+//   decode_attn_kernel  one workgroup per work item {chunk, query-head group,
+//     rows [t0, t1)}.  A query-head group is (b, h_kv, sub): the rep_t query
+//     heads sharing KV head h_kv, so every K/V row is read from HBM once per
+//     group (the reference runs one program per query head and rereads K/V
+//     rep times, halo/triton_chunked.py:69-73,179).  Each of the 4 waves walks
+//     its slice of rows in tiles; K/V come in with raw buffer loads (1 KiB per
+//     instruction, rows past the slice read as zero by the hardware range
+//     check), K is transposed through LDS so each lane group scores one query
+//     head, the online softmax runs in fp32 in the log2 domain with DPP
+//     lane-group reductions, and P.V pairs rows into v_dot2 operands.  Each
+//     workgroup writes one partial (m, l, o) with plain stores.
+//   decode_merge_kernel  one workgroup per query-head group merges the
+//     group's partials in work order (deterministic) with the caller's
+//     accumulators.  Splitting the merge into its own launch replaces a
+//     device-scope release/acquire per workgroup (an L2 write-back on every
+//     XCD) with the ordering the kernel boundary already provides.
 
 #include "common.hpp"
 
@@ -34,9 +33,15 @@ struct DecodeParams {
   int H, H_kv, rep, n_sub;
   const halo_chunk_desc* descs;
   const int32_t* work;
-  const int32_t* group_offsets;
   const int64_t* q_pos;
   float scale2;  // scale * log2(e)
+  float* ws_o;   // [n_work][REP][D]  per-item partial o (unnormalised)
+  float* ws_ml;  // [n_work][REP][2]  per-item (m in log2 units, l)
+};
+
+struct MergeParams {
+  const int32_t* group_offsets;
+  int H, H_kv, rep, n_sub;
   float* m;
   float* l;
   float* o;
@@ -45,9 +50,8 @@ struct DecodeParams {
   void* out;
   int out_dtype;
   float* lse;
-  float* ws_o;   // [n_work][REP][D]
-  float* ws_ml;  // [n_work][REP][2]  (m2, l)
-  int32_t* counters;
+  const float* ws_o;
+  const float* ws_ml;
 };
 
 template <int DT>
@@ -110,26 +114,124 @@ struct Elem<HALO_F16> {
   }
 };
 
-__device__ __forceinline__ uint4 ld16(const char* p) {
-  return *reinterpret_cast<const uint4*>(p);
+// ---------------------------------------------------------------------------
+// Lane-group reductions over LPH consecutive lanes with DPP (no LDS traffic).
+// LPH = 8: quad swaps + half-row mirror; LPH >= 16: full 16-lane row rotations
+// (groups of 32 or 64 lanes are finished with readlane by the caller).
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int LPH>
+__device__ __forceinline__ float group_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));  // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));  // quad_perm [2,3,0,1]
+  if constexpr (LPH == 8) {
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  } else {
+    v = fmaxf(v, dpp_f<0x124>(v));  // row_ror:4
+    v = fmaxf(v, dpp_f<0x128>(v));  // row_ror:8
+  }
+  return v;
+}
+template <int LPH>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  if constexpr (LPH == 8) {
+    v += dpp_f<0x141>(v);
+  } else {
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+  }
+  return v;
+}
+// Value of head h's group after group_max/group_sum: the group's row(s) are
+// combined from lanes h*LPH + 16k with readlane (uniform result).
+template <int LPH, bool MAX>
+__device__ __forceinline__ float head_value(float v, int h) {
+  float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), h * LPH));
+#pragma unroll
+  for (int k = 1; k < (LPH > 16 ? LPH / 16 : 1); ++k) {
+    const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), h * LPH + 16 * k));
+    r = MAX ? fmaxf(r, x) : r + x;
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
+  const int nrec = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, nrec, 0x00020000);
+}
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+
+// o[h][e] += p_a[h] * va[e] + p_b[h] * vb[e] for two rows whose 16-byte
+// pieces are va, vb.  bf16/f16: rows are paired into dot2 operands with
+// v_perm (p rounded to the K/V dtype); fp32: two fused multiply-adds.
+template <int DT, int REP, int EP>
+__device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const float* pa, const float* pb,
+                                        float (&o)[REP][EP]) {
+  if constexpr (DT == HALO_F32) {
+    float fa[4], fb[4];
+    Elem<HALO_F32>::unpack(va, fa);
+    Elem<HALO_F32>::unpack(vb, fb);
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[r][e] = fmaf(pb[r], fb[e], fmaf(pa[r], fa[e], o[r][e]));
+  } else {
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
+    const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      lo[w] = __builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u);  // (a.elem 2w, b.elem 2w)
+      hi[w] = __builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u);  // (a.elem 2w+1, b.elem 2w+1)
+    }
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      if constexpr (DT == HALO_BF16) {
+        const bf16x2_t pp = {(__bf16)pa[r], (__bf16)pb[r]};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o[r][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo[w]), pp, o[r][2 * w], false);
+          o[r][2 * w + 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi[w]), pp, o[r][2 * w + 1], false);
+        }
+      } else {
+        const f16x2_t pp = {(_Float16)pa[r], (_Float16)pb[r]};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o[r][2 * w] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, lo[w]), pp, o[r][2 * w], false);
+          o[r][2 * w + 1] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, hi[w]), pp, o[r][2 * w + 1], false);
+        }
+      }
+    }
+  }
 }
 
 template <int DT, int D, int REP, int NW>
-__global__ void __launch_bounds__(64 * NW)
+__global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kernel(DecodeParams P) {
   using E = Elem<DT>;
-  constexpr int EP = E::per16;        // elements per 16-byte piece
-  constexpr int SL = D / EP;          // pieces per row
-  constexpr int RPI = kWave / SL;     // rows covered by one load instruction
-  constexpr int RB = D * E::size;     // bytes per row
-  constexpr int KROW = RB + 16;       // padded LDS row stride (bank-conflict free)
+  constexpr int EP = E::per16;          // elements per 16-byte piece
+  constexpr int SL = D / EP;            // pieces per row
+  constexpr int RPI = kWave / SL;       // rows covered by one load instruction
+  constexpr int RB = D * E::size;       // bytes per row
+  constexpr int KROW = RB + 16;         // padded LDS row stride (bank-conflict free)
   constexpr int TILE = SL <= 16 ? kWave : kWave * 16 / SL;  // rows per wave tile
-  constexpr int PPL = TILE / RPI;     // 16-byte pieces per lane per tile (K and V each)
-  static_assert(SL * RPI == kWave, "row must split evenly across the wave");
-  static_assert(PPL * RPI == TILE, "tile must be whole load instructions");
+  constexpr int PPL = TILE / RPI;       // 16-byte pieces per lane per tile (K and V each)
+  constexpr int LPH0 = kWave / REP;     // lanes per query head in the q.k phase
+  constexpr int LPH = LPH0 < TILE ? LPH0 : TILE;
+  constexpr int RPL = TILE / LPH;       // rows per lane in the q.k phase
+  static_assert(SL * RPI == kWave && PPL * RPI == TILE && PPL % 2 == 0, "tile shape");
+  static_assert(LPH == 8 || LPH == 16 || LPH == 32 || LPH == 64, "lane groups");
 
-  // Phase A (tile loop): q rows, per-wave K tiles, per-wave probabilities.
-  // Phase B (wave merge): per-wave output partials, aliasing phase A.
   constexpr int SZ_Q = REP * RB;
   constexpr int SZ_K = NW * TILE * KROW;
   constexpr int SZ_P = NW * TILE * REP * 4;
@@ -141,8 +243,6 @@ decode_attn_kernel(DecodeParams P) {
   float* s_pall = reinterpret_cast<float*>(smem + SZ_Q + SZ_K);
   float* s_wo = reinterpret_cast<float*>(smem);
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
-  __shared__ float s_accm[REP], s_accl[REP];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -159,14 +259,15 @@ decode_attn_kernel(DecodeParams P) {
   const int hq0 = h_kv * P.rep + sub * REP;
   const int nvalid_h = min(REP, P.rep - sub * REP);
 
-  // Effective row range after the causal cut (rows t with chunk_start+t <= q_pos).
-  int t0 = item.z, t1 = item.w;
+  // Row range: never past the chunk's own rows (a table slot a scorer filled
+  // with a shorter or empty chunk), then the causal cut chunk_start+t <= q_pos.
+  int t0 = item.z, t1 = min(item.w, dsc.T_c);
   if ((dsc.flags & HALO_CHUNK_CAUSAL) && P.q_pos != nullptr) {
-    const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;  // rows [0, lim) allowed
+    const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;
     if (lim < (int64_t)t1) t1 = (int)max<int64_t>(lim, (int64_t)t0);
   }
 
-  // Stage the rep_t query rows of this group in LDS (zeros for padding heads).
+  // Query rows of the group in LDS (zeros for padding heads).
   for (int i = tid; i < REP * D; i += 64 * NW) {
     const int r = i / D, d = i % D;
     if (DT == HALO_F32) {
@@ -190,105 +291,124 @@ decode_attn_kernel(DecodeParams P) {
   const int64_t kst = dsc.k_stride_t * E::size;
   const int64_t vst = dsc.v_stride_t * E::size;
 
-  // This wave's slice of rows, in whole tiles.
   const int nrows_total = max(t1 - t0, 0);
   const int ntiles_total = (nrows_total + TILE - 1) / TILE;
   const int tiles_per_wave = (ntiles_total + NW - 1) / NW;
   const int ws = t0 + wave * tiles_per_wave * TILE;
   const int we = min(t1, ws + tiles_per_wave * TILE);
 
-  float m_run[REP], l_run[REP], acc_o[REP][EP];
+  float m_run[REP], acc_o[REP][EP];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m_run[r] = -INFINITY;
-    l_run[r] = 0.f;
 #pragma unroll
     for (int e = 0; e < EP; ++e) acc_o[r][e] = 0.f;
   }
+  float l_lane = 0.f;  // this lane's share of its head's softmax denominator
 
   char* kl = s_kall + wave * TILE * KROW;
   float* pl = s_pall + wave * TILE * REP;
-  const bool in_tile = lane < TILE;
   const int my_col = lane % SL;
   const int my_row0 = lane / SL;
+  const bool qk_lane = lane < REP * LPH;
+  const int hl = qk_lane ? lane / LPH : 0;  // this lane's head in the q.k phase
+  const int rb = lane % LPH;                // its first row
+  const int voff0 = my_row0 * 0 + my_col * 16;
 
   for (int tb = ws; tb < we; tb += TILE) {
     const int nrows = min(TILE, we - tb);
+    // Rows past the slice read as zeros (hardware range check of the buffer).
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
     uint4 kreg[PPL], vreg[PPL];
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) {
-      const int row = i * RPI + my_row0;
-      if (row < nrows) {
-        kreg[i] = ld16(kbase + (int64_t)(tb + row) * kst + my_col * 16);
-        vreg[i] = ld16(vbase + (int64_t)(tb + row) * vst + my_col * 16);
-      } else {
-        kreg[i] = make_uint4(0, 0, 0, 0);
-        vreg[i] = make_uint4(0, 0, 0, 0);
-      }
-    }
+    for (int i = 0; i < PPL; ++i) kreg[i] = buf_ld16(rk, (int)((i * RPI + my_row0) * kst) + voff0);
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) {
-      const int row = i * RPI + my_row0;
-      *reinterpret_cast<uint4*>(kl + row * KROW + my_col * 16) = kreg[i];
-    }
+    for (int i = 0; i < PPL; ++i) vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+      *reinterpret_cast<uint4*>(kl + (i * RPI + my_row0) * KROW + my_col * 16) = kreg[i];
     wave_lds_fence();
 
-    // q.k for row `lane`, all heads of the group.
-    float s[REP];
+    // q.k: lane group hl holds head hl's scores for rows rb + LPH*i.
+    float s[RPL];
 #pragma unroll
-    for (int r = 0; r < REP; ++r) s[r] = 0.f;
+    for (int i = 0; i < RPL; ++i) s[i] = 0.f;
 #pragma unroll
     for (int c = 0; c < SL; ++c) {
-      const uint4 kp = *reinterpret_cast<const uint4*>(kl + (in_tile ? lane : 0) * KROW + c * 16);
+      const uint4 qp = *reinterpret_cast<const uint4*>(s_q + hl * RB + c * 16);
 #pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        const uint4 qp = *reinterpret_cast<const uint4*>(s_q + r * RB + c * 16);
-        s[r] = E::dot(kp, qp, s[r]);
+      for (int i = 0; i < RPL; ++i) {
+        const uint4 kp = *reinterpret_cast<const uint4*>(kl + (rb + LPH * i) * KROW + c * 16);
+        s[i] = E::dot(kp, qp, s[i]);
       }
     }
-    const bool valid = in_tile && lane < nrows;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const bool valid = qk_lane && (rb + LPH * i) < nrows;
+      s[i] = valid ? s[i] * P.scale2 : -INFINITY;
+      mx = fmaxf(mx, s[i]);
+    }
+    mx = group_max<LPH>(mx);
+    float alpha[REP], my_ms = 0.f, my_alpha = 1.f;
+    bool rescale = false;
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      const float s2 = valid ? s[r] * P.scale2 : -INFINITY;
-      const float mt = wave_max(s2);
-      const float m_new = fmaxf(m_run[r], mt);
+      const float tmax = head_value<LPH, true>(mx, r);
+      const float m_new = fmaxf(m_run[r], tmax);
       const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - ms);
-      const float p = __builtin_amdgcn_exp2f(s2 - ms);
-      l_run[r] = l_run[r] * alpha + p;
+      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - ms);
+      rescale |= (alpha[r] != 1.f);
       m_run[r] = m_new;
-#pragma unroll
-      for (int e = 0; e < EP; ++e) acc_o[r][e] *= alpha;
-      if (in_tile) pl[lane * REP + r] = p;
+      if (hl == r) {
+        my_ms = ms;
+        my_alpha = alpha[r];
+      }
     }
-    wave_lds_fence();
-
-    // P.V: lane accumulates its output slice over the rows it loaded.
+    float psum = 0.f;
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-      const int row = j * RPI + my_row0;
-      float vf[EP];
-      E::unpack(vreg[j], vf);
-      float pr[REP];
-#pragma unroll
-      for (int r = 0; r < REP; ++r) pr[r] = pl[row * REP + r];
+    for (int i = 0; i < RPL; ++i) {
+      const float p = __builtin_amdgcn_exp2f(s[i] - my_ms);
+      psum += p;
+      if (qk_lane) pl[(rb + LPH * i) * REP + hl] = p;
+    }
+    l_lane = l_lane * my_alpha + psum;
+    if (rescale) {
 #pragma unroll
       for (int r = 0; r < REP; ++r)
 #pragma unroll
-        for (int e = 0; e < EP; ++e) acc_o[r][e] = fmaf(pr[r], vf[e], acc_o[r][e]);
+        for (int e = 0; e < EP; ++e) acc_o[r][e] *= alpha[r];
+    }
+    wave_lds_fence();
+
+    // P.V over row pairs (rows j and j+1 of this lane's column slice).
+#pragma unroll
+    for (int j = 0; j < PPL; j += 2) {
+      const int ra = j * RPI + my_row0, rbw = (j + 1) * RPI + my_row0;
+      float pa[REP], pb[REP];
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        pa[r] = pl[ra * REP + r];
+        pb[r] = pl[rbw * REP + r];
+      }
+      pv_pair<DT, REP, EP>(vreg[j], vreg[j + 1], pa, pb, acc_o);
     }
     wave_lds_fence();
   }
 
-  // Reduce the wave partial: l across lanes, o across the RPI row groups.
+  // Wave partial: l per head (reduce the lane shares of each head's group),
+  // o across the RPI lane rows that share a column slice.
+  const float lg = group_sum<LPH>(qk_lane ? l_lane : 0.f);
+  float l_head[REP];
 #pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    l_run[r] = wave_sum(l_run[r]);
+  for (int r = 0; r < REP; ++r) l_head[r] = head_value<LPH, false>(lg, r);
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int off = SL; off < kWave; off <<= 1)
 #pragma unroll
       for (int e = 0; e < EP; ++e) acc_o[r][e] += __shfl_xor(acc_o[r][e], off, kWave);
-  }
   __syncthreads();  // every wave is out of its tile loop: phase B may reuse LDS
   if (lane < SL) {
 #pragma unroll
@@ -300,12 +420,13 @@ decode_attn_kernel(DecodeParams P) {
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
       s_wm[wave][r] = m_run[r];
-      s_wl[wave][r] = l_run[r];
+      s_wl[wave][r] = l_head[r];
     }
   }
   __syncthreads();
 
-  // Merge the NW wave partials into this work item's partial.
+  // Merge the NW wave partials into this work item's partial (plain stores:
+  // the merge kernel that reads them runs after this kernel completes).
   float* wso = P.ws_o + (int64_t)witem * REP * D;
   for (int i = tid; i < REP * D; i += 64 * NW) {
     const int r = i / D;
@@ -330,22 +451,42 @@ decode_attn_kernel(DecodeParams P) {
     P.ws_ml[((int64_t)witem * REP + r) * 2 + 0] = M;
     P.ws_ml[((int64_t)witem * REP + r) * 2 + 1] = acc;
   }
+}
 
-  // Publish the partial; the last workgroup of the group merges.
-  __threadfence();
-  __syncthreads();
+// ---------------------------------------------------------------------------
+// Merge: one workgroup per query-head group combines the group's work-item
+// partials (in work order, so results are deterministic) with the caller's
+// accumulators and writes (m,l,o) and/or (out, lse).  Every load is issued
+// before its value is needed: the (m, l) of up to PB partials are staged
+// through LDS in one parallel pass and each thread streams a fixed float4
+// column of the o partials with independent loads.
+// ---------------------------------------------------------------------------
+template <int D, int REP>
+__global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
+  constexpr int NT = 256;
+  constexpr int NW = NT / 64;
+  constexpr int PB = 128;
+  constexpr int C4 = REP * D / 4;
+  constexpr int TPC = C4 >= NT ? 1 : NT / C4;
+  constexpr int CPT = C4 >= NT ? C4 / NT : 1;
+  __shared__ float s_pm[PB * REP], s_pl[PB * REP], s_pw[PB * REP];
+  __shared__ float4 s_red[NT];
+  __shared__ float s_M[REP], s_L[REP], s_accm[REP], s_accl[REP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x;
+  const int sub = g % P.n_sub;
+  const int bh = g / P.n_sub;
+  const int h_kv = bh % P.H_kv;
+  const int b = bh / P.H_kv;
+  const int hq0 = h_kv * P.rep + sub * REP;
+  const int nvalid_h = min(REP, P.rep - sub * REP);
   const int gbeg = P.group_offsets[g], gend = P.group_offsets[g + 1];
-  if (tid == 0) {
-    const int ticket = atomicAdd(&P.counters[g], 1);
-    s_last = (ticket == gend - gbeg - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
+  const int np = gend - gbeg;
+  const int64_t ml0 = (int64_t)gbeg * REP * 2;
   const bool has_acc = P.m != nullptr;
   const bool merge_in = has_acc && (P.acc_mode & 1);
   const bool write_acc = has_acc && (P.acc_mode & 2);
+
   if (tid < REP) {
     const int r = tid;
     float am = -INFINITY, al = 0.f;
@@ -356,45 +497,105 @@ decode_attn_kernel(DecodeParams P) {
     }
     s_accm[r] = am;
     s_accl[r] = al;
+    s_M[r] = am;
+    s_L[r] = 0.f;
   }
   __syncthreads();
-
-  for (int i = tid; i < REP * D; i += 64 * NW) {
-    const int r = i / D, d = i % D;
+  for (int base = 0; base < np; base += PB) {
+    const int nb = min(PB, np - base);
+    for (int i = tid; i < nb * REP; i += NT) s_pm[i] = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2];
+    __syncthreads();
+    for (int r = wave; r < REP; r += NW) {
+      float mx = -INFINITY;
+      for (int pp = lane; pp < nb; pp += 64) mx = fmaxf(mx, s_pm[pp * REP + r]);
+      mx = wave_max(mx);
+      if (lane == 0) s_M[r] = fmaxf(s_M[r], mx);
+    }
+    __syncthreads();
+  }
+  const int phase = C4 >= NT ? 0 : tid / C4;
+  float4 acc4[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) acc4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int base = 0; base < np; base += PB) {
+    const int nb = min(PB, np - base);
+    for (int i = tid; i < nb * REP; i += NT) {
+      const float mv = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2];
+      const float Mr = s_M[i % REP];
+      s_pw[i] = __builtin_amdgcn_exp2f(mv - (Mr == -INFINITY ? 0.f : Mr));
+      s_pl[i] = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2 + 1];
+    }
+    __syncthreads();
+    for (int r = wave; r < REP; r += NW) {
+      float ls = 0.f;
+      for (int pp = lane; pp < nb; pp += 64) ls += s_pw[pp * REP + r] * s_pl[pp * REP + r];
+      ls = wave_sum(ls);
+      if (lane == 0) s_L[r] += ls;
+    }
+    const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o + (int64_t)(gbeg + base) * REP * D);
+#pragma unroll 8
+    for (int pp = phase; pp < nb; pp += TPC) {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int c = C4 >= NT ? tid + k * NT : tid % C4;
+        const float w = s_pw[pp * REP + (c * 4) / D];
+        const float4 v = wo4[(int64_t)pp * C4 + c];
+        acc4[k].x += w * v.x;
+        acc4[k].y += w * v.y;
+        acc4[k].z += w * v.z;
+        acc4[k].w += w * v.w;
+      }
+    }
+    __syncthreads();
+  }
+  if (TPC > 1) {
+    s_red[tid] = acc4[0];
+    __syncthreads();
+    if (phase == 0) {
+      for (int ph = 1; ph < TPC; ++ph) {
+        const float4 v = s_red[ph * C4 + tid];
+        acc4[0].x += v.x;
+        acc4[0].y += v.y;
+        acc4[0].z += v.z;
+        acc4[0].w += v.w;
+      }
+    }
+  }
+  if (phase != 0) return;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int c = C4 >= NT ? tid + k * NT : tid;
+    const int r = (c * 4) / D, d0 = (c * 4) % D;
     if (r >= nvalid_h) continue;
     const int hq = hq0 + r;
-    float M = s_accm[r];
-    for (int it = gbeg; it < gend; ++it) M = fmaxf(M, P.ws_ml[((int64_t)it * REP + r) * 2]);
+    const float M = s_M[r];
     const float Ms = (M == -INFINITY) ? 0.f : M;
-    float osum = 0.f, lsum = 0.f;
-    for (int it = gbeg; it < gend; ++it) {
-      const float w = __builtin_amdgcn_exp2f(P.ws_ml[((int64_t)it * REP + r) * 2] - Ms);
-      osum += w * P.ws_o[((int64_t)it * REP + r) * D + d];
-      lsum += w * P.ws_ml[((int64_t)it * REP + r) * 2 + 1];
-    }
-    const int64_t oidx = ((int64_t)b * P.acc_stride_b + hq) * D + d;
+    float lsum = s_L[r];
+    float o4[4] = {acc4[k].x, acc4[k].y, acc4[k].z, acc4[k].w};
+    const int64_t obase = ((int64_t)b * P.acc_stride_b + hq) * D + d0;
     if (merge_in) {
       const float w = __builtin_amdgcn_exp2f(s_accm[r] - Ms);
-      osum += w * P.o[oidx];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] += w * P.o[obase + e];
       lsum += w * s_accl[r];
     }
     if (write_acc) {
-      P.o[oidx] = osum;
-      if (d == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) P.o[obase + e] = o4[e];
+      if (d0 == 0) {
         const int64_t a = (int64_t)b * P.acc_stride_b + hq;
         P.m[a] = (M == -INFINITY) ? -INFINITY : M * kLn2;
         P.l[a] = lsum;
       }
     }
     if (P.out != nullptr) {
-      const float v = lsum > 0.f ? osum / lsum : 0.f;
-      store_elem(P.out, ((int64_t)b * P.H + hq) * D + d, P.out_dtype, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        store_elem(P.out, ((int64_t)b * P.H + hq) * D + d0 + e, P.out_dtype, lsum > 0.f ? o4[e] / lsum : 0.f);
     }
-    if (P.lse != nullptr && d == 0) {
+    if (P.lse != nullptr && d0 == 0)
       P.lse[(int64_t)b * P.H + hq] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
-    }
   }
-  if (tid == 0) P.counters[g] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -446,32 +647,38 @@ extern "C" size_t halo_decode_workspace_size(int n_work, int rep_t, int D) {
 
 namespace {
 
+constexpr int kWavesPerItem = 4;
+
 template <int DT, int D, int REP>
-int launch_decode(const DecodeParams& p, int n_work, hipStream_t st) {
-  constexpr int NW = 4;
-  hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, NW>), dim3(n_work), dim3(64 * NW), 0, st, p);
+int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int n_groups, hipStream_t st) {
+  hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem), 0,
+                     st, p);
+  HALO_CHECK_HIP(hipGetLastError());
+  hipLaunchKernelGGL((decode_merge_kernel<D, REP>), dim3(n_groups), dim3(256), 0, st, mp);
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
 
 template <int DT, int D>
-int dispatch_rep(const DecodeParams& p, int rep_t, int n_work, hipStream_t st) {
+int dispatch_rep(const DecodeParams& p, const MergeParams& mp, int rep_t, int n_work, int n_groups,
+                 hipStream_t st) {
   switch (rep_t) {
-    case 1: return launch_decode<DT, D, 1>(p, n_work, st);
-    case 2: return launch_decode<DT, D, 2>(p, n_work, st);
-    case 4: return launch_decode<DT, D, 4>(p, n_work, st);
-    case 8: return launch_decode<DT, D, 8>(p, n_work, st);
+    case 1: return launch_decode<DT, D, 1>(p, mp, n_work, n_groups, st);
+    case 2: return launch_decode<DT, D, 2>(p, mp, n_work, n_groups, st);
+    case 4: return launch_decode<DT, D, 4>(p, mp, n_work, n_groups, st);
+    case 8: return launch_decode<DT, D, 8>(p, mp, n_work, n_groups, st);
   }
   set_error("rep_t must be 1, 2, 4 or 8");
   return HALO_E_UNSUPPORTED;
 }
 
 template <int DT>
-int dispatch_d(const DecodeParams& p, int D, int rep_t, int n_work, hipStream_t st) {
-  if (D == 64) return dispatch_rep<DT, 64>(p, rep_t, n_work, st);
-  if (D == 128) return dispatch_rep<DT, 128>(p, rep_t, n_work, st);
+int dispatch_d(const DecodeParams& p, const MergeParams& mp, int D, int rep_t, int n_work, int n_groups,
+               hipStream_t st) {
+  if (D == 64) return dispatch_rep<DT, 64>(p, mp, rep_t, n_work, n_groups, st);
+  if (D == 128) return dispatch_rep<DT, 128>(p, mp, rep_t, n_work, n_groups, st);
   if constexpr (DT != HALO_F32) {
-    if (D == 256) return dispatch_rep<DT, 256>(p, rep_t, n_work, st);
+    if (D == 256) return dispatch_rep<DT, 256>(p, mp, rep_t, n_work, n_groups, st);
   }
   set_error("head_dim must be 64, 128 or 256 (256 for bf16/f16 only)");
   return HALO_E_UNSUPPORTED;
@@ -487,9 +694,8 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
                                 const int64_t* q_pos, float scale,
                                 float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
                                 void* out, int out_dtype, float* lse,
-                                void* workspace, size_t workspace_bytes, int32_t* counters,
-                                void* stream) {
-  HALO_CHECK_ARG(q && descs && work && group_offsets && counters, "null pointer argument");
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  HALO_CHECK_ARG(q && descs && work && group_offsets, "null pointer argument");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0, "need H % H_kv == 0 and positive sizes");
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
   HALO_CHECK_ARG(out == nullptr || out_dtype == HALO_F32 || out_dtype == HALO_BF16 || out_dtype == HALO_F16,
@@ -516,25 +722,31 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
   p.n_sub = n_sub;
   p.descs = descs;
   p.work = work;
-  p.group_offsets = group_offsets;
   p.q_pos = q_pos;
   p.scale2 = (float)((double)scale * 1.4426950408889634);
-  p.m = m;
-  p.l = l;
-  p.o = o;
-  p.acc_stride_b = acc_stride_b;
-  p.acc_mode = acc_mode;
-  p.out = out;
-  p.out_dtype = out_dtype;
-  p.lse = lse;
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + (size_t)n_work * rep_t * D;
-  p.counters = counters;
+  MergeParams mp;
+  mp.group_offsets = group_offsets;
+  mp.H = H;
+  mp.H_kv = H_kv;
+  mp.rep = rep;
+  mp.n_sub = n_sub;
+  mp.m = m;
+  mp.l = l;
+  mp.o = o;
+  mp.acc_stride_b = acc_stride_b;
+  mp.acc_mode = acc_mode;
+  mp.out = out;
+  mp.out_dtype = out_dtype;
+  mp.lse = lse;
+  mp.ws_o = p.ws_o;
+  mp.ws_ml = p.ws_ml;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
-    case HALO_F32: return dispatch_d<HALO_F32>(p, D, rep_t, n_work, st);
-    case HALO_BF16: return dispatch_d<HALO_BF16>(p, D, rep_t, n_work, st);
-    default: return dispatch_d<HALO_F16>(p, D, rep_t, n_work, st);
+    case HALO_F32: return dispatch_d<HALO_F32>(p, mp, D, rep_t, n_work, n_groups, st);
+    case HALO_BF16: return dispatch_d<HALO_BF16>(p, mp, D, rep_t, n_work, n_groups, st);
+    default: return dispatch_d<HALO_F16>(p, mp, D, rep_t, n_work, n_groups, st);
   }
 }
 

@@ -123,6 +123,49 @@ def _num_cus(device) -> int:
         return 256
 
 
+def pack_descs(chunks: Sequence[ChunkRef], *, B: int, H_kv: int, D: int, dtype: torch.dtype):
+    """halo_chunk_desc records for ``chunks`` (validated); returns
+    (numpy structured array, list of tensors to keep alive)."""
+    descs = np.zeros(len(chunks), dtype=DESC_DTYPE)
+    keep = []
+    for i, c in enumerate(chunks):
+        k, v = c.k, c.v
+        if k.dtype != dtype or v.dtype != dtype:
+            raise AssertionError(f"chunk {i}: dtype {k.dtype}/{v.dtype} != {dtype}")
+        if k.shape[-1] != D or v.shape[-1] != D:
+            raise AssertionError(f"chunk {i}: head dim {k.shape[-1]}/{v.shape[-1]} != {D}")
+        if c.batch < 0:
+            if k.dim() != 4 or k.shape[0] != B or k.shape[1] != H_kv:
+                raise AssertionError(f"k shape {tuple(k.shape)} != ({B}, {H_kv}, T_c, {D})")
+            if tuple(v.shape) != tuple(k.shape):
+                raise AssertionError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
+        else:
+            if k.dim() != 3 or k.shape[0] != H_kv or tuple(v.shape) != tuple(k.shape):
+                raise AssertionError(f"ragged chunk {i}: expected (H_kv, T_c, D), got {tuple(k.shape)}")
+            if not 0 <= c.batch < B:
+                raise AssertionError(f"ragged chunk {i}: batch {c.batch} outside [0, {B})")
+        _check_kv(k, f"chunk {i} k")
+        _check_kv(v, f"chunk {i} v")
+        keep += [k, v]
+        d = descs[i]
+        d["k"], d["v"] = k.data_ptr(), v.data_ptr()
+        if c.batch < 0:
+            d["ksb"], d["ksh"], d["kst"] = k.stride(0), k.stride(1), k.stride(2)
+            d["vsb"], d["vsh"], d["vst"] = v.stride(0), v.stride(1), v.stride(2)
+        else:
+            d["ksb"], d["ksh"], d["kst"] = 0, k.stride(0), k.stride(1)
+            d["vsb"], d["vsh"], d["vst"] = 0, v.stride(0), v.stride(1)
+        d["start"] = int(c.chunk_start)
+        d["T"] = c.T
+        d["flags"] = nat.CHUNK_CAUSAL if c.causal else 0
+        d["batch"] = int(c.batch)
+    return descs, keep
+
+
+def descs_to_device(descs: np.ndarray, device) -> torch.Tensor:
+    return _to_device(descs.view(np.uint8).copy(), device)
+
+
 def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                chunks: Sequence[ChunkRef], device, rep_t: Optional[int] = None,
                split: Optional[int] = None, q_pos_host: Optional[Sequence[int]] = None) -> DecodePlan:
@@ -140,37 +183,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
     n_sub = -(-rep // rep_t)
     n_groups = B * H_kv * n_sub
 
-    descs = np.zeros(len(chunks), dtype=DESC_DTYPE)
-    keep = []
-    for i, c in enumerate(chunks):
-        k, v = c.k, c.v
-        if k.dtype != dtype or v.dtype != dtype:
-            raise AssertionError(f"chunk {i}: dtype {k.dtype}/{v.dtype} != {dtype}")
-        if k.shape[-1] != D or v.shape[-1] != D:
-            raise AssertionError(f"chunk {i}: head dim {k.shape[-1]}/{v.shape[-1]} != {D}")
-        if c.batch < 0:
-            if k.dim() != 4 or k.shape[0] != B or k.shape[1] != H_kv:
-                raise AssertionError(f"k shape {tuple(k.shape)} != ({B}, {H_kv}, T_c, {D})")
-            if tuple(v.shape) != tuple(k.shape):
-                raise AssertionError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
-        else:
-            if k.dim() != 3 or k.shape[0] != H_kv or tuple(v.shape) != tuple(k.shape):
-                raise AssertionError(f"ragged chunk {i}: expected (H_kv, T_c, D), got {tuple(k.shape)}")
-        _check_kv(k, f"chunk {i} k")
-        _check_kv(v, f"chunk {i} v")
-        keep += [k, v]
-        d = descs[i]
-        d["k"], d["v"] = k.data_ptr(), v.data_ptr()
-        if c.batch < 0:
-            d["ksb"], d["ksh"], d["kst"] = k.stride(0), k.stride(1), k.stride(2)
-            d["vsb"], d["vsh"], d["vst"] = v.stride(0), v.stride(1), v.stride(2)
-        else:
-            d["ksb"], d["ksh"], d["kst"] = 0, k.stride(0), k.stride(1)
-            d["vsb"], d["vsh"], d["vst"] = 0, v.stride(0), v.stride(1)
-        d["start"] = int(c.chunk_start)
-        d["T"] = c.T
-        d["flags"] = nat.CHUNK_CAUSAL if c.causal else 0
-        d["batch"] = int(c.batch)
+    descs, keep = pack_descs(chunks, B=B, H_kv=H_kv, D=D, dtype=dtype)
 
     def live(c: ChunkRef, b: int) -> bool:
         if c.batch >= 0 and c.batch != b:
@@ -225,20 +238,19 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
 
 
 # ---------------------------------------------------------------------------
-# Workspace: per (device, stream) partial buffer plus self-cleaning counters.
+# Workspace: one partial buffer per (device, stream); launches on one stream
+# are ordered, so reusing it across calls is safe.
 # ---------------------------------------------------------------------------
 _WS: dict = {}
 
 
-def workspace(device, stream_ptr: int, nbytes: int, n_counters: int):
+def workspace(device, stream_ptr: int, nbytes: int) -> torch.Tensor:
     key = (torch.device(device).index, stream_ptr)
-    ws, ctr = _WS.get(key, (None, None))
+    ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-    if ctr is None or ctr.numel() < n_counters:
-        ctr = torch.zeros(max(n_counters, 4096), dtype=torch.int32, device=device)
-    _WS[key] = (ws, ctr)
-    return ws, ctr
+        _WS[key] = ws
+    return ws
 
 
 def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
@@ -280,7 +292,7 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
             raise AssertionError("all tensors must be on the query's device")
     sp = nat.stream_ptr(stream)
     nbytes = int(L.halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
-    ws, ctr = workspace(q.device, sp, nbytes, plan.n_groups)
+    ws = workspace(q.device, sp, nbytes)
     status = L.halo_decode_attn(
         q.data_ptr(), q.stride(0), q.stride(1), nat.dtype_code(plan.dtype),
         plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t,
@@ -290,6 +302,6 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         nat.ptr(q_pos), float(scale),
         nat.ptr(m), nat.ptr(l), nat.ptr(o), plan.H, acc_mode,
         nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse),
-        ws.data_ptr(), ws.numel(), ctr.data_ptr(), sp,
+        ws.data_ptr(), ws.numel(), sp,
     )
     nat.check(status, "halo_decode_attn")

@@ -70,12 +70,12 @@ typedef struct halo_chunk_desc {
  * is an empty partial).
  */
 
-/* Bytes of workspace a launch with `n_work` items needs (partials). */
+/* Bytes of workspace a launch with `n_work` items needs (one partial per item). */
 size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
 
 /*
- * Split-K GQA decode attention over a chunk table with a fused
- * log-sum-exp merge.  One query token per batch row.
+ * Split-K GQA decode attention over a chunk table with a log-sum-exp merge.
+ * One query token per batch row.
  *
  *   q        (B, H, D) elements of `dtype`, q[b*q_stride_b + h*q_stride_h + d]
  *   descs    device array of n_desc halo_chunk_desc
@@ -89,8 +89,12 @@ size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
  *            bit1: write the merged (m,l,o) back.  Ignored when m == NULL.
  *   out      (B,H,D) of `out_dtype` = o/l (0 where l == 0), or NULL
  *   lse      (B,H) fp32 = m + log(l) (-inf where l == 0), or NULL
- *   counters device int32 [n_groups], zero on entry; left zero on return
+ *   workspace caller-owned device memory of halo_decode_workspace_size()
+ *            bytes; calls that overlap on one stream must not share it
  *
+ * Enqueues two kernels on `stream`: the split-K attention pass, which writes
+ * one partial per work item, and a merge pass that combines each group's
+ * partials (in work order: results are deterministic) with the accumulators.
  * Replaces update_chunk / finalize / triton_chunked_attention
  * (halo/triton_chunked.py:151-267) and the PyTorch chunk walk
  * (halo/kv_cache_chunked.py:194-276, 864-964) for T_q == 1.
@@ -103,8 +107,7 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
                      const int64_t* q_pos, float scale,
                      float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
                      void* out, int out_dtype, float* lse,
-                     void* workspace, size_t workspace_bytes, int32_t* counters,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * finalize: out = o / (l > 0 ? l : 1) cast to out_dtype, optional
@@ -123,6 +126,53 @@ int halo_finalize(const float* m, const float* l, const float* o, int B, int H, 
 int halo_lse_merge(const float* out_a, const float* lse_a, const float* out_b,
                    const float* lse_b, int64_t n, int D, float* out, float* lse,
                    void* stream);
+
+/* ---- chunk-relevance scoring ------------------------------------------- */
+
+/*
+ * Page-mean keys for `n_pages` pages of `page` rows starting at row `row0`:
+ * kmean[b,h,j,:] = dtype(sum_t K[b,h,row0+j*page+t,:] / page), fp32 sums in
+ * row order, one rounding to the key dtype (torch's .mean keeps the dtype).
+ * Replaces the per-update recomputation of baselines/scorer_ablations.py:
+ * 209-216; called once per page when it fills.
+ */
+int halo_chunk_means(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                     int dtype, int B, int H_kv, int D, int64_t row0, int page, int n_pages,
+                     void* kmean, int64_t km_stride_b, int64_t km_stride_h, int64_t km_stride_p,
+                     void* stream);
+
+/*
+ * Chunk scoring + top-k, one selection per batch row (per_row != 0) or one
+ * over all rows (per_row == 0: the reference's amax over batch).  For
+ * selection s, eligible chunk indices are eligible[s*elig_stride + i],
+ * i < n_elig_per_sel[s] (or n_elig when that array is NULL; n_elig <= 1024).
+ *   attn[i] = max over (rows, h_kv) of sum_d qbar[h_kv,d] * kmean[p_i,d], with
+ *   qbar the mean of each KV head's query heads rounded to the q dtype
+ *   (baselines/scorer_ablations.py:223-237).  With normalize != 0 the score is
+ *   alpha*minmax(attn) + beta*recency + gamma*sink over P_total pages
+ *   (:238-263); otherwise the raw attn.
+ * Top-k order: score descending, then chunk index ascending; the k chosen
+ * indices are written ascending to idx_out[s*k + j] (-1 when fewer than k are
+ * eligible); raw/final scores to score_out[s*n_elig + i] when non-NULL.  When
+ * `table` is non-NULL, descriptor catalog[s*catalog_stride + p] of each chosen
+ * chunk p is copied to table[s*table_stride + table_slot0 + j] (an empty
+ * descriptor, T_c = 0, fills unused slots), so a following halo_decode_attn
+ * on the same stream attends the selection with no host round trip.
+ * Replaces select_hot_pages (baselines/scorer_ablations.py:218-268) and the
+ * torch.topk + .cpu() sync at :266.
+ */
+int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                          int B, int H, int H_kv, int D,
+                          const void* kmean, int64_t km_stride_b, int64_t km_stride_h,
+                          int64_t km_stride_p,
+                          const int32_t* eligible, int64_t elig_stride,
+                          const int32_t* n_elig_per_sel, int n_elig, int k, int per_row,
+                          int32_t* idx_out, float* score_out,
+                          const halo_chunk_desc* catalog, int64_t catalog_stride,
+                          halo_chunk_desc* table, int64_t table_stride, int table_slot0,
+                          int normalize, float alpha, float beta, float gamma,
+                          int refresh, int sink_pages, int P_total,
+                          void* stream);
 
 /* ---- build metadata ---------------------------------------------------- */
 const char* halo_last_error(void);

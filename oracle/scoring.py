@@ -47,8 +47,14 @@ def gqa_mean_query(query: np.ndarray, H_kv: int, dtype: str = "float32") -> np.n
     if H == H_kv:
         return query.astype(np.float32)
     rep = H // H_kv
-    g = query.reshape(B, H_kv, rep, T_q, D).astype(np.float64).mean(axis=2)
-    return round_to(g.astype(np.float32), dtype)
+    g = query.reshape(B, H_kv, rep, T_q, D).astype(np.float32)
+    # torch's mean: fp32 accumulation in order, times the fp32 factor 1/rep,
+    # one rounding to the query dtype.
+    acc = np.zeros((B, H_kv, T_q, D), np.float32)
+    for r in range(rep):
+        acc = (acc + g[:, :, r]).astype(np.float32)
+    acc = (acc * np.float32(1.0 / rep)).astype(np.float32)
+    return round_to(acc, dtype)
 
 
 def mean_key_scores(query: np.ndarray, k_mean: np.ndarray, dtype: str = "float32") -> np.ndarray:

@@ -1,0 +1,167 @@
+"""GPU parity of the chunk scorer (page means, q.Kbar scores, top-k) and of
+the tiered decode layer (scorer -> chunk table -> attention, no host sync)."""
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import scoring as S
+from oracle.inputs import C1, C2, decode_inputs, round_bf16
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TDT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
+
+
+def _gpu(a, dtype, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(TDT[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_chunk_means(dev, dtype):
+    from halo_amd.chunk_scorer import chunk_means
+    x = decode_inputs(21, B=2, H=4, H_kv=2, T=1100, D=128, dtype=dtype)
+    k = _gpu(x.k, dtype, dev)
+    km = chunk_means(k, 256).float().cpu().numpy()
+    ref = S.page_means(x.k, 256, dtype)
+    assert km.shape == ref.shape == (2, 2, 4, 128)
+    if dtype == "float32":
+        np.testing.assert_allclose(km, ref, rtol=1e-6, atol=1e-7)
+    else:  # at most one rounding step of the storage dtype apart
+        ulp = np.abs(ref) * (2.0 ** -7 if dtype == "bfloat16" else 2.0 ** -10) + 1e-6
+        assert (np.abs(km - ref) <= ulp).all()
+        assert (km == ref).mean() > 0.97
+
+
+@pytest.mark.parametrize("H,H_kv,dtype", [(8, 8, "float32"), (32, 8, "bfloat16"), (28, 4, "float16")])
+def test_scores_and_topk_match_oracle(dev, H, H_kv, dtype):
+    from halo_amd.chunk_scorer import score_topk
+    rng = np.random.default_rng(5)
+    D, P = 128, 40
+    for trial in range(5):
+        q = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+        km = rng.standard_normal((1, H_kv, P, D)).astype(np.float32) * 0.3
+        if dtype != "float32":
+            q = q.astype(np.float16).astype(np.float32) if dtype == "float16" else round_bf16(q)
+            km = km.astype(np.float16).astype(np.float32) if dtype == "float16" else round_bf16(km)
+        elig = np.sort(rng.choice(P, size=30, replace=False))
+        idx, sc = score_topk(_gpu(q, dtype, dev), _gpu(km, dtype, dev), torch.from_numpy(elig).to(dev), 6)
+        ref_sc = S.mean_key_scores(q, km, dtype)[elig]
+        np.testing.assert_allclose(sc[0, :30].cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-5)
+        ref_sel = S.select_chunks(q, km, elig, 6, dtype)
+        srt = np.sort(ref_sc.astype(np.float64))[::-1]
+        if srt[5] - srt[6] > 1e-4:  # margin-checked
+            assert idx[0].cpu().numpy().tolist() == ref_sel.tolist()
+
+
+def test_topk_tie_break_on_device(dev):
+    from halo_amd.chunk_scorer import score_topk
+    # identical means for chunks 1, 2 and 4: ties resolve to lower index
+    km = np.zeros((1, 1, 6, 64), np.float32)
+    km[0, 0, [1, 2, 4], 0] = 3.0
+    km[0, 0, 3, 0] = 2.0
+    km[0, 0, 0, 0] = 1.0
+    q = np.zeros((1, 1, 1, 64), np.float32)
+    q[..., 0] = 1.0
+    for k, want in [(1, [1]), (2, [1, 2]), (3, [1, 2, 4]), (4, [1, 2, 3, 4]), (8, [0, 1, 2, 3, 4, 5, -1, -1])]:
+        idx, _ = score_topk(_gpu(q, "float32", dev), _gpu(km, "float32", dev),
+                            torch.arange(6, device=dev), k)
+        assert idx[0].cpu().tolist() == want
+
+
+def test_halopress_normalised_score(dev):
+    from halo_amd.chunk_scorer import score_topk
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((1, 8, 1, 64)).astype(np.float32)
+    km = rng.standard_normal((1, 2, 50, 64)).astype(np.float32)
+    kw = dict(alpha=1.0, beta=0.5, gamma=2.0, refresh_window=16, sink_tokens=4, page_size=16)
+    attn = S.mean_key_scores(q, km)
+    ref = S.halopress_page_scores(attn, **kw)
+    idx, sc = score_topk(_gpu(q, "float32", dev), _gpu(km, "float32", dev), torch.arange(50, device=dev), 13,
+                         normalize=True, alpha=1.0, beta=0.5, gamma=2.0, refresh_window=16,
+                         sink_pages=min(4 // 16 + 1, 50), P_total=50)
+    np.testing.assert_allclose(sc[0].cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    assert idx[0].cpu().numpy().tolist() == S.topk_indices(ref, 13).tolist()
+
+
+def test_per_row_ragged_selection(dev):
+    from halo_amd.chunk_scorer import score_topk
+    rng = np.random.default_rng(9)
+    B, H, H_kv, D, P = 4, 8, 2, 64, 20
+    q = rng.standard_normal((B, H, 1, D)).astype(np.float32)
+    km = rng.standard_normal((B, H_kv, P, D)).astype(np.float32)
+    n_el = np.array([20, 7, 3, 12], np.int32)
+    elig = np.tile(np.arange(P, dtype=np.int32), (B, 1))
+    idx, sc = score_topk(_gpu(q, "float32", dev), _gpu(km, "float32", dev), torch.from_numpy(elig).to(dev), 5,
+                         per_row=True, n_elig_per_sel=torch.from_numpy(n_el).to(dev))
+    for b in range(B):
+        want = S.select_chunks(q[b:b + 1], km[b:b + 1], np.arange(n_el[b]), 5).tolist()
+        want += [-1] * (5 - len(want))
+        assert idx[b].cpu().tolist() == want
+
+
+def _tiered_from_fixture(cfg, dev):
+    from halo_amd.decode import ChunkRef
+    from halo_amd.tiered import TieredDecodeLayer
+    x = decode_inputs(cfg["seed"], B=1, H=cfg["H"], H_kv=cfg["H_kv"], T=cfg["T"], D=cfg["D"], dtype=cfg["dtype"],
+                      n_planted=cfg.get("n_planted", 0), sigma=cfg.get("sigma", 1.0))
+    q, k, v = (_gpu(a, cfg["dtype"], dev) for a in (x.q, x.k, x.v))
+    c = cfg["chunk"]
+    n = cfg["T"] // c
+    n_cold = n - cfg["n_hot"]
+    refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True) for i in range(n)]
+    layer = TieredDecodeLayer(B=1, H=cfg["H"], H_kv=cfg["H_kv"], D=cfg["D"], dtype=TDT[cfg["dtype"]],
+                              hot=refs[n_cold:], cold=refs[:n_cold], top_k=cfg["top_k"], device=dev)
+    return layer, q
+
+
+@pytest.mark.parametrize("name,cfg", [("c1_decode", C1), ("c2_layer0", C2)])
+def test_tiered_layer_matches_golden(dev, name, cfg):
+    """Scorer picks the fixture's chunks bit-exactly; attention over hot +
+    selected matches the float64 closed form (1e-5 fp32, 2e-2 bf16)."""
+    fx = np.load(os.path.join(GOLD, name + ".npz"))
+    layer, q = _tiered_from_fixture(cfg, dev)
+    out = torch.empty((1, cfg["H"], cfg["D"]), device=dev, dtype=TDT[cfg["dtype"]])
+    lse = torch.empty((1, cfg["H"]), device=dev)
+    layer.step(q[:, :, 0], scale=1 / math.sqrt(cfg["D"]), out=out, lse=lse)
+    assert layer.idx[0].cpu().numpy().tolist() == fx["selected"].tolist()
+    tol = 1e-5 if cfg["dtype"] == "float32" else 2e-2
+    assert np.abs(out.float().cpu().numpy() - fx["out"]).max() <= tol
+    ltol = 1e-5 if cfg["dtype"] == "float32" else 1e-3
+    assert np.abs(lse.cpu().numpy() - fx["lse"]).max() <= ltol
+    np.testing.assert_allclose(layer.scores[0].cpu().numpy(), fx["scores"], rtol=1e-4, atol=1e-5)
+
+
+def test_tiered_layer_in_hip_graph(dev):
+    """The two-kernel step replays from a captured graph; every replay
+    matches the eager result (fresh inputs copied in between replays)."""
+    layer, q = _tiered_from_fixture(C1, dev)
+    q3 = q[:, :, 0].contiguous()
+    out = torch.empty((1, 8, 64), device=dev)
+    lse = torch.empty((1, 8), device=dev)
+    layer.step(q3, scale=0.125, out=out, lse=lse)  # warm the workspace
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer.step(q3, scale=0.125, out=out, lse=lse)  # warm the capture stream's workspace
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            layer.step(q3, scale=0.125, out=out, lse=lse)
+    torch.cuda.current_stream().wait_stream(s)
+    rng = np.random.default_rng(3)
+    for rep in range(4):
+        newq = torch.from_numpy(rng.standard_normal((1, 8, 64)).astype(np.float32)).to(dev)
+        q3.copy_(newq)
+        g.replay()
+        torch.cuda.synchronize()
+        got_o, got_l, got_i = out.clone(), lse.clone(), layer.idx.clone()
+        layer.step(q3, scale=0.125, out=out, lse=lse)
+        torch.cuda.synchronize()
+        assert torch.equal(got_i, layer.idx)
+        assert torch.equal(got_o, out) and torch.equal(got_l, lse)

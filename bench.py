@@ -6,9 +6,10 @@ hot_ratio 0.25 (the last 8 chunks), 24 cold chunks of which the scorer
 selects the top 4 per layer per step by mean-key dot product; keys carry 4
 planted high-variance channels (sigma 8).  32 layers with distinct buffers
 (4 GiB of K/V in HBM, far above the 256 MB last-level cache).  One step =
-for every layer: score + top-4 selection kernel, then the split-K attention
-kernel over hot + selected chunks; the 64 launches are replayed from one
-HIP graph.  Inputs are resident in HBM when the timed region starts (the
+for every layer: the split-K attention kernel over the hot chunks and 4
+selection slots (whose workgroups first score the 24 cold chunks' mean keys
+and pick the top 4 in-kernel), then the split-K merge kernel; the 64
+launches are replayed from one HIP graph.  Inputs are resident in HBM when the timed region starts (the
 cold chunks' HBM copies stand for their refetched state); the rate with the
 top-4 refetched over PCIe every step is measured separately and reported as
 ``pcie_inclusive``.
@@ -254,35 +255,49 @@ def main() -> int:
     dt = (time.perf_counter() - t0) / args.steps
     log(f"timed {args.steps} steps: {dt * 1e3:.3f} ms/step")
 
-    # Per-kernel durations with HIP events on the launch stream (default
-    # stream; one eager step first so its workspace is allocated).
-    step()
-    torch.cuda.synchronize()
-    rows = layers[0].attended_rows
-    attn_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4
-    score_bytes = (T // chunk - n_hot) * H_kv * D * 2 + H * D * 2
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2 * L)]
-    attn_ms, score_ms = [], []
-    reps = max(3, min(args.steps, 20))
-    for _ in range(reps):
-        for li in range(L):
-            a0, a1 = ev[2 * li]
-            b0, b1 = ev[2 * li + 1]
-            b0.record()
-            layers[li].select(qs[li])
-            b1.record()
-            a0.record()
-            layers[li].attend(qs[li], scale=scale, out=outs[li], lse=lses[li])
-            a1.record()
+    # Per-kernel durations with HIP events on the launch stream.  Host-side
+    # launch latency would inflate per-launch event pairs, so the attention
+    # launches (split-K kernel + merge kernel) and the scorer launches are each
+    # captured in a graph of their own and timed over whole replays on the
+    # capture stream.
+    def capture(fn):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr, stream=s):
+                fn()
         torch.cuda.synchronize()
-        for li in range(L):
-            attn_ms.append(ev[2 * li][0].elapsed_time(ev[2 * li][1]))
-            score_ms.append(ev[2 * li + 1][0].elapsed_time(ev[2 * li + 1][1]))
-    attn_avg = statistics.mean(attn_ms)
-    score_avg = statistics.mean(score_ms)
+        return gr
+
+    # one layer's launch pair: attention with in-kernel selection + merge
+    g_attn = capture(lambda: [layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li]) for li in range(L)])
+    # the standalone scorer kernel (plug-in API path), for reference
+    g_score = capture(lambda: [layers[li].select(qs[li]) for li in range(L)])
+
+    def time_graph(gr, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            gr.replay()
+            e0.record(s)
+            for _ in range(reps):
+                gr.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * L)
+
+    reps = max(5, min(args.steps, 50))
+    attn_avg = time_graph(g_attn, reps)
+    score_avg = time_graph(g_score, reps)
+    rows = layers[0].attended_rows
+    # algorithmic bytes of one layer's launch: K+V rows of hot + selected
+    # chunks, q, out and lse, plus the cold chunks' mean keys it scores
+    score_bytes = (T // chunk - n_hot) * H_kv * D * 2
+    attn_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4 + (score_bytes if layers[0].fused else 0)
     achieved = attn_bytes / (attn_avg * 1e-3) / 1e9
-    step_bytes = L * (attn_bytes + score_bytes)
-    log(f"attention kernel avg {attn_avg * 1e3:.2f} us ({achieved:.0f} GB/s), scorer {score_avg * 1e3:.2f} us")
+    step_bytes = L * (attn_bytes if layers[0].fused else attn_bytes + score_bytes + H * D * 2)
+    log(f"attention launch avg {attn_avg * 1e3:.2f} us ({achieved:.0f} GB/s), "
+        f"standalone scorer {score_avg * 1e3:.2f} us")
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "decode_attn_c2_traffic.json")
@@ -309,7 +324,9 @@ def main() -> int:
             "workload": "Llama-3-8B-shaped GQA decode, 32 layers looped, batch 1, 32/8 heads, d128, "
                         "32768 ctx in 32x1024 chunks, 8 hot + top-4 of 24 cold by mean-key score",
             "layers": L, "batch": 1, "q_heads": H, "kv_heads": H_kv, "head_dim": D, "ctx": T,
-            "chunk": chunk, "hot_chunks": n_hot, "top_k": top_k, "launch": "hip graph, 2 kernels per layer",
+            "chunk": chunk, "hot_chunks": n_hot, "top_k": top_k,
+            "launch": ("hip graph; per layer: attention kernel with in-kernel top-k selection + merge kernel"
+                       if layers[0].fused else "hip graph; per layer: scorer + attention + merge kernels"),
             "split_rows": int(layers[0].plan.work_host[0, 3] - layers[0].plan.work_host[0, 2]),
             "work_items": layers[0].plan.n_work,
         },
@@ -317,7 +334,7 @@ def main() -> int:
         "hbm_bytes_per_step": step_bytes,
         "roofline": {
             "bound": "hbm",
-            "kernel": "halo::decode_attn_kernel<bf16, 128, 4, 4>",
+            "kernel": "halo_decode_attn_tiered (decode_attn_kernel<bf16,128,4,4> + decode_merge_kernel<128,4>)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -325,7 +342,7 @@ def main() -> int:
             "traffic": traffic,
             "bytes_per_launch": attn_bytes,
             "avg_launch_us": attn_avg * 1e3,
-            "scorer_avg_us": score_avg * 1e3,
+            "standalone_scorer_avg_us": score_avg * 1e3,
         },
     }
     if not args.no_pcie:

@@ -36,21 +36,39 @@ _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _size_t = ctypes.c_size_t
 
+
+
+class SelectCfg(ctypes.Structure):
+    """halo_select_cfg (include/halo_hip.h)."""
+    _fields_ = [
+        ("kmean", _c_void_p),
+        ("km_stride_b", _i64), ("km_stride_h", _i64), ("km_stride_p", _i64),
+        ("catalog", _c_void_p),
+        ("catalog_stride", _i64),
+        ("n_cold_per_sel", _c_void_p),
+        ("n_cold", _i32), ("top_k", _i32), ("slot0", _i32), ("per_row", _i32),
+        ("idx_out", _c_void_p),
+        ("score_out", _c_void_p),
+    ]
+
+
+_DECODE_ARGS = [
+    _c_void_p, _i64, _i64, _i32,             # q, q_stride_b, q_stride_h, dtype
+    _i32, _i32, _i32, _i32, _i32,            # B, H, H_kv, D, rep_t
+    _c_void_p, _i32,                         # descs, n_desc
+    _c_void_p, _i32,                         # work, n_work
+    _c_void_p, _i32,                         # group_offsets, n_groups
+    _c_void_p, _f32,                         # q_pos, scale
+    _c_void_p, _c_void_p, _c_void_p, _i64, _i32,  # m, l, o, acc_stride_b, acc_mode
+    _c_void_p, _i32, _c_void_p,              # out, out_dtype, lse
+    _c_void_p, _size_t,                      # workspace, bytes
+]
+
 # name -> (restype, argtypes); mirrors include/halo_hip.h one to one.
 _SIGNATURES = {
     "halo_decode_workspace_size": (_size_t, [_i32, _i32, _i32]),
-    "halo_decode_attn": (_i32, [
-        _c_void_p, _i64, _i64, _i32,             # q, q_stride_b, q_stride_h, dtype
-        _i32, _i32, _i32, _i32, _i32,            # B, H, H_kv, D, rep_t
-        _c_void_p, _i32,                         # descs, n_desc
-        _c_void_p, _i32,                         # work, n_work
-        _c_void_p, _i32,                         # group_offsets, n_groups
-        _c_void_p, _f32,                         # q_pos, scale
-        _c_void_p, _c_void_p, _c_void_p, _i64, _i32,  # m, l, o, acc_stride_b, acc_mode
-        _c_void_p, _i32, _c_void_p,              # out, out_dtype, lse
-        _c_void_p, _size_t,                      # workspace, bytes
-        _c_void_p,                               # stream
-    ]),
+    "halo_decode_attn": (_i32, _DECODE_ARGS + [_c_void_p]),                      # + stream
+    "halo_decode_attn_tiered": (_i32, _DECODE_ARGS + [ctypes.POINTER(SelectCfg), _c_void_p]),  # + sel, stream
     "halo_finalize": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                              _c_void_p, _i32, _c_void_p, _c_void_p]),
     "halo_lse_merge": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,

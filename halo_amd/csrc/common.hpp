@@ -63,6 +63,14 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return __builtin_bit_cast(uint16_t, v);
 }
 
+// Materialises an fp32 value in a register so the compiler cannot fold the
+// operation that produced it into a later conversion (e.g. fptrunc(fmul) into
+// one mixed-precision FMA that rounds once instead of twice).
+__device__ __forceinline__ float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Store one fp32 value as element `dtype`.
 __device__ __forceinline__ void store_elem(void* base, int64_t idx, int dtype, float v) {
   if (dtype == HALO_F32) {

@@ -30,13 +30,17 @@ namespace halo {
 struct DecodeParams {
   const void* q;
   int64_t q_stride_b, q_stride_h;
-  int H, H_kv, rep, n_sub;
+  int B, H, H_kv, rep, n_sub;
   const halo_chunk_desc* descs;
   const int32_t* work;
   const int64_t* q_pos;
   float scale2;  // scale * log2(e)
+  int q_aligned;  // q rows 16-byte aligned: stage them with 16-byte loads
   float* ws_o;   // [n_work][REP][D]  per-item partial o (unnormalised)
   float* ws_ml;  // [n_work][REP][2]  per-item (m in log2 units, l)
+  int sel_on;     // fused chunk selection (halo_decode_attn_tiered)
+  float inv_rep;  // fp32(1/rep): the GQA query-mean factor
+  halo_select_cfg sel;
 };
 
 struct MergeParams {
@@ -215,6 +219,143 @@ __device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused chunk selection (selection-slot workgroups only).  Same arithmetic
+// as halo_chunk_score_topk: GQA-mean query rounded to the q dtype, ordered
+// fp32 dot products with the page means (products and sums rounded
+// separately), max over (row, KV head), rank by (score desc, index asc).
+// Every load is issued before the first barrier: one memory round trip.
+// Returns the chunk index for `slot` (-1: slot past the eligible count);
+// the chosen descriptors are left in LDS at s_cat.
+// ---------------------------------------------------------------------------
+constexpr int kSelMaxCold = 128;
+constexpr int kSelMaxQbar = 2048;
+constexpr int kSelBytes = kSelMaxQbar * 4 + 4 * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
+
+__device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
+  halo_chunk_desc u;
+  auto rf64 = [](int64_t x) {
+    const uint64_t ux = (uint64_t)x;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)ux);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(ux >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  u.k = reinterpret_cast<const void*>(rf64(reinterpret_cast<int64_t>(d.k)));
+  u.v = reinterpret_cast<const void*>(rf64(reinterpret_cast<int64_t>(d.v)));
+  u.k_stride_b = rf64(d.k_stride_b);
+  u.k_stride_h = rf64(d.k_stride_h);
+  u.k_stride_t = rf64(d.k_stride_t);
+  u.v_stride_b = rf64(d.v_stride_b);
+  u.v_stride_h = rf64(d.v_stride_h);
+  u.v_stride_t = rf64(d.v_stride_t);
+  u.chunk_start = rf64(d.chunk_start);
+  u.T_c = __builtin_amdgcn_readfirstlane(d.T_c);
+  u.flags = __builtin_amdgcn_readfirstlane(d.flags);
+  u.batch = __builtin_amdgcn_readfirstlane(d.batch);
+  u.reserved = 0;
+  return u;
+}
+
+template <int DT, int D, int NT>
+__device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, bool writer) {
+  using E = Elem<DT>;
+  constexpr int PIECES = D * E::size / 16;
+  const halo_select_cfg& S = P.sel;
+  const int tid = threadIdx.x;
+  const int rows = S.per_row ? 1 : P.B;
+  const int b0 = S.per_row ? b : 0;
+  const int sel = S.per_row ? b : 0;
+  const int n = __builtin_amdgcn_readfirstlane(S.n_cold_per_sel ? min(S.n_cold_per_sel[sel], S.n_cold) : S.n_cold);
+  const int kk = min(S.top_k, n);
+  const int H_kv = P.H_kv, rep = P.rep;
+  const int nrh = rows * H_kv;
+  const int triples = n * nrh;
+  float* s_qbar = reinterpret_cast<float*>(smem);
+  float* s_dot = s_qbar + kSelMaxQbar;
+  float* s_score = s_dot + 256;
+  int* s_sel = reinterpret_cast<int*>(s_score + 256);
+  int* s_pick = s_sel + 256;
+  halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
+
+  // one (page, row, head) page-mean row per thread, straight to registers
+  uint4 kb[PIECES];
+  int my_r = 0, my_h = 0;
+  if (tid < triples) {
+    const int i = tid / nrh, rh = tid % nrh;
+    my_r = rh / H_kv;
+    my_h = rh % H_kv;
+    const char* row = reinterpret_cast<const char*>(S.kmean) +
+                      ((int64_t)(b0 + my_r) * S.km_stride_b + (int64_t)my_h * S.km_stride_h + (int64_t)i * S.km_stride_p) *
+                          E::size;
+#pragma unroll
+    for (int c = 0; c < PIECES; ++c) kb[c] = *reinterpret_cast<const uint4*>(row + c * 16);
+  }
+  // GQA-mean query rows, rounded to the q dtype
+  for (int e = tid; e < rows * H_kv * D; e += NT) {
+    const int d = e % D, h = (e / D) % H_kv, r = e / (D * H_kv);
+    const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
+    float v;
+    if (rep == 1) {
+      v = load_elem(P.q, qb + (int64_t)h * P.q_stride_h + d, DT);
+    } else {
+      float acc = 0.f;
+      for (int j = 0; j < rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * rep + j) * P.q_stride_h + d, DT);
+      acc = opaque(acc * P.inv_rep);
+      v = DT == HALO_F32 ? acc
+          : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(acc) << 16)
+                             : f16_bits_to_f32(f32_to_f16_rne(acc)));
+    }
+    s_qbar[e] = v;
+  }
+  // the candidate descriptors
+  const uint32_t* cat = reinterpret_cast<const uint32_t*>(S.catalog + (int64_t)sel * S.catalog_stride);
+  constexpr int DW = sizeof(halo_chunk_desc) / 4;
+  for (int w = tid; w < n * DW; w += NT) reinterpret_cast<uint32_t*>(s_cat)[w] = cat[w];
+  __syncthreads();
+
+  if (tid < triples) {
+    const float* qg = s_qbar + (my_r * H_kv + my_h) * D;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < PIECES; ++c) {
+      float f[E::per16];
+      E::unpack(kb[c], f);
+#pragma unroll
+      for (int e = 0; e < E::per16; ++e) acc = acc + qg[c * E::per16 + e] * f[e];
+    }
+    s_dot[tid] = acc;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) {
+    float best = -INFINITY;
+    for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
+    s_score[i] = (best != best) ? -INFINITY : best;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) {
+    const float si = s_score[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) {
+      const float sj = s_score[j];
+      rank += (sj > si || (sj == si && j < i)) ? 1 : 0;
+    }
+    s_sel[i] = rank < kk;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) {
+    if (writer && S.score_out) S.score_out[(int64_t)sel * S.n_cold + i] = s_score[i];
+    if (!s_sel[i]) continue;
+    int pos = 0;
+    for (int j = 0; j < i; ++j) pos += s_sel[j];
+    s_pick[pos] = i;
+  }
+  __syncthreads();
+  if (writer && S.idx_out) {
+    for (int j = tid; j < S.top_k; j += NT) S.idx_out[(int64_t)sel * S.top_k + j] = j < kk ? s_pick[j] : -1;
+  }
+  return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
+}
+
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kernel(DecodeParams P) {
@@ -231,14 +372,15 @@ decode_attn_kernel(DecodeParams P) {
   constexpr int RPL = TILE / LPH;       // rows per lane in the q.k phase
   static_assert(SL * RPI == kWave && PPL * RPI == TILE && PPL % 2 == 0, "tile shape");
   static_assert(LPH == 8 || LPH == 16 || LPH == 32 || LPH == 64, "lane groups");
+  static_assert(kSelBytes <= (NW * REP * RB + NW * TILE * KROW + NW * TILE * REP * 4), "selection scratch");
 
-  constexpr int SZ_Q = REP * RB;
+  constexpr int SZ_Q = NW * REP * RB;  // one copy of the group's q per wave
   constexpr int SZ_K = NW * TILE * KROW;
   constexpr int SZ_P = NW * TILE * REP * 4;
   constexpr int SZ_A = SZ_Q + SZ_K + SZ_P;
   constexpr int SZ_B = NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
-  char* s_q = smem;
+  char* s_q = smem + (threadIdx.x / kWave) * REP * RB;
   char* s_kall = smem + SZ_Q;
   float* s_pall = reinterpret_cast<float*>(smem + SZ_Q + SZ_K);
   float* s_wo = reinterpret_cast<float*>(smem);
@@ -246,16 +388,36 @@ decode_attn_kernel(DecodeParams P) {
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  // Wave index and work item are wave-uniform; saying so keeps every value
+  // derived from them (buffer descriptors, row ranges) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int witem = blockIdx.x;
 
-  const int4 item = reinterpret_cast<const int4*>(P.work)[witem];
-  const halo_chunk_desc dsc = P.descs[item.x];
+  int4 item = reinterpret_cast<const int4*>(P.work)[witem];
+  item.x = __builtin_amdgcn_readfirstlane(item.x);
+  item.y = __builtin_amdgcn_readfirstlane(item.y);
+  item.z = __builtin_amdgcn_readfirstlane(item.z);
+  item.w = __builtin_amdgcn_readfirstlane(item.w);
   const int g = item.y;
   const int sub = g % P.n_sub;
   const int bh = g / P.n_sub;
   const int h_kv = bh % P.H_kv;
   const int b = bh / P.H_kv;
+  halo_chunk_desc dsc;
+  if (P.sel_on && item.x >= P.sel.slot0 && item.x < P.sel.slot0 + P.sel.top_k) {
+    // selection slot: choose the chunk first (workgroup-uniform branch)
+    const bool writer = (P.sel.per_row || b == 0) && h_kv == 0 && sub == 0 && item.x == P.sel.slot0 && item.z == 0;
+    const int pick = fused_select<DT, D, 64 * NW>(P, b, smem, item.x - P.sel.slot0, writer);
+    if (pick >= 0) {
+      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelMaxQbar * 4 + 4 * 256 * 4)[pick]);
+    } else {
+      dsc = P.descs[item.x];
+      dsc.T_c = 0;
+    }
+    __syncthreads();  // LDS is reused for q and tiles below
+  } else {
+    dsc = P.descs[item.x];
+  }
   const int hq0 = h_kv * P.rep + sub * REP;
   const int nvalid_h = min(REP, P.rep - sub * REP);
 
@@ -266,23 +428,6 @@ decode_attn_kernel(DecodeParams P) {
     const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;
     if (lim < (int64_t)t1) t1 = (int)max<int64_t>(lim, (int64_t)t0);
   }
-
-  // Query rows of the group in LDS (zeros for padding heads).
-  for (int i = tid; i < REP * D; i += 64 * NW) {
-    const int r = i / D, d = i % D;
-    if (DT == HALO_F32) {
-      float v = 0.f;
-      if (r < nvalid_h)
-        v = reinterpret_cast<const float*>(P.q)[b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h + d];
-      reinterpret_cast<float*>(s_q)[i] = v;
-    } else {
-      uint16_t v = 0;
-      if (r < nvalid_h)
-        v = reinterpret_cast<const uint16_t*>(P.q)[b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h + d];
-      reinterpret_cast<uint16_t*>(s_q)[i] = v;
-    }
-  }
-  __syncthreads();
 
   const char* kbase = reinterpret_cast<const char*>(dsc.k) +
                       ((dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h) * E::size;
@@ -315,16 +460,47 @@ decode_attn_kernel(DecodeParams P) {
   const int rb = lane % LPH;                // its first row
   const int voff0 = my_row0 * 0 + my_col * 16;
 
-  for (int tb = ws; tb < we; tb += TILE) {
-    const int nrows = min(TILE, we - tb);
-    // Rows past the slice read as zeros (hardware range check of the buffer).
+  // Tile loads: rows past the slice read as zeros (hardware range check).
+  uint4 kreg[PPL], vreg[PPL];
+  auto load_k = [&](int tb) {
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
-    uint4 kreg[PPL], vreg[PPL];
 #pragma unroll
     for (int i = 0; i < PPL; ++i) kreg[i] = buf_ld16(rk, (int)((i * RPI + my_row0) * kst) + voff0);
+  };
+  auto load_v = [&](int tb) {
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
 #pragma unroll
     for (int i = 0; i < PPL; ++i) vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
+  };
+  for (int tb = ws; tb < we; tb += TILE) {
+    const int nrows = min(TILE, we - tb);
+    load_k(tb);
+    load_v(tb);
+    if (tb == ws) {
+      // This wave's copy of the group's query rows (zeros for padding
+      // heads), fetched while the first tile's K/V loads are in flight.
+      if (P.q_aligned) {
+        for (int pc = lane; pc < REP * SL; pc += kWave) {
+          const int r = pc / SL, c = pc % SL;
+          uint4 v = make_uint4(0, 0, 0, 0);
+          if (r < nvalid_h)
+            v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(P.q) +
+                                                (b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h) * E::size +
+                                                c * 16);
+          *reinterpret_cast<uint4*>(s_q + pc * 16) = v;
+        }
+      } else {
+        for (int i = lane; i < REP * D; i += kWave) {
+          const int r = i / D, d = i % D;
+          const int64_t qi = b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h + d;
+          if (DT == HALO_F32) {
+            reinterpret_cast<float*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const float*>(P.q)[qi] : 0.f;
+          } else {
+            reinterpret_cast<uint16_t*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const uint16_t*>(P.q)[qi] : 0;
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < PPL; ++i)
       *reinterpret_cast<uint4*>(kl + (i * RPI + my_row0) * KROW + my_col * 16) = kreg[i];
@@ -454,147 +630,105 @@ decode_attn_kernel(DecodeParams P) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per query-head group combines the group's work-item
-// partials (in work order, so results are deterministic) with the caller's
-// accumulators and writes (m,l,o) and/or (out, lse).  Every load is issued
-// before its value is needed: the (m, l) of up to PB partials are staged
-// through LDS in one parallel pass and each thread streams a fixed float4
-// column of the o partials with independent loads.
+// Merge: one workgroup per (query-head group, head) combines that head's
+// partials over the group's work items with the caller's accumulators and
+// writes (m,l,o) and/or (out, lse).  Thread t owns float4 column t % C4 and
+// the partials p = t / C4 + k * TPC; it merges them online (its own running
+// max), so every load is independent and the whole merge costs one memory
+// round trip; the TPC per-thread results are then combined in a fixed order
+// through LDS (deterministic run to run).
 // ---------------------------------------------------------------------------
 template <int D, int REP>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
   constexpr int NT = 256;
-  constexpr int NW = NT / 64;
-  constexpr int PB = 128;
-  constexpr int C4 = REP * D / 4;
-  constexpr int TPC = C4 >= NT ? 1 : NT / C4;
-  constexpr int CPT = C4 >= NT ? C4 / NT : 1;
-  __shared__ float s_pm[PB * REP], s_pl[PB * REP], s_pw[PB * REP];
-  __shared__ float4 s_red[NT];
-  __shared__ float s_M[REP], s_L[REP], s_accm[REP], s_accl[REP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int C4 = D / 4;           // float4 columns of one head
+  constexpr int TPC = NT / C4;        // threads sharing a column
+  __shared__ float4 s_o[NT];
+  __shared__ float s_m[NT], s_l[NT];
+  const int tid = threadIdx.x;
   const int g = blockIdx.x;
+  const int r = blockIdx.y;
   const int sub = g % P.n_sub;
   const int bh = g / P.n_sub;
   const int h_kv = bh % P.H_kv;
   const int b = bh / P.H_kv;
   const int hq0 = h_kv * P.rep + sub * REP;
-  const int nvalid_h = min(REP, P.rep - sub * REP);
+  if (r >= min(REP, P.rep - sub * REP)) return;  // padding head
+  const int hq = hq0 + r;
   const int gbeg = P.group_offsets[g], gend = P.group_offsets[g + 1];
   const int np = gend - gbeg;
-  const int64_t ml0 = (int64_t)gbeg * REP * 2;
   const bool has_acc = P.m != nullptr;
   const bool merge_in = has_acc && (P.acc_mode & 1);
   const bool write_acc = has_acc && (P.acc_mode & 2);
+  const int64_t aidx = (int64_t)b * P.acc_stride_b + hq;
+  const int col = tid % C4, phase = tid / C4;
 
-  if (tid < REP) {
-    const int r = tid;
-    float am = -INFINITY, al = 0.f;
-    if (merge_in && r < nvalid_h) {
-      const int64_t a = (int64_t)b * P.acc_stride_b + hq0 + r;
-      am = P.m[a] * kLog2e;
-      al = P.l[a];
-    }
-    s_accm[r] = am;
-    s_accl[r] = al;
-    s_M[r] = am;
-    s_L[r] = 0.f;
+  float mt = -INFINITY, lt = 0.f;
+  float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4 + col;
+  const float* wml = P.ws_ml + ((int64_t)gbeg * REP + r) * 2;
+#pragma unroll 4
+  for (int pp = phase; pp < np; pp += TPC) {
+    const float mp = wml[(int64_t)pp * REP * 2];
+    const float lp = wml[(int64_t)pp * REP * 2 + 1];
+    const float4 op = wo4[(int64_t)pp * REP * C4];
+    const float mn = fmaxf(mt, mp);
+    const float ms = (mn == -INFINITY) ? 0.f : mn;
+    const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(mp - ms);
+    lt = lt * a + lp * c;
+    ot.x = ot.x * a + op.x * c;
+    ot.y = ot.y * a + op.y * c;
+    ot.z = ot.z * a + op.z * c;
+    ot.w = ot.w * a + op.w * c;
+    mt = mn;
   }
+  // The incoming accumulator is read by every thread before the barrier:
+  // the column-0 thread overwrites m/l after it.
+  const float am = merge_in ? P.m[aidx] * kLog2e : -INFINITY;
+  const float al = merge_in ? P.l[aidx] : 0.f;
+  s_m[tid] = mt;
+  s_l[tid] = lt;
+  s_o[tid] = ot;
   __syncthreads();
-  for (int base = 0; base < np; base += PB) {
-    const int nb = min(PB, np - base);
-    for (int i = tid; i < nb * REP; i += NT) s_pm[i] = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2];
-    __syncthreads();
-    for (int r = wave; r < REP; r += NW) {
-      float mx = -INFINITY;
-      for (int pp = lane; pp < nb; pp += 64) mx = fmaxf(mx, s_pm[pp * REP + r]);
-      mx = wave_max(mx);
-      if (lane == 0) s_M[r] = fmaxf(s_M[r], mx);
-    }
-    __syncthreads();
-  }
-  const int phase = C4 >= NT ? 0 : tid / C4;
-  float4 acc4[CPT];
-#pragma unroll
-  for (int k = 0; k < CPT; ++k) acc4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int base = 0; base < np; base += PB) {
-    const int nb = min(PB, np - base);
-    for (int i = tid; i < nb * REP; i += NT) {
-      const float mv = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2];
-      const float Mr = s_M[i % REP];
-      s_pw[i] = __builtin_amdgcn_exp2f(mv - (Mr == -INFINITY ? 0.f : Mr));
-      s_pl[i] = P.ws_ml[ml0 + ((int64_t)base * REP + i) * 2 + 1];
-    }
-    __syncthreads();
-    for (int r = wave; r < REP; r += NW) {
-      float ls = 0.f;
-      for (int pp = lane; pp < nb; pp += 64) ls += s_pw[pp * REP + r] * s_pl[pp * REP + r];
-      ls = wave_sum(ls);
-      if (lane == 0) s_L[r] += ls;
-    }
-    const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o + (int64_t)(gbeg + base) * REP * D);
-#pragma unroll 8
-    for (int pp = phase; pp < nb; pp += TPC) {
-#pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int c = C4 >= NT ? tid + k * NT : tid % C4;
-        const float w = s_pw[pp * REP + (c * 4) / D];
-        const float4 v = wo4[(int64_t)pp * C4 + c];
-        acc4[k].x += w * v.x;
-        acc4[k].y += w * v.y;
-        acc4[k].z += w * v.z;
-        acc4[k].w += w * v.w;
-      }
-    }
-    __syncthreads();
-  }
-  if (TPC > 1) {
-    s_red[tid] = acc4[0];
-    __syncthreads();
-    if (phase == 0) {
-      for (int ph = 1; ph < TPC; ++ph) {
-        const float4 v = s_red[ph * C4 + tid];
-        acc4[0].x += v.x;
-        acc4[0].y += v.y;
-        acc4[0].z += v.z;
-        acc4[0].w += v.w;
-      }
-    }
-  }
   if (phase != 0) return;
+  // combine the TPC partial merges of this column in phase order
+  float M = am;
+  for (int ph = 0; ph < TPC; ++ph) M = fmaxf(M, s_m[ph * C4 + col]);
+  const float Ms = (M == -INFINITY) ? 0.f : M;
+  float lsum = 0.f;
+  float o4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int ph = 0; ph < TPC; ++ph) {
+    const float w = __builtin_amdgcn_exp2f(s_m[ph * C4 + col] - Ms);
+    const float4 v = s_o[ph * C4 + col];
+    lsum += w * s_l[ph * C4 + col];
+    o4[0] += w * v.x;
+    o4[1] += w * v.y;
+    o4[2] += w * v.z;
+    o4[3] += w * v.w;
+  }
+  const int d0 = col * 4;
+  const int64_t obase = aidx * D + d0;
+  if (merge_in) {
+    const float w = __builtin_amdgcn_exp2f(am - Ms);
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) {
-    const int c = C4 >= NT ? tid + k * NT : tid;
-    const int r = (c * 4) / D, d0 = (c * 4) % D;
-    if (r >= nvalid_h) continue;
-    const int hq = hq0 + r;
-    const float M = s_M[r];
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    float lsum = s_L[r];
-    float o4[4] = {acc4[k].x, acc4[k].y, acc4[k].z, acc4[k].w};
-    const int64_t obase = ((int64_t)b * P.acc_stride_b + hq) * D + d0;
-    if (merge_in) {
-      const float w = __builtin_amdgcn_exp2f(s_accm[r] - Ms);
+    for (int e = 0; e < 4; ++e) o4[e] += w * P.o[obase + e];
+    lsum += w * al;
+  }
+  if (write_acc) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] += w * P.o[obase + e];
-      lsum += w * s_accl[r];
-    }
+    for (int e = 0; e < 4; ++e) P.o[obase + e] = o4[e];
+  }
+  if (P.out != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      store_elem(P.out, ((int64_t)b * P.H + hq) * D + d0 + e, P.out_dtype, lsum > 0.f ? o4[e] / lsum : 0.f);
+  }
+  if (d0 == 0) {
+    if (P.lse != nullptr) P.lse[(int64_t)b * P.H + hq] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
     if (write_acc) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) P.o[obase + e] = o4[e];
-      if (d0 == 0) {
-        const int64_t a = (int64_t)b * P.acc_stride_b + hq;
-        P.m[a] = (M == -INFINITY) ? -INFINITY : M * kLn2;
-        P.l[a] = lsum;
-      }
+      P.m[aidx] = (M == -INFINITY) ? -INFINITY : M * kLn2;
+      P.l[aidx] = lsum;
     }
-    if (P.out != nullptr) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        store_elem(P.out, ((int64_t)b * P.H + hq) * D + d0 + e, P.out_dtype, lsum > 0.f ? o4[e] / lsum : 0.f);
-    }
-    if (P.lse != nullptr && d0 == 0)
-      P.lse[(int64_t)b * P.H + hq] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
   }
 }
 
@@ -654,7 +788,7 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
   hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem), 0,
                      st, p);
   HALO_CHECK_HIP(hipGetLastError());
-  hipLaunchKernelGGL((decode_merge_kernel<D, REP>), dim3(n_groups), dim3(256), 0, st, mp);
+  hipLaunchKernelGGL((decode_merge_kernel<D, REP>), dim3(n_groups, REP), dim3(256), 0, st, mp);
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
@@ -686,15 +820,13 @@ int dispatch_d(const DecodeParams& p, const MergeParams& mp, int D, int rep_t, i
 
 }  // namespace
 
-extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
-                                int B, int H, int H_kv, int D, int rep_t,
-                                const halo_chunk_desc* descs, int n_desc,
-                                const int32_t* work, int n_work,
-                                const int32_t* group_offsets, int n_groups,
-                                const int64_t* q_pos, float scale,
-                                float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
-                                void* out, int out_dtype, float* lse,
-                                void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype, int B, int H, int H_kv, int D,
+                int rep_t, const halo_chunk_desc* descs, int n_desc, const int32_t* work, int n_work,
+                const int32_t* group_offsets, int n_groups, const int64_t* q_pos, float scale, float* m, float* l,
+                float* o, int64_t acc_stride_b, int acc_mode, void* out, int out_dtype, float* lse, void* workspace,
+                size_t workspace_bytes, const halo_select_cfg* sel, void* stream) {
   HALO_CHECK_ARG(q && descs && work && group_offsets, "null pointer argument");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0, "need H % H_kv == 0 and positive sizes");
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
@@ -716,6 +848,7 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
   p.q = q;
   p.q_stride_b = q_stride_b;
   p.q_stride_h = q_stride_h;
+  p.B = B;
   p.H = H;
   p.H_kv = H_kv;
   p.rep = rep;
@@ -724,8 +857,32 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
   p.work = work;
   p.q_pos = q_pos;
   p.scale2 = (float)((double)scale * 1.4426950408889634);
+  {
+    const int esz = elem_size(dtype);
+    p.q_aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && (q_stride_h * esz) % 16 == 0 &&
+                  (q_stride_b * esz) % 16 == 0 && (D * esz) % 16 == 0;
+  }
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + (size_t)n_work * rep_t * D;
+  p.inv_rep = 1.0f / (float)rep;
+  p.sel_on = sel != nullptr;
+  p.sel = {};
+  if (sel) {
+    const halo_select_cfg& S = *sel;
+    const int esz = elem_size(dtype);
+    const int rows = S.per_row ? 1 : B;
+    HALO_CHECK_ARG(S.kmean && S.catalog, "selection needs kmean and catalog");
+    HALO_CHECK_ARG(S.n_cold >= 1 && S.n_cold <= kSelMaxCold, "n_cold must be in [1, 128]");
+    HALO_CHECK_ARG(S.top_k >= 1 && S.slot0 >= 0 && S.slot0 + S.top_k <= n_desc,
+                   "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
+    HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");
+    HALO_CHECK_ARG(S.n_cold * rows * H_kv <= 256, "n_cold * rows * H_kv must be <= 256");
+    HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
+    HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(S.kmean) % 16 == 0 && (S.km_stride_b * esz) % 16 == 0 &&
+                       (S.km_stride_h * esz) % 16 == 0 && (S.km_stride_p * esz) % 16 == 0,
+                   "kmean rows must be 16-byte aligned");
+    p.sel = S;
+  }
   MergeParams mp;
   mp.group_offsets = group_offsets;
   mp.H = H;
@@ -748,6 +905,38 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
     case HALO_BF16: return dispatch_d<HALO_BF16>(p, mp, D, rep_t, n_work, n_groups, st);
     default: return dispatch_d<HALO_F16>(p, mp, D, rep_t, n_work, n_groups, st);
   }
+}
+
+}  // namespace
+
+extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                int B, int H, int H_kv, int D, int rep_t,
+                                const halo_chunk_desc* descs, int n_desc,
+                                const int32_t* work, int n_work,
+                                const int32_t* group_offsets, int n_groups,
+                                const int64_t* q_pos, float scale,
+                                float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                                void* out, int out_dtype, float* lse,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
+                     group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
+                     workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int halo_decode_attn_tiered(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                       int B, int H, int H_kv, int D, int rep_t,
+                                       const halo_chunk_desc* descs, int n_desc,
+                                       const int32_t* work, int n_work,
+                                       const int32_t* group_offsets, int n_groups,
+                                       const int64_t* q_pos, float scale,
+                                       float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                                       void* out, int out_dtype, float* lse,
+                                       void* workspace, size_t workspace_bytes,
+                                       const halo_select_cfg* sel, void* stream) {
+  HALO_CHECK_ARG(sel != nullptr, "selection config is null");
+  return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
+                     group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
+                     workspace, workspace_bytes, sel, stream);
 }
 
 extern "C" int halo_finalize(const float* m, const float* l, const float* o, int B, int H, int D,

@@ -16,22 +16,65 @@
 namespace halo {
 
 // ---------------------------------------------------------------------------
-// Page means: kmean[b,h,j,d] = dtype(sum_t K[b,h,row0+j*page+t,d] / page),
-// summed in fp32 in row order and rounded once to the storage dtype.
-// One workgroup per (b, h, page); threads walk the head dim (coalesced rows).
+// Page means: kmean[b,h,j,d] = dtype(sum_t K[b,h,row0+j*page+t,d] / page).
+// One workgroup per (b, h, page).  Thread t owns the 16-byte piece
+// t % SL of rows t/SL, t/SL + RG, ... (RG = 256/SL row groups), so loads are
+// whole coalesced rows and independent; the RG fp32 partial sums are then
+// added in row-group order through LDS and rounded once to the key dtype.
 // ---------------------------------------------------------------------------
-__global__ void chunk_means_kernel(const void* k, int64_t ksb, int64_t ksh, int64_t kst, int dtype,
-                                   int H_kv, int D, int64_t row0, int page, int n_pages,
-                                   void* km, int64_t msb, int64_t msh, int64_t msp) {
+template <int DT>
+__global__ void __launch_bounds__(256) chunk_means_kernel(const void* k, int64_t ksb, int64_t ksh, int64_t kst,
+                                                          int H_kv, int D, int64_t row0, int page, int n_pages,
+                                                          void* km, int64_t msb, int64_t msh, int64_t msp) {
+  constexpr int ESZ = DT == HALO_F32 ? 4 : 2;
+  constexpr int EPC = 16 / ESZ;
+  __shared__ float s_part[256 * 8];
   const int j = blockIdx.x % n_pages;
   const int bh = blockIdx.x / n_pages;
   const int h = bh % H_kv, b = bh / H_kv;
-  const int64_t base = (int64_t)b * ksb + (int64_t)h * ksh + (row0 + (int64_t)j * page) * kst;
+  const int SL = D / EPC;
+  const int RG = 256 / SL;
+  const int tid = threadIdx.x;
+  const int col = tid % SL, rg = tid / SL;
+  float acc[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+  if (rg < RG) {
+    const char* base = reinterpret_cast<const char*>(k) +
+                       ((int64_t)b * ksb + (int64_t)h * ksh + (row0 + (int64_t)j * page) * kst) * ESZ + col * 16;
+#pragma unroll 8
+    for (int t = rg; t < page; t += RG) {
+      const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)t * kst * ESZ);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      if constexpr (DT == HALO_F32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += __uint_as_float(w[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float lo, hi;
+          if constexpr (DT == HALO_BF16) {
+            lo = bf16_lo(w[e]);
+            hi = bf16_hi(w[e]);
+          } else {
+            lo = f16_bits_to_f32((uint16_t)(w[e] & 0xffffu));
+            hi = f16_bits_to_f32((uint16_t)(w[e] >> 16));
+          }
+          acc[2 * e] += lo;
+          acc[2 * e + 1] += hi;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) s_part[tid * 8 + e] = acc[e];
+  __syncthreads();
   const float inv = 1.0f / (float)page;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float acc = 0.f;
-    for (int t = 0; t < page; ++t) acc += load_elem(k, base + (int64_t)t * kst + d, dtype);
-    store_elem(km, (int64_t)b * msb + (int64_t)h * msh + (int64_t)j * msp + d, dtype, acc * inv);
+  for (int d = tid; d < D; d += 256) {
+    const int c = d / EPC, e = d % EPC;
+    float sum = 0.f;
+    for (int g = 0; g < RG; ++g) sum += s_part[(g * SL + c) * 8 + e];
+    store_elem(km, (int64_t)b * msb + (int64_t)h * msh + (int64_t)j * msp + d, DT, sum * inv);
   }
 }
 
@@ -44,6 +87,7 @@ struct ScoreParams {
   int64_t qsb, qsh;
   int dtype;
   int B, H, H_kv, D, rep;
+  float inv_rep;  // fp32(1/rep), rounded on the host: torch's mean factor
   const void* km;
   int64_t msb, msh, msp;
   const int32_t* elig;
@@ -76,6 +120,7 @@ __device__ __forceinline__ bool beats(float sa, int ea, float sb, int eb) {
   return sa > sb || (sa == sb && ea < eb);
 }
 
+template <int DT>
 __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
   __shared__ float s_qg[kMaxQg];
   __shared__ float s_score[kMaxElig];
@@ -101,14 +146,14 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
     const int64_t qb = (int64_t)(b0 + r) * P.qsb;
     float v;
     if (P.rep == 1) {
-      v = load_elem(P.q, qb + (int64_t)h * P.qsh + d, P.dtype);
+      v = load_elem(P.q, qb + (int64_t)h * P.qsh + d, DT);
     } else {
       float acc = 0.f;
-      for (int j = 0; j < P.rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * P.rep + j) * P.qsh + d, P.dtype);
-      acc = acc * (1.0f / (float)P.rep);
-      v = P.dtype == HALO_F32 ? acc
-          : (P.dtype == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(acc) << 16)
-                                  : f16_bits_to_f32(f32_to_f16_rne(acc)));
+      for (int j = 0; j < P.rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * P.rep + j) * P.qsh + d, DT);
+      acc = opaque(acc * P.inv_rep);  // fp32 product, then one rounding to the q dtype
+      v = DT == HALO_F32 ? acc
+          : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(acc) << 16)
+                             : f16_bits_to_f32(f32_to_f16_rne(acc)));
     }
     s_qg[i] = v;
   }
@@ -122,8 +167,8 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
   // summed in channel order; the max over (row, h) is folded in order.
   const int nrh = nrows * P.H_kv;
   const int triples = n * nrh;
-  const int esz = P.dtype == HALO_F32 ? 4 : 2;
-  const int ep = 16 / esz;
+  constexpr int esz = DT == HALO_F32 ? 4 : 2;
+  constexpr int ep = 16 / esz;
   for (int i = tid; i < n; i += nthr) s_score[i] = -INFINITY;
   for (int t0 = 0; t0 < triples; t0 += kMaxDots) {
     const int nt = min(kMaxDots, triples - t0);
@@ -139,10 +184,10 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
       for (int c = 0; c < P.D / ep; ++c) {
         const uint4 v = *reinterpret_cast<const uint4*>(row + c * 16);
         float f[8];
-        if (P.dtype == HALO_F32) {
+        if constexpr (DT == HALO_F32) {
           f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
           f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
-        } else if (P.dtype == HALO_BF16) {
+        } else if constexpr (DT == HALO_BF16) {
           f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
           f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
         } else {
@@ -153,6 +198,7 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
             f[2 * e + 1] = f16_bits_to_f32((uint16_t)(w[e] >> 16));
           }
         }
+#pragma unroll
         for (int e = 0; e < ep; ++e) acc = __fadd_rn(acc, __fmul_rn(qg[c * ep + e], f[e]));
       }
       s_dot[t] = acc;
@@ -263,10 +309,21 @@ extern "C" int halo_chunk_means(const void* k, int64_t k_stride_b, int64_t k_str
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
   HALO_CHECK_ARG(B > 0 && H_kv > 0 && D > 0 && page > 0 && n_pages >= 0 && row0 >= 0, "bad sizes");
   if (n_pages == 0) return HALO_OK;
+  HALO_CHECK_ARG(D % (dtype == HALO_F32 ? 4 : 8) == 0 && D <= 256 * (dtype == HALO_F32 ? 4 : 8),
+                 "head dim must fill whole 16-byte pieces");
+  HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(k) % 16 == 0 && (k_stride_t * elem_size(dtype)) % 16 == 0 &&
+                 (k_stride_h * elem_size(dtype)) % 16 == 0 && (k_stride_b * elem_size(dtype)) % 16 == 0,
+                 "key rows must be 16-byte aligned");
   const int64_t blocks = (int64_t)B * H_kv * n_pages;
-  hipLaunchKernelGGL(chunk_means_kernel, dim3((unsigned)blocks), dim3(D >= 256 ? 256 : 128), 0,
-                     reinterpret_cast<hipStream_t>(stream), k, k_stride_b, k_stride_h, k_stride_t, dtype,
-                     H_kv, D, row0, page, n_pages, kmean, km_stride_b, km_stride_h, km_stride_p);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define HALO_MEANS(DTV)                                                                                  \
+  hipLaunchKernelGGL(chunk_means_kernel<DTV>, dim3((unsigned)blocks), dim3(256), 0, st, k, k_stride_b,   \
+                     k_stride_h, k_stride_t, H_kv, D, row0, page, n_pages, kmean, km_stride_b, km_stride_h, \
+                     km_stride_p)
+  if (dtype == HALO_F32) HALO_MEANS(HALO_F32);
+  else if (dtype == HALO_BF16) HALO_MEANS(HALO_BF16);
+  else HALO_MEANS(HALO_F16);
+#undef HALO_MEANS
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
@@ -307,6 +364,7 @@ extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t 
   p.H_kv = H_kv;
   p.D = D;
   p.rep = H / H_kv;
+  p.inv_rep = (float)(1.0 / (double)p.rep);
   p.km = kmean;
   p.msb = km_stride_b;
   p.msh = km_stride_h;
@@ -333,7 +391,10 @@ extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t 
   p.P_total = P_total;
   HALO_CHECK_ARG(!normalize || P_total > 0, "P_total must be positive when normalising");
   const int n_sel = per_row ? B : 1;
-  hipLaunchKernelGGL(score_topk_kernel, dim3(n_sel), dim3(512), 0, reinterpret_cast<hipStream_t>(stream), p);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == HALO_F32) hipLaunchKernelGGL(score_topk_kernel<HALO_F32>, dim3(n_sel), dim3(512), 0, st, p);
+  else if (dtype == HALO_BF16) hipLaunchKernelGGL(score_topk_kernel<HALO_BF16>, dim3(n_sel), dim3(512), 0, st, p);
+  else hipLaunchKernelGGL(score_topk_kernel<HALO_F16>, dim3(n_sel), dim3(512), 0, st, p);
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }

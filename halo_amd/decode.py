@@ -13,6 +13,7 @@ per-launch arguments of ``update_chunk`` (halo/triton_chunked.py:151-192).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -258,8 +259,11 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
            m: Optional[torch.Tensor] = None, l: Optional[torch.Tensor] = None,
            o: Optional[torch.Tensor] = None, acc_mode: int = 0,
            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-           stream: Optional[torch.cuda.Stream] = None) -> None:
-    """Enqueue one ``halo_decode_attn`` on ``stream`` (default: current)."""
+           stream: Optional[torch.cuda.Stream] = None, select=None) -> None:
+    """Enqueue one ``halo_decode_attn`` on ``stream`` (default: current).
+
+    ``select`` (a ``_native.SelectCfg``) enqueues ``halo_decode_attn_tiered``
+    instead: the table's selection slots choose their chunks in-kernel."""
     L = nat.lib()
     if q.dim() != 3 or tuple(q.shape) != (plan.B, plan.H, plan.D):
         raise AssertionError(f"expected q (B, H, D) = {(plan.B, plan.H, plan.D)}, got {tuple(q.shape)}")
@@ -293,7 +297,7 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
     sp = nat.stream_ptr(stream)
     nbytes = int(L.halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
     ws = workspace(q.device, sp, nbytes)
-    status = L.halo_decode_attn(
+    args = (
         q.data_ptr(), q.stride(0), q.stride(1), nat.dtype_code(plan.dtype),
         plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t,
         plan.descs.data_ptr(), plan.n_desc,
@@ -302,6 +306,9 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         nat.ptr(q_pos), float(scale),
         nat.ptr(m), nat.ptr(l), nat.ptr(o), plan.H, acc_mode,
         nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse),
-        ws.data_ptr(), ws.numel(), sp,
+        ws.data_ptr(), ws.numel(),
     )
-    nat.check(status, "halo_decode_attn")
+    if select is None:
+        nat.check(L.halo_decode_attn(*args, sp), "halo_decode_attn")
+    else:
+        nat.check(L.halo_decode_attn_tiered(*args, ctypes.byref(select), sp), "halo_decode_attn_tiered")

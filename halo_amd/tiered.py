@@ -1,14 +1,16 @@
 """One decode layer over a tiered chunk table: hot chunks plus the top-k cold
 chunks a scorer picks each step.
 
-Per step this enqueues two kernels on the current stream and nothing else:
-  1. ``halo_chunk_score_topk`` scores the cold chunks' page-mean keys against
-     the query and copies the chosen chunks' descriptors into the table's
-     ``top_k`` selection slots;
-  2. ``halo_decode_attn`` attends the hot chunks and the selection slots with
-     the fused log-sum-exp merge, writing (out, lse).
-There is no host round trip between the two, so a whole multi-layer decode
-step can be captured in one HIP graph.
+Per step (fused mode, the default) this enqueues one
+``halo_decode_attn_tiered`` on the current stream: the workgroups of the
+``top_k`` selection slots score the cold chunks' page-mean keys against the
+query, take the chosen chunks' descriptors from the catalog and attend them,
+while the other workgroups attend the hot chunks; the split-K merge kernel
+then writes (out, lse).  Unfused mode (``fused=False``, or shapes beyond the
+in-kernel selection limits) enqueues ``halo_chunk_score_topk`` (which copies
+the chosen descriptors into the table's slots) followed by
+``halo_decode_attn``.  Either way there is no host round trip, so a whole
+multi-layer decode step can be captured in one HIP graph.
 
 Reference: the Path-D placement loop -- a page scorer picks which pages stay
 hot (halo/kv_cache_chunked.py:416-457 with baselines/scorer_ablations.py:
@@ -24,24 +26,39 @@ from typing import Optional, Sequence
 
 import torch
 
+from . import _native as nat
 from .chunk_scorer import chunk_means, score_topk
 from .decode import ChunkRef, DecodePlan, build_plan, descs_to_device, launch, pack_descs
+
+# In-kernel selection limits of halo_decode_attn_tiered (include/halo_hip.h).
+_SEL_MAX_COLD = 128
+_SEL_MAX_TRIPLES = 256
+_SEL_MAX_QBAR = 2048
 
 
 class TieredDecodeLayer:
     def __init__(self, *, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                  hot: Sequence[ChunkRef], cold: Sequence[ChunkRef], top_k: int, device,
-                 cold_kmean: Optional[torch.Tensor] = None, split: Optional[int] = None) -> None:
-        if top_k > len(cold):
-            raise AssertionError(f"top_k={top_k} > {len(cold)} cold chunks")
+                 cold_kmean: Optional[torch.Tensor] = None, split: Optional[int] = None,
+                 fused: bool = True) -> None:
+        if not 1 <= top_k <= len(cold):
+            raise AssertionError(f"top_k={top_k} must be in [1, {len(cold)} cold chunks]")
         self.B, self.H, self.H_kv, self.D, self.dtype = B, H, H_kv, D, dtype
         self.n_hot, self.top_k = len(hot), top_k
         self.hot, self.cold = list(hot), list(cold)
-        # Selection slots start as placeholders (the first cold chunks); the
-        # scorer overwrites them on the device every step.
-        slots = [cold[i] for i in range(top_k)]
+        n_cold = len(cold)
+        self.fused = bool(fused) and n_cold <= _SEL_MAX_COLD and n_cold * B * H_kv <= _SEL_MAX_TRIPLES \
+            and B * H_kv * D <= _SEL_MAX_QBAR
+        # Selection slots come first in the table (their workgroups are
+        # dispatched first, which hides the selection work behind the hot
+        # chunks).  Each slot is planned over the largest cold chunk, so its
+        # work items cover whichever chunk is chosen; the unfused scorer
+        # overwrites the slot descriptors on the device every step.
+        widest = max(range(n_cold), key=lambda i: cold[i].T)
+        slots = [cold[widest]] * top_k
+        self.slot0 = 0
         self.plan: DecodePlan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype,
-                                           chunks=list(hot) + slots, device=device, split=split)
+                                           chunks=slots + list(hot), device=device, split=split)
         cat, keep = pack_descs(cold, B=B, H_kv=H_kv, D=D, dtype=dtype)
         self.catalog = descs_to_device(cat, device)
         self.plan.keep += keep
@@ -51,6 +68,16 @@ class TieredDecodeLayer:
         self.kmean = cold_kmean
         self.idx = torch.empty((1, top_k), device=device, dtype=torch.int32)
         self.scores = torch.empty((1, max(len(cold), 1)), device=device, dtype=torch.float32)
+        self.select_cfg = None
+        if self.fused:
+            km = self.kmean
+            if km.shape != (B, H_kv, n_cold, D) or km.dtype != dtype or km.stride(-1) != 1:
+                raise AssertionError(f"cold_kmean must be ({B}, {H_kv}, {n_cold}, {D}) {dtype} with unit stride")
+            self.select_cfg = nat.SelectCfg(
+                kmean=km.data_ptr(), km_stride_b=km.stride(0), km_stride_h=km.stride(1), km_stride_p=km.stride(2),
+                catalog=self.catalog.data_ptr(), catalog_stride=n_cold, n_cold_per_sel=None,
+                n_cold=n_cold, top_k=top_k, slot0=self.slot0, per_row=0,
+                idx_out=self.idx.data_ptr(), score_out=self.scores.data_ptr())
 
     def build_means(self, cold: Sequence[ChunkRef]) -> torch.Tensor:
         """One mean key per cold chunk (B, H_kv, n_cold, D)."""
@@ -66,14 +93,21 @@ class TieredDecodeLayer:
         return sum(c.T for c in self.hot) + self.top_k * per
 
     def select(self, q: torch.Tensor) -> None:
+        """Standalone selection (``halo_chunk_score_topk``): fills idx/scores
+        and the table's selection slots."""
         score_topk(q, self.kmean, self.eligible, self.top_k, catalog=self.catalog,
-                   table=self.plan.descs, table_slot0=self.n_hot, idx_out=self.idx, score_out=self.scores)
+                   table=self.plan.descs, table_slot0=self.slot0, idx_out=self.idx, score_out=self.scores)
 
     def attend(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse: Optional[torch.Tensor] = None,
                q_pos: Optional[torch.Tensor] = None) -> None:
+        """Attention over the table as it stands (slots as last selected)."""
         launch(self.plan, q, scale=scale, q_pos=q_pos, out=out, lse=lse)
 
     def step(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse: Optional[torch.Tensor] = None,
              q_pos: Optional[torch.Tensor] = None) -> None:
+        if self.fused:
+            launch(self.plan, q, scale=scale, q_pos=q_pos, out=out, lse=lse, select=self.select_cfg)
+            return
         self.select(q)
         self.attend(q, scale=scale, out=out, lse=lse, q_pos=q_pos)
+

@@ -110,6 +110,50 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * In-kernel chunk selection for halo_decode_attn_tiered.  Work items whose
+ * descriptor index d lies in [slot0, slot0 + top_k) are selection slots:
+ * their workgroup scores the cold chunks catalog[s*catalog_stride + p],
+ * p < n_cold (or n_cold_per_sel[s]), with the alpha-only mean-key score of
+ * halo_chunk_score_topk (raw q.Kbar, max over rows and KV heads; selection s
+ * is batch row s when per_row != 0, else all rows) and attends the
+ * (d - slot0)-th chosen chunk in ascending index order (top-k order: score
+ * descending, then index ascending); a slot past the number of eligible
+ * chunks attends nothing.  idx_out[s*top_k + j] / score_out[s*n_cold + p]
+ * receive the selection when non-NULL.  Limits: n_cold <= 128,
+ * n_cold * rows * H_kv <= 256 and rows * H_kv * D <= 2048 per selection
+ * (rows = 1 when per_row).  The work items of a slot must cover as many rows
+ * as the largest catalog chunk (rows past a chunk's T_c are skipped).
+ */
+typedef struct halo_select_cfg {
+  const void* kmean; /* (B|1, H_kv, n_cold, D) page means, K dtype, rows 16-byte aligned */
+  int64_t km_stride_b, km_stride_h, km_stride_p;
+  const halo_chunk_desc* catalog;
+  int64_t catalog_stride;
+  const int32_t* n_cold_per_sel; /* NULL: n_cold for every selection */
+  int32_t n_cold, top_k, slot0, per_row;
+  int32_t* idx_out;
+  float* score_out;
+} halo_select_cfg;
+
+/*
+ * halo_decode_attn with the chunk selection fused in (sel != NULL), so a
+ * decode layer over hot + scorer-chosen cold chunks is one attention launch
+ * plus its merge, with no host round trip.  Replaces the select_hot_pages ->
+ * chunk walk sequence (baselines/scorer_ablations.py:218-268,
+ * halo/kv_cache_chunked.py:416-457, 571-763) for T_q == 1.
+ */
+int halo_decode_attn_tiered(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                            int B, int H, int H_kv, int D, int rep_t,
+                            const halo_chunk_desc* descs, int n_desc,
+                            const int32_t* work, int n_work,
+                            const int32_t* group_offsets, int n_groups,
+                            const int64_t* q_pos, float scale,
+                            float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                            void* out, int out_dtype, float* lse,
+                            void* workspace, size_t workspace_bytes,
+                            const halo_select_cfg* sel, void* stream);
+
+/*
  * finalize: out = o / (l > 0 ? l : 1) cast to out_dtype, optional
  * lse = m + log(l).  Replaces halo/triton_chunked.py:195-207 (which does not
  * return the LSE).  m,l: (B,H) fp32 contiguous, o: (B,H,D) fp32 contiguous.

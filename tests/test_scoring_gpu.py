@@ -105,7 +105,7 @@ def test_per_row_ragged_selection(dev):
         assert idx[b].cpu().tolist() == want
 
 
-def _tiered_from_fixture(cfg, dev):
+def _tiered_from_fixture(cfg, dev, fused=True):
     from halo_amd.decode import ChunkRef
     from halo_amd.tiered import TieredDecodeLayer
     x = decode_inputs(cfg["seed"], B=1, H=cfg["H"], H_kv=cfg["H_kv"], T=cfg["T"], D=cfg["D"], dtype=cfg["dtype"],
@@ -116,16 +116,18 @@ def _tiered_from_fixture(cfg, dev):
     n_cold = n - cfg["n_hot"]
     refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True) for i in range(n)]
     layer = TieredDecodeLayer(B=1, H=cfg["H"], H_kv=cfg["H_kv"], D=cfg["D"], dtype=TDT[cfg["dtype"]],
-                              hot=refs[n_cold:], cold=refs[:n_cold], top_k=cfg["top_k"], device=dev)
+                              hot=refs[n_cold:], cold=refs[:n_cold], top_k=cfg["top_k"], device=dev, fused=fused)
+    assert layer.fused == fused
     return layer, q
 
 
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "two_kernel"])
 @pytest.mark.parametrize("name,cfg", [("c1_decode", C1), ("c2_layer0", C2)])
-def test_tiered_layer_matches_golden(dev, name, cfg):
+def test_tiered_layer_matches_golden(dev, name, cfg, fused):
     """Scorer picks the fixture's chunks bit-exactly; attention over hot +
     selected matches the float64 closed form (1e-5 fp32, 2e-2 bf16)."""
     fx = np.load(os.path.join(GOLD, name + ".npz"))
-    layer, q = _tiered_from_fixture(cfg, dev)
+    layer, q = _tiered_from_fixture(cfg, dev, fused)
     out = torch.empty((1, cfg["H"], cfg["D"]), device=dev, dtype=TDT[cfg["dtype"]])
     lse = torch.empty((1, cfg["H"]), device=dev)
     layer.step(q[:, :, 0], scale=1 / math.sqrt(cfg["D"]), out=out, lse=lse)
@@ -137,10 +139,76 @@ def test_tiered_layer_matches_golden(dev, name, cfg):
     np.testing.assert_allclose(layer.scores[0].cpu().numpy(), fx["scores"], rtol=1e-4, atol=1e-5)
 
 
-def test_tiered_layer_in_hip_graph(dev):
-    """The two-kernel step replays from a captured graph; every replay
-    matches the eager result (fresh inputs copied in between replays)."""
-    layer, q = _tiered_from_fixture(C1, dev)
+def test_fused_selection_matches_two_kernel_path(dev):
+    """In-kernel selection and the standalone scorer produce identical
+    indices, scores, outputs and LSEs (same arithmetic, same tie rule)."""
+    scale = 1 / math.sqrt(C2["D"])
+    res = []
+    for fused in (True, False):
+        layer, q = _tiered_from_fixture(C2, dev, fused)
+        out = torch.empty((1, C2["H"], C2["D"]), device=dev, dtype=torch.bfloat16)
+        lse = torch.empty((1, C2["H"]), device=dev)
+        layer.step(q[:, :, 0], scale=scale, out=out, lse=lse)
+        torch.cuda.synchronize()
+        res.append((layer.idx.clone(), layer.scores.clone(), out, lse))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_fused_selection_per_row_ragged(dev, dtype):
+    """halo_decode_attn_tiered with one selection per batch row over a
+    ragged number of eligible chunks; a slot past the eligible count attends
+    nothing and reports -1.  Checked against the oracle's selector and the
+    float64 closed form over hot + selected rows."""
+    from halo_amd import _native as nat
+    from halo_amd.chunk_scorer import chunk_means
+    from halo_amd.decode import ChunkRef, build_plan, descs_to_device, launch, pack_descs
+    B, H, H_kv, D, T, c, top_k = 2, 8, 2, 64, 1024, 128, 3
+    n_el = np.array([5, 2], np.int32)
+    x = decode_inputs(44, B=B, H=H, H_kv=H_kv, T=T, D=D, dtype=dtype, n_planted=2, sigma=4.0)
+    q, k, v = (_gpu(a, dtype, dev) for a in (x.q, x.k, x.v))
+    refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True) for i in range(T // c)]
+    cold, hot = refs[:6], refs[6:]
+    plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=TDT[dtype], chunks=[cold[0]] * top_k + hot, device=dev)
+    cat_np, keep = pack_descs(cold + cold, B=B, H_kv=H_kv, D=D, dtype=TDT[dtype])
+    cat = descs_to_device(cat_np, dev)
+    km = chunk_means(k, c, n_pages=6)
+    n_el_d = torch.from_numpy(n_el).to(dev)
+    idx = torch.full((B, top_k), -7, device=dev, dtype=torch.int32)
+    sc = torch.full((B, 6), -7.0, device=dev)
+    cfg = nat.SelectCfg(kmean=km.data_ptr(), km_stride_b=km.stride(0), km_stride_h=km.stride(1),
+                        km_stride_p=km.stride(2), catalog=cat.data_ptr(), catalog_stride=6,
+                        n_cold_per_sel=n_el_d.data_ptr(), n_cold=6, top_k=top_k, slot0=0, per_row=1,
+                        idx_out=idx.data_ptr(), score_out=sc.data_ptr())
+    out = torch.empty((B, H, D), device=dev)
+    lse = torch.empty((B, H), device=dev)
+    launch(plan, q[:, :, 0], scale=0.125, out=out, lse=lse, select=cfg)
+    torch.cuda.synchronize()
+    km_np = km.float().cpu().numpy()
+    for b in range(B):
+        ref_sc = S.mean_key_scores(x.q[b:b + 1], km_np[b:b + 1], dtype)[: n_el[b]]
+        np.testing.assert_allclose(sc[b, : n_el[b]].cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-5)
+        assert (sc[b, n_el[b]:].cpu().numpy() == -7.0).all()
+        srt = np.sort(ref_sc.astype(np.float64))[::-1]
+        assert len(srt) <= top_k or srt[top_k - 1] - srt[top_k] > 1e-4, "fixture seed lost its margin"
+        want = S.select_chunks(x.q[b:b + 1], km_np[b:b + 1], np.arange(n_el[b]), top_k, dtype).tolist()
+        assert idx[b].cpu().tolist() == want + [-1] * (top_k - len(want))
+        keep_rows = np.zeros(T, bool)
+        keep_rows[6 * c:] = True
+        for j in want:
+            keep_rows[j * c:(j + 1) * c] = True
+        ro, rl = A.attention_f64(x.q[b:b + 1, :, 0], x.k[b:b + 1], x.v[b:b + 1], scale=0.125, keep=keep_rows)
+        tol = 1e-5 if dtype == "float32" else 2e-2
+        assert np.abs(out[b:b + 1].cpu().numpy() - ro).max() <= tol
+        assert np.abs(lse[b:b + 1].cpu().numpy() - rl).max() <= (1e-5 if dtype == "float32" else 1e-3)
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "two_kernel"])
+def test_tiered_layer_in_hip_graph(dev, fused):
+    """The decode step replays from a captured graph; every replay matches
+    the eager result (fresh inputs copied in between replays)."""
+    layer, q = _tiered_from_fixture(C1, dev, fused)
     q3 = q[:, :, 0].contiguous()
     out = torch.empty((1, 8, 64), device=dev)
     lse = torch.empty((1, 8), device=dev)

@@ -38,7 +38,8 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_layers(torch, *, L, H, H_kv, D, T, chunk, n_hot, top_k, n_planted, sigma, dev, seed, split=None):
+def make_layers(torch, *, L, H, H_kv, D, T, chunk, n_hot, top_k, n_planted, sigma, dev, seed, split=None,
+                fused=True):
     import numpy as np
 
     from halo_amd.decode import ChunkRef
@@ -61,7 +62,7 @@ def make_layers(torch, *, L, H, H_kv, D, T, chunk, n_hot, top_k, n_planted, sigm
                 for i in range(n_chunks)]
         layers.append(TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16,
                                         hot=refs[n_cold:], cold=refs[:n_cold], top_k=top_k, device=dev,
-                                        split=split))
+                                        split=split, fused=fused))
         qs.append(q)
         kvs.append((k, v))
     return layers, qs, kvs
@@ -210,6 +211,8 @@ def main() -> int:
     ap.add_argument("--no-pcie", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="select with the standalone scorer kernel instead of in the attention kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not run (how the path shards across "
@@ -226,7 +229,8 @@ def main() -> int:
     scale = 1.0 / math.sqrt(D)
     log(f"building {L} layers of K/V ({L * 2 * H_kv * T * D * 2 / 2**30:.1f} GiB)")
     layers, qs, kvs = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
-                                  n_planted=4, sigma=8.0, dev=dev, seed=1, split=args.split)
+                                  n_planted=4, sigma=8.0, dev=dev, seed=1, split=args.split,
+                                  fused=not args.unfused)
     outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
     lses = [torch.empty((1, H), device=dev, dtype=torch.float32) for _ in range(L)]
 

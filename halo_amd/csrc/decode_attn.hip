@@ -27,12 +27,15 @@
 
 namespace halo {
 
+constexpr int kWorkInts = 8;  // work record: desc, group, t0, t1, partial slot, 3 x pad
+
 struct DecodeParams {
   const void* q;
   int64_t q_stride_b, q_stride_h;
   int B, H, H_kv, rep, n_sub;
   const halo_chunk_desc* descs;
   const int32_t* work;
+  int n_work;
   const int64_t* q_pos;
   float scale2;  // scale * log2(e)
   int q_aligned;  // q rows 16-byte aligned: stage them with 16-byte loads
@@ -164,8 +167,12 @@ __device__ __forceinline__ float head_value(float v, int h) {
   return r;
 }
 
+// K/V rows are read once per launch: non-temporal loads (cache policy NT)
+// keep them from evicting the small, reused data (work list, descriptors,
+// page means, q) out of L2 and the last-level cache.
+constexpr int kCachePolicyNT = 2;
 __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kCachePolicyNT));
 }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
   const int nrec = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes);
@@ -174,6 +181,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, in
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
 
 // o[h][e] += p_a[h] * va[e] + p_b[h] * vb[e] for two rows whose 16-byte
 // pieces are va, vb.  bf16/f16: rows are paired into dot2 operands with
@@ -228,9 +236,11 @@ __device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const 
 // Returns the chunk index for `slot` (-1: slot past the eligible count);
 // the chosen descriptors are left in LDS at s_cat.
 // ---------------------------------------------------------------------------
-constexpr int kSelMaxCold = 128;
+constexpr int kSelMaxCold = 64;
+static_assert(sizeof(halo_chunk_desc) % 8 == 0, "descriptors are copied as 8-byte words");
 constexpr int kSelMaxQbar = 2048;
-constexpr int kSelBytes = kSelMaxQbar * 4 + 4 * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
+constexpr int kSelQbarLds = kSelMaxQbar + 4 * 64;  // padded rows: at most 2048 / 64 rows of +4 floats
+constexpr int kSelBytes = kSelQbarLds * 4 + 4 * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
 
 __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
   halo_chunk_desc u;
@@ -259,7 +269,13 @@ __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d
 template <int DT, int D, int NT>
 __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, bool writer) {
   using E = Elem<DT>;
-  constexpr int PIECES = D * E::size / 16;
+  constexpr int EP = E::per16;
+  constexpr int PIECES = D / EP;                               // 16-byte pieces per row
+  constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
+  constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
+  constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
+  constexpr int QB = 8;                                        // query heads summed per load batch
+  constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
   const halo_select_cfg& S = P.sel;
   const int tid = threadIdx.x;
   const int rows = S.per_row ? 1 : P.B;
@@ -270,14 +286,14 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
   const int H_kv = P.H_kv, rep = P.rep;
   const int nrh = rows * H_kv;
   const int triples = n * nrh;
-  float* s_qbar = reinterpret_cast<float*>(smem);
-  float* s_dot = s_qbar + kSelMaxQbar;
-  float* s_score = s_dot + 256;
-  int* s_sel = reinterpret_cast<int*>(s_score + 256);
-  int* s_pick = s_sel + 256;
+  float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
+  float* s_dot = s_qbar + kSelQbarLds;
+  int* s_pick = reinterpret_cast<int*>(s_dot + 3 * 256);
   halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
 
-  // one (page, row, head) page-mean row per thread, straight to registers
+  // Every global load below is issued before the first wait: the page-mean
+  // row of this thread's (page, row, head) triple, its share of the
+  // candidate descriptors and its query pieces.
   uint4 kb[PIECES];
   int my_r = 0, my_h = 0;
   if (tid < triples) {
@@ -290,64 +306,114 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
 #pragma unroll
     for (int c = 0; c < PIECES; ++c) kb[c] = *reinterpret_cast<const uint4*>(row + c * 16);
   }
-  // GQA-mean query rows, rounded to the q dtype
-  for (int e = tid; e < rows * H_kv * D; e += NT) {
-    const int d = e % D, h = (e / D) % H_kv, r = e / (D * H_kv);
-    const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
-    float v;
-    if (rep == 1) {
-      v = load_elem(P.q, qb + (int64_t)h * P.q_stride_h + d, DT);
-    } else {
+  const uint2* cat = reinterpret_cast<const uint2*>(S.catalog + (int64_t)sel * S.catalog_stride);
+  uint2 cw[CW];
+#pragma unroll
+  for (int k = 0; k < CW; ++k) {
+    const int w = tid + k * NT;
+    if (w < n * DW2) cw[k] = cat[w];
+  }
+  // GQA-mean query rows: fp32 sum over the rep heads in head order, times
+  // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
+  if (P.q_aligned) {
+    const int npieces = rows * H_kv * PIECES;
+#pragma unroll
+    for (int k = 0; k < QP; ++k) {
+      const int pc = tid + k * NT;
+      if (pc >= npieces) break;
+      const int c = pc % PIECES, h = (pc / PIECES) % H_kv, r = pc / (PIECES * H_kv);
+      const char* qrow = reinterpret_cast<const char*>(P.q) +
+                         ((int64_t)(b0 + r) * P.q_stride_b + (int64_t)h * rep * P.q_stride_h) * E::size + c * 16;
+      float acc[EP];
+#pragma unroll
+      for (int e = 0; e < EP; ++e) acc[e] = 0.f;
+      for (int j0 = 0; j0 < rep; j0 += QB) {
+        uint4 qv[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j)
+          if (j0 + j < rep) qv[j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)(j0 + j) * P.q_stride_h * E::size);
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+          if (j0 + j < rep) {
+            float f[EP];
+            E::unpack(qv[j], f);
+#pragma unroll
+            for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
+          }
+        }
+      }
+      float* dst = s_qbar + (r * H_kv + h) * QS + c * EP;
+#pragma unroll
+      for (int e = 0; e < EP; ++e) {
+        float v = acc[e];
+        if (rep != 1) {
+          v = opaque(v * P.inv_rep);
+          v = DT == HALO_F32 ? v
+              : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
+                                 : f16_bits_to_f32(f32_to_f16_rne(v)));
+        }
+        dst[e] = v;
+      }
+    }
+  } else {
+    for (int e = tid; e < rows * H_kv * D; e += NT) {
+      const int d = e % D, h = (e / D) % H_kv, r = e / (D * H_kv);
+      const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
       float acc = 0.f;
       for (int j = 0; j < rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * rep + j) * P.q_stride_h + d, DT);
-      acc = opaque(acc * P.inv_rep);
-      v = DT == HALO_F32 ? acc
-          : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(acc) << 16)
-                             : f16_bits_to_f32(f32_to_f16_rne(acc)));
+      float v = acc;
+      if (rep != 1) {
+        v = opaque(v * P.inv_rep);
+        v = DT == HALO_F32 ? v
+            : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
+                               : f16_bits_to_f32(f32_to_f16_rne(v)));
+      }
+      s_qbar[(e / D) * QS + d] = v;
     }
-    s_qbar[e] = v;
   }
-  // the candidate descriptors
-  const uint32_t* cat = reinterpret_cast<const uint32_t*>(S.catalog + (int64_t)sel * S.catalog_stride);
-  constexpr int DW = sizeof(halo_chunk_desc) / 4;
-  for (int w = tid; w < n * DW; w += NT) reinterpret_cast<uint32_t*>(s_cat)[w] = cat[w];
+#pragma unroll
+  for (int k = 0; k < CW; ++k) {
+    const int w = tid + k * NT;
+    if (w < n * DW2) reinterpret_cast<uint2*>(s_cat)[w] = cw[k];
+  }
   __syncthreads();
 
   if (tid < triples) {
-    const float* qg = s_qbar + (my_r * H_kv + my_h) * D;
+    const float* qg = s_qbar + (my_r * H_kv + my_h) * QS;
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < PIECES; ++c) {
-      float f[E::per16];
+      float f[EP];
       E::unpack(kb[c], f);
 #pragma unroll
-      for (int e = 0; e < E::per16; ++e) acc = acc + qg[c * E::per16 + e] * f[e];
+      for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
     }
     s_dot[tid] = acc;
   }
   __syncthreads();
-  for (int i = tid; i < n; i += NT) {
-    float best = -INFINITY;
-    for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
-    s_score[i] = (best != best) ? -INFINITY : best;
-  }
-  __syncthreads();
-  for (int i = tid; i < n; i += NT) {
-    const float si = s_score[i];
+  // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
+  // over (row, KV head), NaN -> -inf; rank by (score desc, index asc) with
+  // readlane broadcasts; the chosen chunks are listed in ascending index
+  // order with a ballot prefix count.
+  if (tid < kWave) {
+    const int i = tid;
+    float sc = -INFINITY;
+    if (i < n) {
+      float best = -INFINITY;
+#pragma unroll 8
+      for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
+      sc = (best != best) ? -INFINITY : best;
+    }
     int rank = 0;
     for (int j = 0; j < n; ++j) {
-      const float sj = s_score[j];
-      rank += (sj > si || (sj == si && j < i)) ? 1 : 0;
+      const float sj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), j));
+      rank += (sj > sc || (sj == sc && j < i)) ? 1 : 0;
     }
-    s_sel[i] = rank < kk;
-  }
-  __syncthreads();
-  for (int i = tid; i < n; i += NT) {
-    if (writer && S.score_out) S.score_out[(int64_t)sel * S.n_cold + i] = s_score[i];
-    if (!s_sel[i]) continue;
-    int pos = 0;
-    for (int j = 0; j < i; ++j) pos += s_sel[j];
-    s_pick[pos] = i;
+    const bool chosen = i < n && rank < kk;
+    const uint64_t mask = __ballot(chosen);
+    const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+    if (chosen) s_pick[pos] = i;
+    if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
   }
   __syncthreads();
   if (writer && S.idx_out) {
@@ -356,10 +422,28 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
   return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
 }
 
+template <int DT>
+struct MfmaOp;
+template <>
+struct MfmaOp<HALO_BF16> {
+  typedef __attribute__((ext_vector_type(8))) __bf16 v8;
+  __device__ static __forceinline__ f32x4 run(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaOp<HALO_F16> {
+  typedef __attribute__((ext_vector_type(8))) _Float16 v8;
+  __device__ static __forceinline__ f32x4 run(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kernel(DecodeParams P) {
   using E = Elem<DT>;
+  constexpr bool kMfma = DT != HALO_F32;  // q.k on the matrix cores
   constexpr int EP = E::per16;          // elements per 16-byte piece
   constexpr int SL = D / EP;            // pieces per row
   constexpr int RPI = kWave / SL;       // rows covered by one load instruction
@@ -367,17 +451,22 @@ decode_attn_kernel(DecodeParams P) {
   constexpr int KROW = RB + 16;         // padded LDS row stride (bank-conflict free)
   constexpr int TILE = SL <= 16 ? kWave : kWave * 16 / SL;  // rows per wave tile
   constexpr int PPL = TILE / RPI;       // 16-byte pieces per lane per tile (K and V each)
-  constexpr int LPH0 = kWave / REP;     // lanes per query head in the q.k phase
+  constexpr int LPH0 = kWave / REP;     // lanes per query head in the VALU q.k phase
   constexpr int LPH = LPH0 < TILE ? LPH0 : TILE;
-  constexpr int RPL = TILE / LPH;       // rows per lane in the q.k phase
+  constexpr int RPL = TILE / LPH;       // rows per lane in the VALU q.k phase
   static_assert(SL * RPI == kWave && PPL * RPI == TILE && PPL % 2 == 0, "tile shape");
   static_assert(LPH == 8 || LPH == 16 || LPH == 32 || LPH == 64, "lane groups");
-  static_assert(kSelBytes <= (NW * REP * RB + NW * TILE * KROW + NW * TILE * REP * 4), "selection scratch");
+  // MFMA path: 16-row blocks, k-steps of 32 elements, V pieces per block
+  constexpr int NB = TILE / 16;
+  constexpr int KS = D / 32;
+  constexpr int VPB = 16 / RPI;
+  static_assert(!kMfma || (REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL), "mfma tile shape");
 
-  constexpr int SZ_Q = NW * REP * RB;  // one copy of the group's q per wave
-  constexpr int SZ_K = NW * TILE * KROW;
+  constexpr int SZ_Q = kMfma ? 0 : NW * REP * RB;  // VALU path: one copy of the group's q per wave
+  constexpr int SZ_K = kMfma ? 0 : NW * TILE * KROW;
   constexpr int SZ_P = NW * TILE * REP * 4;
-  constexpr int SZ_A = SZ_Q + SZ_K + SZ_P;
+  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P;
+  constexpr int SZ_A = SZ_A0 > kSelBytes ? SZ_A0 : kSelBytes;
   constexpr int SZ_B = NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
   char* s_q = smem + (threadIdx.x / kWave) * REP * RB;
@@ -393,11 +482,14 @@ decode_attn_kernel(DecodeParams P) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int witem = blockIdx.x;
 
-  int4 item = reinterpret_cast<const int4*>(P.work)[witem];
+  const int32_t* wrec = P.work + (int64_t)witem * kWorkInts;
+  int4 item = *reinterpret_cast<const int4*>(wrec);
   item.x = __builtin_amdgcn_readfirstlane(item.x);
   item.y = __builtin_amdgcn_readfirstlane(item.y);
   item.z = __builtin_amdgcn_readfirstlane(item.z);
   item.w = __builtin_amdgcn_readfirstlane(item.w);
+  const int wslot = __builtin_amdgcn_readfirstlane(wrec[4]);
+  if ((unsigned)wslot >= (unsigned)P.n_work) return;  // malformed record: no partial slot to write
   const int g = item.y;
   const int sub = g % P.n_sub;
   const int bh = g / P.n_sub;
@@ -409,12 +501,12 @@ decode_attn_kernel(DecodeParams P) {
     const bool writer = (P.sel.per_row || b == 0) && h_kv == 0 && sub == 0 && item.x == P.sel.slot0 && item.z == 0;
     const int pick = fused_select<DT, D, 64 * NW>(P, b, smem, item.x - P.sel.slot0, writer);
     if (pick >= 0) {
-      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelMaxQbar * 4 + 4 * 256 * 4)[pick]);
+      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelQbarLds * 4 + 4 * 256 * 4)[pick]);
     } else {
       dsc = P.descs[item.x];
       dsc.T_c = 0;
     }
-    __syncthreads();  // LDS is reused for q and tiles below
+    __syncthreads();  // LDS is reused below
   } else {
     dsc = P.descs[item.x];
   }
@@ -442,143 +534,257 @@ decode_attn_kernel(DecodeParams P) {
   const int ws = t0 + wave * tiles_per_wave * TILE;
   const int we = min(t1, ws + tiles_per_wave * TILE);
 
-  float m_run[REP], acc_o[REP][EP];
+  float m_run[REP], acc_o[REP][EP], l_head[REP];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m_run[r] = -INFINITY;
 #pragma unroll
     for (int e = 0; e < EP; ++e) acc_o[r][e] = 0.f;
   }
-  float l_lane = 0.f;  // this lane's share of its head's softmax denominator
 
-  char* kl = s_kall + wave * TILE * KROW;
   float* pl = s_pall + wave * TILE * REP;
   const int my_col = lane % SL;
   const int my_row0 = lane / SL;
-  const bool qk_lane = lane < REP * LPH;
-  const int hl = qk_lane ? lane / LPH : 0;  // this lane's head in the q.k phase
-  const int rb = lane % LPH;                // its first row
-  const int voff0 = my_row0 * 0 + my_col * 16;
+  const int voff0 = my_col * 16;
 
-  // Tile loads: rows past the slice read as zeros (hardware range check).
-  uint4 kreg[PPL], vreg[PPL];
-  auto load_k = [&](int tb) {
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
+  if constexpr (kMfma) {
+    // ---- q.k on MFMA 16x16x32: A = 16 K rows x 32 elements (lane l holds
+    // row l%16, elements 8*(l/16)..+8 of the k-step), B = q^T (lane l holds
+    // head l%16, same elements), D = scores (lane l: head l%16, rows
+    // 4*(l/16)..+4).  K goes from the buffer loads straight into A operands.
+    const int hl = lane & 15;   // this lane's head in the score layout
+    const int kg = lane >> 4;   // its k-group / row quad
+    uint4 qb[KS];
+    {
+      const bool live = hl < nvalid_h;
+      const char* qrow = reinterpret_cast<const char*>(P.q) +
+                         ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + (live ? hl : 0)) * P.q_stride_h) * E::size;
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) kreg[i] = buf_ld16(rk, (int)((i * RPI + my_row0) * kst) + voff0);
-  };
-  auto load_v = [&](int tb) {
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
-#pragma unroll
-    for (int i = 0; i < PPL; ++i) vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
-  };
-  for (int tb = ws; tb < we; tb += TILE) {
-    const int nrows = min(TILE, we - tb);
-    load_k(tb);
-    load_v(tb);
-    if (tb == ws) {
-      // This wave's copy of the group's query rows (zeros for padding
-      // heads), fetched while the first tile's K/V loads are in flight.
-      if (P.q_aligned) {
-        for (int pc = lane; pc < REP * SL; pc += kWave) {
-          const int r = pc / SL, c = pc % SL;
-          uint4 v = make_uint4(0, 0, 0, 0);
-          if (r < nvalid_h)
-            v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(P.q) +
-                                                (b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h) * E::size +
-                                                c * 16);
-          *reinterpret_cast<uint4*>(s_q + pc * 16) = v;
-        }
-      } else {
-        for (int i = lane; i < REP * D; i += kWave) {
-          const int r = i / D, d = i % D;
-          const int64_t qi = b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h + d;
-          if (DT == HALO_F32) {
-            reinterpret_cast<float*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const float*>(P.q)[qi] : 0.f;
+      for (int s = 0; s < KS; ++s) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (live) {
+          if (P.q_aligned) {
+            v = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
           } else {
-            reinterpret_cast<uint16_t*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const uint16_t*>(P.q)[qi] : 0;
+            const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
+            v.x = qh[0] | ((uint32_t)qh[1] << 16);
+            v.y = qh[2] | ((uint32_t)qh[3] << 16);
+            v.z = qh[4] | ((uint32_t)qh[5] << 16);
+            v.w = qh[6] | ((uint32_t)qh[7] << 16);
+          }
+        }
+        qb[s] = v;
+      }
+    }
+    float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
+    float l_lane = 0.f;        // this lane's share of head hl's denominator
+    uint4 kreg[NB][KS], vreg[PPL];
+    for (int tb = ws; tb < we; tb += TILE) {
+      const int nrows = min(TILE, we - tb);
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
+      // issue order K0 V0 K1 V1 ...: block j is processed as soon as its
+      // own loads have landed (the load counter drains in issue order)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kreg[nb][s] = buf_ld16(rk, (int)((nb * 16 + hl) * kst) + s * 64 + kg * 16);
+#pragma unroll
+        for (int j = 0; j < VPB; ++j) {
+          const int i = nb * VPB + j;
+          vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sc = MfmaOp<DT>::run(kreg[nb][s], qb[s], sc);
+        float sv[4], bm = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool valid = nb * 16 + kg * 4 + c < nrows;
+          sv[c] = valid ? sc[c] * P.scale2 : -INFINITY;
+          bm = fmaxf(bm, sv[c]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        const float m_new = fmaxf(m_lane, bm);
+        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+        m_lane = m_new;
+        float psum = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float p = __builtin_amdgcn_exp2f(sv[c] - ms);
+          psum += p;
+          if (hl < REP) pl[(nb * 16 + kg * 4 + c) * REP + hl] = p;
+        }
+        l_lane = l_lane * alpha + psum;
+        float al[REP];
+        bool rescale = false;
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          al[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
+          rescale |= al[r] != 1.f;
+        }
+        if (rescale) {
+#pragma unroll
+          for (int r = 0; r < REP; ++r)
+#pragma unroll
+            for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
+        }
+        wave_lds_fence();
+        // P.V over the block's row pairs (VALU, V straight from registers)
+#pragma unroll
+        for (int j = 0; j < VPB; j += 2) {
+          const int i = nb * VPB + j;
+          const int ra = i * RPI + my_row0, rbw = (i + 1) * RPI + my_row0;
+          float pa[REP], pb[REP];
+#pragma unroll
+          for (int r = 0; r < REP; ++r) {
+            pa[r] = pl[ra * REP + r];
+            pb[r] = pl[rbw * REP + r];
+          }
+          pv_pair<DT, REP, EP>(vreg[i], vreg[i + 1], pa, pb, acc_o);
+        }
+      }
+      wave_lds_fence();  // the next tile rewrites pl
+    }
+    float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
+      l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
+    }
+  } else {
+    // ---- VALU path (fp32): K transposed through LDS, lane groups per head.
+    float l_lane = 0.f;  // this lane's share of its head's softmax denominator
+    char* kl = s_kall + wave * TILE * KROW;
+    const bool qk_lane = lane < REP * LPH;
+    const int hl = qk_lane ? lane / LPH : 0;  // this lane's head in the q.k phase
+    const int rb = lane % LPH;                // its first row
+
+    // Tile loads: rows past the slice read as zeros (hardware range check).
+    uint4 kreg[PPL], vreg[PPL];
+    auto load_k = [&](int tb) {
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) kreg[i] = buf_ld16(rk, (int)((i * RPI + my_row0) * kst) + voff0);
+    };
+    auto load_v = [&](int tb) {
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
+    };
+    for (int tb = ws; tb < we; tb += TILE) {
+      const int nrows = min(TILE, we - tb);
+      load_k(tb);
+      load_v(tb);
+      if (tb == ws) {
+        // This wave's copy of the group's query rows (zeros for padding
+        // heads), fetched while the first tile's K/V loads are in flight.
+        if (P.q_aligned) {
+          for (int pc = lane; pc < REP * SL; pc += kWave) {
+            const int r = pc / SL, c = pc % SL;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (r < nvalid_h)
+              v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(P.q) +
+                                                  (b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h) * E::size +
+                                                  c * 16);
+            *reinterpret_cast<uint4*>(s_q + pc * 16) = v;
+          }
+        } else {
+          for (int i = lane; i < REP * D; i += kWave) {
+            const int r = i / D, d = i % D;
+            const int64_t qi = b * P.q_stride_b + (int64_t)(hq0 + r) * P.q_stride_h + d;
+            if (DT == HALO_F32) {
+              reinterpret_cast<float*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const float*>(P.q)[qi] : 0.f;
+            } else {
+              reinterpret_cast<uint16_t*>(s_q)[i] = r < nvalid_h ? reinterpret_cast<const uint16_t*>(P.q)[qi] : 0;
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < PPL; ++i)
-      *reinterpret_cast<uint4*>(kl + (i * RPI + my_row0) * KROW + my_col * 16) = kreg[i];
-    wave_lds_fence();
+      for (int i = 0; i < PPL; ++i)
+        *reinterpret_cast<uint4*>(kl + (i * RPI + my_row0) * KROW + my_col * 16) = kreg[i];
+      wave_lds_fence();
 
-    // q.k: lane group hl holds head hl's scores for rows rb + LPH*i.
-    float s[RPL];
+      // q.k: lane group hl holds head hl's scores for rows rb + LPH*i.
+      float s[RPL];
 #pragma unroll
-    for (int i = 0; i < RPL; ++i) s[i] = 0.f;
+      for (int i = 0; i < RPL; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int c = 0; c < SL; ++c) {
-      const uint4 qp = *reinterpret_cast<const uint4*>(s_q + hl * RB + c * 16);
+      for (int c = 0; c < SL; ++c) {
+        const uint4 qp = *reinterpret_cast<const uint4*>(s_q + hl * RB + c * 16);
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+          const uint4 kp = *reinterpret_cast<const uint4*>(kl + (rb + LPH * i) * KROW + c * 16);
+          s[i] = E::dot(kp, qp, s[i]);
+        }
+      }
+      float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < RPL; ++i) {
-        const uint4 kp = *reinterpret_cast<const uint4*>(kl + (rb + LPH * i) * KROW + c * 16);
-        s[i] = E::dot(kp, qp, s[i]);
+        const bool valid = qk_lane && (rb + LPH * i) < nrows;
+        s[i] = valid ? s[i] * P.scale2 : -INFINITY;
+        mx = fmaxf(mx, s[i]);
       }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < RPL; ++i) {
-      const bool valid = qk_lane && (rb + LPH * i) < nrows;
-      s[i] = valid ? s[i] * P.scale2 : -INFINITY;
-      mx = fmaxf(mx, s[i]);
-    }
-    mx = group_max<LPH>(mx);
-    float alpha[REP], my_ms = 0.f, my_alpha = 1.f;
-    bool rescale = false;
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      const float tmax = head_value<LPH, true>(mx, r);
-      const float m_new = fmaxf(m_run[r], tmax);
-      const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-      alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - ms);
-      rescale |= (alpha[r] != 1.f);
-      m_run[r] = m_new;
-      if (hl == r) {
-        my_ms = ms;
-        my_alpha = alpha[r];
-      }
-    }
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < RPL; ++i) {
-      const float p = __builtin_amdgcn_exp2f(s[i] - my_ms);
-      psum += p;
-      if (qk_lane) pl[(rb + LPH * i) * REP + hl] = p;
-    }
-    l_lane = l_lane * my_alpha + psum;
-    if (rescale) {
-#pragma unroll
-      for (int r = 0; r < REP; ++r)
-#pragma unroll
-        for (int e = 0; e < EP; ++e) acc_o[r][e] *= alpha[r];
-    }
-    wave_lds_fence();
-
-    // P.V over row pairs (rows j and j+1 of this lane's column slice).
-#pragma unroll
-    for (int j = 0; j < PPL; j += 2) {
-      const int ra = j * RPI + my_row0, rbw = (j + 1) * RPI + my_row0;
-      float pa[REP], pb[REP];
+      mx = group_max<LPH>(mx);
+      float alpha[REP], my_ms = 0.f, my_alpha = 1.f;
+      bool rescale = false;
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
-        pa[r] = pl[ra * REP + r];
-        pb[r] = pl[rbw * REP + r];
+        const float tmax = head_value<LPH, true>(mx, r);
+        const float m_new = fmaxf(m_run[r], tmax);
+        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+        alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - ms);
+        rescale |= (alpha[r] != 1.f);
+        m_run[r] = m_new;
+        if (hl == r) {
+          my_ms = ms;
+          my_alpha = alpha[r];
+        }
       }
-      pv_pair<DT, REP, EP>(vreg[j], vreg[j + 1], pa, pb, acc_o);
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[i] - my_ms);
+        psum += p;
+        if (qk_lane) pl[(rb + LPH * i) * REP + hl] = p;
+      }
+      l_lane = l_lane * my_alpha + psum;
+      if (rescale) {
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+#pragma unroll
+          for (int e = 0; e < EP; ++e) acc_o[r][e] *= alpha[r];
+      }
+      wave_lds_fence();
+
+      // P.V over row pairs (rows j and j+1 of this lane's column slice).
+#pragma unroll
+      for (int j = 0; j < PPL; j += 2) {
+        const int ra = j * RPI + my_row0, rbw = (j + 1) * RPI + my_row0;
+        float pa[REP], pb[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          pa[r] = pl[ra * REP + r];
+          pb[r] = pl[rbw * REP + r];
+        }
+        pv_pair<DT, REP, EP>(vreg[j], vreg[j + 1], pa, pb, acc_o);
+      }
+      wave_lds_fence();
     }
-    wave_lds_fence();
+    // l per head: reduce the lane shares of each head's group
+    const float lg = group_sum<LPH>(qk_lane ? l_lane : 0.f);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) l_head[r] = head_value<LPH, false>(lg, r);
   }
 
-  // Wave partial: l per head (reduce the lane shares of each head's group),
-  // o across the RPI lane rows that share a column slice.
-  const float lg = group_sum<LPH>(qk_lane ? l_lane : 0.f);
-  float l_head[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r) l_head[r] = head_value<LPH, false>(lg, r);
+  // Wave partial: o across the RPI lane rows that share a column slice.
 #pragma unroll
   for (int r = 0; r < REP; ++r)
 #pragma unroll
@@ -603,7 +809,7 @@ decode_attn_kernel(DecodeParams P) {
 
   // Merge the NW wave partials into this work item's partial (plain stores:
   // the merge kernel that reads them runs after this kernel completes).
-  float* wso = P.ws_o + (int64_t)witem * REP * D;
+  float* wso = P.ws_o + (int64_t)wslot * REP * D;
   for (int i = tid; i < REP * D; i += 64 * NW) {
     const int r = i / D;
     float M = -INFINITY;
@@ -624,8 +830,8 @@ decode_attn_kernel(DecodeParams P) {
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
-    P.ws_ml[((int64_t)witem * REP + r) * 2 + 0] = M;
-    P.ws_ml[((int64_t)witem * REP + r) * 2 + 1] = acc;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc;
   }
 }
 
@@ -667,20 +873,32 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
   float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
   const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4 + col;
   const float* wml = P.ws_ml + ((int64_t)gbeg * REP + r) * 2;
-#pragma unroll 4
-  for (int pp = phase; pp < np; pp += TPC) {
-    const float mp = wml[(int64_t)pp * REP * 2];
-    const float lp = wml[(int64_t)pp * REP * 2 + 1];
-    const float4 op = wo4[(int64_t)pp * REP * C4];
-    const float mn = fmaxf(mt, mp);
-    const float ms = (mn == -INFINITY) ? 0.f : mn;
-    const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(mp - ms);
-    lt = lt * a + lp * c;
-    ot.x = ot.x * a + op.x * c;
-    ot.y = ot.y * a + op.y * c;
-    ot.z = ot.z * a + op.z * c;
-    ot.w = ot.w * a + op.w * c;
-    mt = mn;
+  constexpr int MB = 8;  // partials per thread whose loads are issued together
+  for (int p0 = phase; p0 < np; p0 += MB * TPC) {
+    float mp[MB], lp[MB];
+    float4 op[MB];
+#pragma unroll
+    for (int k = 0; k < MB; ++k) {
+      const int pp = p0 + k * TPC;
+      if (pp < np) {
+        mp[k] = wml[(int64_t)pp * REP * 2];
+        lp[k] = wml[(int64_t)pp * REP * 2 + 1];
+        op[k] = wo4[(int64_t)pp * REP * C4];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MB; ++k) {
+      if (p0 + k * TPC >= np) break;
+      const float mn = fmaxf(mt, mp[k]);
+      const float ms = (mn == -INFINITY) ? 0.f : mn;
+      const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(mp[k] - ms);
+      lt = lt * a + lp[k] * c;
+      ot.x = ot.x * a + op[k].x * c;
+      ot.y = ot.y * a + op[k].y * c;
+      ot.z = ot.z * a + op[k].z * c;
+      ot.w = ot.w * a + op[k].w * c;
+      mt = mn;
+    }
   }
   // The incoming accumulator is read by every thread before the barrier:
   // the column-0 thread overwrites m/l after it.
@@ -855,6 +1073,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
   p.n_sub = n_sub;
   p.descs = descs;
   p.work = work;
+  p.n_work = n_work;
   p.q_pos = q_pos;
   p.scale2 = (float)((double)scale * 1.4426950408889634);
   {
@@ -872,7 +1091,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
     const int esz = elem_size(dtype);
     const int rows = S.per_row ? 1 : B;
     HALO_CHECK_ARG(S.kmean && S.catalog, "selection needs kmean and catalog");
-    HALO_CHECK_ARG(S.n_cold >= 1 && S.n_cold <= kSelMaxCold, "n_cold must be in [1, 128]");
+    HALO_CHECK_ARG(S.n_cold >= 1 && S.n_cold <= kSelMaxCold, "n_cold must be in [1, 64]");
     HALO_CHECK_ARG(S.top_k >= 1 && S.slot0 >= 0 && S.slot0 + S.top_k <= n_desc,
                    "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
     HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");

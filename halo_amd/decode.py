@@ -1,7 +1,7 @@
 """Planning and launching of the split-K decode-attention kernel.
 
 A *plan* is the device-resident chunk table (``halo_chunk_desc`` records) and
-work list (``{desc, group, t0, t1}`` int32 quadruples) of one
+work list (``{desc, group, t0, t1, partial slot}`` int32 records) of one
 ``halo_decode_attn`` launch.  Building it costs a few host microseconds per
 chunk; a plan can be replayed for as long as the K/V tensors it points at
 stay alive (the plan keeps references to them), which is how the benchmark
@@ -22,6 +22,8 @@ import numpy as np
 import torch
 
 from . import _native as nat
+
+WORK_INTS = 8  # int32 per work record (kWorkInts in the kernels)
 
 DESC_DTYPE = np.dtype([
     ("k", "<u8"), ("v", "<u8"),
@@ -169,13 +171,21 @@ def descs_to_device(descs: np.ndarray, device) -> torch.Tensor:
 
 def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                chunks: Sequence[ChunkRef], device, rep_t: Optional[int] = None,
-               split: Optional[int] = None, q_pos_host: Optional[Sequence[int]] = None) -> DecodePlan:
+               split: Optional[int] = None, q_pos_host: Optional[Sequence[int]] = None,
+               first: Optional[Sequence[int]] = None) -> DecodePlan:
     """Lay out descriptors and work items for a chunk list.
 
     ``q_pos_host`` (per batch row) lets the planner drop causal chunks that
     lie entirely after the query, as the reference's chunk walk does with
     ``c0 > q_pos`` (halo/kv_cache_chunked.py:658,714); the kernel applies the
     row-level causal cut itself either way.
+
+    Work records are ``WORK_INTS`` int32: (chunk, group, t0, t1, partial
+    slot, 0, 0, 0).  Partial slots are numbered group by group, which is the
+    order the merge reads them; the records themselves are in dispatch
+    order, where the items of the chunks listed in ``first`` come before
+    all others (the tiered layer puts its selection slots there, so their
+    longer dependency chain starts first).
     """
     if H % H_kv:
         raise AssertionError(f"head count mismatch: q has {H}, kv has {H_kv}")
@@ -221,13 +231,16 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                     if chunks[i].causal and q_pos_host is not None:
                         hi = min(T, int(q_pos_host[b]) - chunks[i].chunk_start + 1)
                     for t0 in range(0, hi, split):
-                        work.append((i, g, t0, min(t0 + split, hi)))
+                        work.append((i, g, t0, min(t0 + split, hi), len(work), 0, 0, 0))
                     if s == 0:
                         rows_attended += hi
                 if len(work) == n0:
-                    work.append((0, g, 0, 0))
+                    work.append((0, g, 0, 0, len(work), 0, 0, 0))
                 offsets.append(len(work))
-    work_np = np.asarray(work, dtype=np.int32).reshape(-1, 4)
+    if first:
+        early = set(int(i) for i in first)
+        work = [w for w in work if w[0] in early] + [w for w in work if w[0] not in early]
+    work_np = np.asarray(work, dtype=np.int32).reshape(-1, WORK_INTS)
     dev_descs = _to_device(descs.view(np.uint8).copy(), device)
     return DecodePlan(
         B=B, H=H, H_kv=H_kv, D=D, rep_t=rep_t, dtype=dtype,

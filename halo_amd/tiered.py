@@ -31,7 +31,7 @@ from .chunk_scorer import chunk_means, score_topk
 from .decode import ChunkRef, DecodePlan, build_plan, descs_to_device, launch, pack_descs
 
 # In-kernel selection limits of halo_decode_attn_tiered (include/halo_hip.h).
-_SEL_MAX_COLD = 128
+_SEL_MAX_COLD = 64
 _SEL_MAX_TRIPLES = 256
 _SEL_MAX_QBAR = 2048
 
@@ -58,7 +58,8 @@ class TieredDecodeLayer:
         slots = [cold[widest]] * top_k
         self.slot0 = 0
         self.plan: DecodePlan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype,
-                                           chunks=slots + list(hot), device=device, split=split)
+                                           chunks=slots + list(hot), device=device, split=split,
+                                           first=range(top_k))
         cat, keep = pack_descs(cold, B=B, H_kv=H_kv, D=D, dtype=dtype)
         self.catalog = descs_to_device(cat, device)
         self.plan.keep += keep

@@ -79,7 +79,12 @@ size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
  *
  *   q        (B, H, D) elements of `dtype`, q[b*q_stride_b + h*q_stride_h + d]
  *   descs    device array of n_desc halo_chunk_desc
- *   work     device int32 array [n_work][4]; group_offsets device int32 [n_groups+1]
+ *   work     device int32 array [n_work][8] of {desc, group, t0, t1, slot, 0,
+ *            0, 0} in dispatch order: the item attends rows [t0, t1) of
+ *            descs[desc] for query-head group `group` = (b*H_kv + h_kv)*n_sub
+ *            + sub (n_sub = ceil(rep/rep_t)) and writes partial `slot`;
+ *            the slots of group g are group_offsets[g] .. group_offsets[g+1]-1
+ *            (device int32 [n_groups+1]), a permutation of 0 .. n_work-1
  *   q_pos    device int64 [B] global query position, or NULL (no causal mask)
  *   scale    softmax scale applied to q.k in fp32
  *   m,l,o    fp32 online-softmax accumulators (B,H), (B,H), (B,H,D) with the
@@ -94,7 +99,7 @@ size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
  *
  * Enqueues two kernels on `stream`: the split-K attention pass, which writes
  * one partial per work item, and a merge pass that combines each group's
- * partials (in work order: results are deterministic) with the accumulators.
+ * partials (in slot order: results are deterministic) with the accumulators.
  * Replaces update_chunk / finalize / triton_chunked_attention
  * (halo/triton_chunked.py:151-267) and the PyTorch chunk walk
  * (halo/kv_cache_chunked.py:194-276, 864-964) for T_q == 1.
@@ -119,7 +124,7 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
  * (d - slot0)-th chosen chunk in ascending index order (top-k order: score
  * descending, then index ascending); a slot past the number of eligible
  * chunks attends nothing.  idx_out[s*top_k + j] / score_out[s*n_cold + p]
- * receive the selection when non-NULL.  Limits: n_cold <= 128,
+ * receive the selection when non-NULL.  Limits: n_cold <= 64,
  * n_cold * rows * H_kv <= 256 and rows * H_kv * D <= 2048 per selection
  * (rows = 1 when per_row).  The work items of a slot must cover as many rows
  * as the largest catalog chunk (rows past a chunk's T_c are skipped).

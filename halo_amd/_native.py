@@ -27,6 +27,7 @@ HALO_E_WORKSPACE = -4
 
 F32, BF16, F16 = 0, 1, 2
 CHUNK_CAUSAL = 1
+CHUNK_KIVI2 = 2
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -69,10 +70,16 @@ _SIGNATURES = {
     "halo_decode_workspace_size": (_size_t, [_i32, _i32, _i32]),
     "halo_decode_attn": (_i32, _DECODE_ARGS + [_c_void_p]),                      # + stream
     "halo_decode_attn_tiered": (_i32, _DECODE_ARGS + [ctypes.POINTER(SelectCfg), _c_void_p]),  # + sel, stream
+    "halo_decode_attn_kivi": (_i32, _DECODE_ARGS + [_c_void_p]),                 # + stream
     "halo_finalize": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                              _c_void_p, _i32, _c_void_p, _c_void_p]),
     "halo_lse_merge": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
                               _c_void_p, _c_void_p, _c_void_p]),
+    "halo_kivi_block_bytes": (_size_t, [_i32, _i32]),
+    "halo_kivi_quantize": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
+                                  _i32, _i32, _i32, _i32, _i32, _i32, _c_void_p, _i64, _i64, _c_void_p]),
+    "halo_kivi_dequantize": (_i32, [_c_void_p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+                                    _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "halo_chunk_means": (_i32, [_c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
                                 _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "halo_chunk_score_topk": (_i32, [

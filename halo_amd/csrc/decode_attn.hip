@@ -422,6 +422,72 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
   return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
 }
 
+// ---------------------------------------------------------------------------
+// Work-item epilogue shared by the decode kernels: reduce each wave's o over
+// the lanes that share a column slice, merge the NW wave partials (m, l, o)
+// through LDS and store this item's partial at workspace slot `wslot` with
+// plain stores (the merge kernel that reads them runs after this kernel).
+// ---------------------------------------------------------------------------
+template <int D, int REP, int NW, int SL, int EP>
+__device__ __forceinline__ void write_partial(const DecodeParams& P, int wslot, float (&acc_o)[REP][EP],
+                                              const float* m_run, const float* l_head, float* s_wo,
+                                              float (*s_wm)[REP], float (*s_wl)[REP]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int off = SL; off < kWave; off <<= 1)
+#pragma unroll
+      for (int e = 0; e < EP; ++e) acc_o[r][e] += __shfl_xor(acc_o[r][e], off, kWave);
+  __syncthreads();  // every wave is out of its tile loop: LDS may be reused
+  if (lane < SL) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int e = 0; e < EP; ++e) s_wo[(wave * REP + r) * D + lane * EP + e] = acc_o[r][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      s_wm[wave][r] = m_run[r];
+      s_wl[wave][r] = l_head[r];
+    }
+  }
+  __syncthreads();
+  float* wso = P.ws_o + (int64_t)wslot * REP * D;
+  for (int i = tid; i < REP * D; i += 64 * NW) {
+    const int r = i / D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
+    wso[i] = acc;
+  }
+  if (tid < REP) {
+    const int r = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float from_bits16(uint16_t h) {
+  if constexpr (DT == HALO_BF16) return __uint_as_float((uint32_t)h << 16);
+  return f16_bits_to_f32(h);
+}
+
 template <int DT>
 struct MfmaOp;
 template <>
@@ -515,7 +581,8 @@ decode_attn_kernel(DecodeParams P) {
 
   // Row range: never past the chunk's own rows (a table slot a scorer filled
   // with a shorter or empty chunk), then the causal cut chunk_start+t <= q_pos.
-  int t0 = item.z, t1 = min(item.w, dsc.T_c);
+  // A KIVI chunk holds no plain rows: this kernel reads nothing of it.
+  int t0 = item.z, t1 = (dsc.flags & HALO_CHUNK_KIVI2) ? item.z : min(item.w, dsc.T_c);
   if ((dsc.flags & HALO_CHUNK_CAUSAL) && P.q_pos != nullptr) {
     const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;
     if (lim < (int64_t)t1) t1 = (int)max<int64_t>(lim, (int64_t)t0);
@@ -784,55 +851,234 @@ decode_attn_kernel(DecodeParams P) {
     for (int r = 0; r < REP; ++r) l_head[r] = head_value<LPH, false>(lg, r);
   }
 
-  // Wave partial: o across the RPI lane rows that share a column slice.
+  write_partial<D, REP, NW, SL, EP>(P, wslot, acc_o, m_run, l_head, s_wo, s_wm, s_wl);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention over KIVI 2-bit blocks (halo_decode_attn_kivi).  Each wave
+// takes one 32-token block per tile: the raw block (K codes, K scale/zero,
+// V codes, V scale/zero; 3 KiB at D=128) arrives with three 16-byte loads
+// per lane into this wave's LDS slot, K is dequantised straight into MFMA A
+// operands (dtype(fp32(code*scale) + zero), the dequant arithmetic of
+// baselines/kivi_cache.py:72-78) and V into the P.V pieces, so the values the
+// scores and the output see are exactly the dequantised cache.
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_dt(float a, float b) {
+  if constexpr (DT == HALO_BF16) return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+  return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+}
+// 8 consecutive 2-bit codes (16 bits) with their scales/zeros -> 8 elements
+template <int DT>
+__device__ __forceinline__ uint4 kivi_deq8(uint32_t c16, const float* s, const float* z) {
+  uint32_t w[4];
 #pragma unroll
-  for (int r = 0; r < REP; ++r)
-#pragma unroll
-    for (int off = SL; off < kWave; off <<= 1)
-#pragma unroll
-      for (int e = 0; e < EP; ++e) acc_o[r][e] += __shfl_xor(acc_o[r][e], off, kWave);
-  __syncthreads();  // every wave is out of its tile loop: phase B may reuse LDS
-  if (lane < SL) {
-#pragma unroll
-    for (int r = 0; r < REP; ++r)
-#pragma unroll
-      for (int e = 0; e < EP; ++e) s_wo[(wave * REP + r) * D + lane * EP + e] = acc_o[r][e];
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = opaque(opaque((float)((c16 >> (4 * p)) & 3u) * s[2 * p]) + z[2 * p]);
+    const float x1 = opaque(opaque((float)((c16 >> (4 * p + 2)) & 3u) * s[2 * p + 1]) + z[2 * p + 1]);
+    w[p] = pack2_dt<DT>(x0, x1);
   }
-  if (lane == 0) {
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// 8 codes sharing one scale/zero
+template <int DT>
+__device__ __forceinline__ uint4 kivi_deq8_1(uint32_t c16, float s, float z) {
+  uint32_t w[4];
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      s_wm[wave][r] = m_run[r];
-      s_wl[wave][r] = l_head[r];
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = opaque(opaque((float)((c16 >> (4 * p)) & 3u) * s) + z);
+    const float x1 = opaque(opaque((float)((c16 >> (4 * p + 2)) & 3u) * s) + z);
+    w[p] = pack2_dt<DT>(x0, x1);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <int DT, int D, int REP, int NW>
+__global__ void __launch_bounds__(64 * NW, 2)
+decode_attn_kivi_kernel(DecodeParams P) {
+  using E = Elem<DT>;
+  constexpr int EP = 8;
+  constexpr int SL = D / EP;           // 16-byte pieces per dequantised row
+  constexpr int RPI = kWave / SL;      // rows per piece layer
+  constexpr int TILE = 32;             // one block per wave tile
+  constexpr int PPL = TILE / RPI;      // V pieces per lane per tile
+  constexpr int NB = TILE / 16;        // 16-row MFMA blocks per tile
+  constexpr int KS = D / 32;           // MFMA k-steps
+  constexpr int VPB = 16 / RPI;
+  constexpr int RB2 = D / 4;           // code bytes per token row (2 bits)
+  constexpr int CB = 32 * RB2;         // code bytes of K (or V) per block
+  constexpr int BB = 2 * CB + 8 * D;   // block bytes
+  constexpr int NG = D / 32;           // V groups per token
+  constexpr int RAW16 = BB / 16;
+  constexpr int LPR = (RAW16 + kWave - 1) / kWave;  // raw 16-byte loads per lane
+  static_assert(REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL && BB % 16 == 0, "kivi tile shape");
+
+  __shared__ __attribute__((aligned(16))) char s_raw[NW][BB];
+  __shared__ float s_pall[NW][TILE * REP];
+  __shared__ float s_wo[NW * REP * D];
+  __shared__ float s_wm[NW][REP], s_wl[NW][REP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int witem = blockIdx.x;
+  const int32_t* wrec = P.work + (int64_t)witem * kWorkInts;
+  int4 item = *reinterpret_cast<const int4*>(wrec);
+  item.x = __builtin_amdgcn_readfirstlane(item.x);
+  item.y = __builtin_amdgcn_readfirstlane(item.y);
+  item.z = __builtin_amdgcn_readfirstlane(item.z);
+  item.w = __builtin_amdgcn_readfirstlane(item.w);
+  const int wslot = __builtin_amdgcn_readfirstlane(wrec[4]);
+  if ((unsigned)wslot >= (unsigned)P.n_work) return;  // malformed record: no partial slot to write
+  const int g = item.y;
+  const int sub = g % P.n_sub;
+  const int bh = g / P.n_sub;
+  const int h_kv = bh % P.H_kv;
+  const int b = bh / P.H_kv;
+  const halo_chunk_desc dsc = P.descs[item.x];
+  const int hq0 = h_kv * P.rep + sub * REP;
+  const int nvalid_h = min(REP, P.rep - sub * REP);
+
+  int t0 = item.z, t1 = min(item.w, dsc.T_c);
+  if (!(dsc.flags & HALO_CHUNK_KIVI2)) t1 = t0;  // not a KIVI chunk: nothing this kernel can read
+  if ((dsc.flags & HALO_CHUNK_CAUSAL) && P.q_pos != nullptr) {
+    const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;
+    if (lim < (int64_t)t1) t1 = (int)max<int64_t>(lim, (int64_t)t0);
+  }
+  // block bytes of this (b, h_kv); strides are in bytes for KIVI chunks
+  const char* base = reinterpret_cast<const char*>(dsc.k) +
+                     (dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h;
+
+  const int nrows_total = max(t1 - t0, 0);
+  const int ntiles_total = (nrows_total + TILE - 1) / TILE;
+  const int tiles_per_wave = (ntiles_total + NW - 1) / NW;
+  const int ws = t0 + wave * tiles_per_wave * TILE;
+  const int we = min(t1, ws + tiles_per_wave * TILE);
+
+  float m_run[REP], acc_o[REP][EP], l_head[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    m_run[r] = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) acc_o[r][e] = 0.f;
+  }
+  char* raw = s_raw[wave];
+  float* pl = s_pall[wave];
+  const int my_col = lane % SL;
+  const int my_row0 = lane / SL;
+  const int hl = lane & 15;
+  const int kg = lane >> 4;
+
+  uint4 qb[KS];
+  {
+    const bool live = hl < nvalid_h;
+    const char* qrow = reinterpret_cast<const char*>(P.q) +
+                       ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + (live ? hl : 0)) * P.q_stride_h) * E::size;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (live) {
+        if (P.q_aligned) {
+          v = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
+        } else {
+          const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
+          v.x = qh[0] | ((uint32_t)qh[1] << 16);
+          v.y = qh[2] | ((uint32_t)qh[3] << 16);
+          v.z = qh[4] | ((uint32_t)qh[5] << 16);
+          v.w = qh[6] | ((uint32_t)qh[7] << 16);
+        }
+      }
+      qb[s] = v;
     }
   }
-  __syncthreads();
-
-  // Merge the NW wave partials into this work item's partial (plain stores:
-  // the merge kernel that reads them runs after this kernel completes).
-  float* wso = P.ws_o + (int64_t)wslot * REP * D;
-  for (int i = tid; i < REP * D; i += 64 * NW) {
-    const int r = i / D;
-    float M = -INFINITY;
+  float m_lane = -INFINITY, l_lane = 0.f;
+  for (int tb = ws; tb < we; tb += TILE) {
+    const int nrows = min(TILE, we - tb);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + (int64_t)(tb / 32) * BB, BB);
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][r]);
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    float acc = 0.f;
+    for (int k = 0; k < LPR; ++k) {
+      const int idx = lane + k * kWave;
+      if (idx < RAW16) reinterpret_cast<uint4*>(raw)[idx] = buf_ld16(rr, idx * 16);
+    }
+    wave_lds_fence();
+    const uint16_t* meta_v = reinterpret_cast<const uint16_t*>(raw + 2 * CB + 4 * D);
 #pragma unroll
-    for (int w = 0; w < NW; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
-    wso[i] = acc;
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slice
+        const uint32_t c16 = *reinterpret_cast<const uint16_t*>(raw + (nb * 16 + hl) * RB2 + c0 / 4);
+        float sk[8], zk[8];
+        E::unpack(*reinterpret_cast<const uint4*>(raw + CB + 2 * c0), sk);
+        E::unpack(*reinterpret_cast<const uint4*>(raw + CB + 2 * D + 2 * c0), zk);
+        sc = MfmaOp<DT>::run(kivi_deq8<DT>(c16, sk, zk), qb[s], sc);
+      }
+      float sv[4], bm = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bool valid = nb * 16 + kg * 4 + c < nrows;
+        sv[c] = valid ? sc[c] * P.scale2 : -INFINITY;
+        bm = fmaxf(bm, sv[c]);
+      }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+      const float m_new = fmaxf(m_lane, bm);
+      const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+      m_lane = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float p = __builtin_amdgcn_exp2f(sv[c] - ms);
+        psum += p;
+        if (hl < REP) pl[(nb * 16 + kg * 4 + c) * REP + hl] = p;
+      }
+      l_lane = l_lane * alpha + psum;
+      float al[REP];
+      bool rescale = false;
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        al[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
+        rescale |= al[r] != 1.f;
+      }
+      if (rescale) {
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+#pragma unroll
+          for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
+      }
+      wave_lds_fence();
+#pragma unroll
+      for (int j = 0; j < VPB; j += 2) {
+        const int i = nb * VPB + j;
+        const int ra = i * RPI + my_row0, rbw = (i + 1) * RPI + my_row0;
+        const int grp = my_col * EP / 32;
+        const uint32_t ca = *reinterpret_cast<const uint16_t*>(raw + CB + 4 * D + ra * RB2 + my_col * 2);
+        const uint32_t cb = *reinterpret_cast<const uint16_t*>(raw + CB + 4 * D + rbw * RB2 + my_col * 2);
+        const uint4 va = kivi_deq8_1<DT>(ca, from_bits16<DT>(meta_v[ra * NG + grp]),
+                                         from_bits16<DT>(meta_v[32 * NG + ra * NG + grp]));
+        const uint4 vb = kivi_deq8_1<DT>(cb, from_bits16<DT>(meta_v[rbw * NG + grp]),
+                                         from_bits16<DT>(meta_v[32 * NG + rbw * NG + grp]));
+        float pa[REP], pb[REP];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          pa[r] = pl[ra * REP + r];
+          pb[r] = pl[rbw * REP + r];
+        }
+        pv_pair<DT, REP, EP>(va, vb, pa, pb, acc_o);
+      }
+    }
+    wave_lds_fence();  // the next tile rewrites raw and pl
   }
-  if (tid < REP) {
-    const int r = tid;
-    float M = -INFINITY;
+  float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
+  lsum += __shfl_xor(lsum, 32, kWave);
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][r]);
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
-    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
-    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc;
+  for (int r = 0; r < REP; ++r) {
+    m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
+    l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
   }
+  write_partial<D, REP, NW, SL, EP>(P, wslot, acc_o, m_run, l_head, s_wo, s_wm, s_wl);
 }
 
 // ---------------------------------------------------------------------------
@@ -1002,9 +1248,20 @@ namespace {
 constexpr int kWavesPerItem = 4;
 
 template <int DT, int D, int REP>
-int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int n_groups, hipStream_t st) {
-  hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem), 0,
-                     st, p);
+int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int n_groups, bool kivi,
+                  hipStream_t st) {
+  if constexpr (DT != HALO_F32) {
+    if (kivi) {
+      hipLaunchKernelGGL((decode_attn_kivi_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work),
+                         dim3(64 * kWavesPerItem), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem),
+                         0, st, p);
+    }
+  } else {
+    hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem), 0,
+                       st, p);
+  }
   HALO_CHECK_HIP(hipGetLastError());
   hipLaunchKernelGGL((decode_merge_kernel<D, REP>), dim3(n_groups, REP), dim3(256), 0, st, mp);
   HALO_CHECK_HIP(hipGetLastError());
@@ -1012,25 +1269,25 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
 }
 
 template <int DT, int D>
-int dispatch_rep(const DecodeParams& p, const MergeParams& mp, int rep_t, int n_work, int n_groups,
+int dispatch_rep(const DecodeParams& p, const MergeParams& mp, int rep_t, int n_work, int n_groups, bool kivi,
                  hipStream_t st) {
   switch (rep_t) {
-    case 1: return launch_decode<DT, D, 1>(p, mp, n_work, n_groups, st);
-    case 2: return launch_decode<DT, D, 2>(p, mp, n_work, n_groups, st);
-    case 4: return launch_decode<DT, D, 4>(p, mp, n_work, n_groups, st);
-    case 8: return launch_decode<DT, D, 8>(p, mp, n_work, n_groups, st);
+    case 1: return launch_decode<DT, D, 1>(p, mp, n_work, n_groups, kivi, st);
+    case 2: return launch_decode<DT, D, 2>(p, mp, n_work, n_groups, kivi, st);
+    case 4: return launch_decode<DT, D, 4>(p, mp, n_work, n_groups, kivi, st);
+    case 8: return launch_decode<DT, D, 8>(p, mp, n_work, n_groups, kivi, st);
   }
   set_error("rep_t must be 1, 2, 4 or 8");
   return HALO_E_UNSUPPORTED;
 }
 
 template <int DT>
-int dispatch_d(const DecodeParams& p, const MergeParams& mp, int D, int rep_t, int n_work, int n_groups,
+int dispatch_d(const DecodeParams& p, const MergeParams& mp, int D, int rep_t, int n_work, int n_groups, bool kivi,
                hipStream_t st) {
-  if (D == 64) return dispatch_rep<DT, 64>(p, mp, rep_t, n_work, n_groups, st);
-  if (D == 128) return dispatch_rep<DT, 128>(p, mp, rep_t, n_work, n_groups, st);
+  if (D == 64) return dispatch_rep<DT, 64>(p, mp, rep_t, n_work, n_groups, kivi, st);
+  if (D == 128) return dispatch_rep<DT, 128>(p, mp, rep_t, n_work, n_groups, kivi, st);
   if constexpr (DT != HALO_F32) {
-    if (D == 256) return dispatch_rep<DT, 256>(p, mp, rep_t, n_work, n_groups, st);
+    if (D == 256) return dispatch_rep<DT, 256>(p, mp, rep_t, n_work, n_groups, kivi, st);
   }
   set_error("head_dim must be 64, 128 or 256 (256 for bf16/f16 only)");
   return HALO_E_UNSUPPORTED;
@@ -1044,8 +1301,10 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
                 int rep_t, const halo_chunk_desc* descs, int n_desc, const int32_t* work, int n_work,
                 const int32_t* group_offsets, int n_groups, const int64_t* q_pos, float scale, float* m, float* l,
                 float* o, int64_t acc_stride_b, int acc_mode, void* out, int out_dtype, float* lse, void* workspace,
-                size_t workspace_bytes, const halo_select_cfg* sel, void* stream) {
+                size_t workspace_bytes, const halo_select_cfg* sel, bool kivi, void* stream) {
   HALO_CHECK_ARG(q && descs && work && group_offsets, "null pointer argument");
+  HALO_CHECK_ARG(!kivi || dtype == HALO_F16 || dtype == HALO_BF16, "KIVI chunks need fp16 or bf16 q and scales");
+  HALO_CHECK_ARG(!(kivi && sel), "in-kernel selection is not available for KIVI chunk tables");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0, "need H % H_kv == 0 and positive sizes");
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
   HALO_CHECK_ARG(out == nullptr || out_dtype == HALO_F32 || out_dtype == HALO_BF16 || out_dtype == HALO_F16,
@@ -1120,9 +1379,9 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
   mp.ws_ml = p.ws_ml;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
-    case HALO_F32: return dispatch_d<HALO_F32>(p, mp, D, rep_t, n_work, n_groups, st);
-    case HALO_BF16: return dispatch_d<HALO_BF16>(p, mp, D, rep_t, n_work, n_groups, st);
-    default: return dispatch_d<HALO_F16>(p, mp, D, rep_t, n_work, n_groups, st);
+    case HALO_F32: return dispatch_d<HALO_F32>(p, mp, D, rep_t, n_work, n_groups, kivi, st);
+    case HALO_BF16: return dispatch_d<HALO_BF16>(p, mp, D, rep_t, n_work, n_groups, kivi, st);
+    default: return dispatch_d<HALO_F16>(p, mp, D, rep_t, n_work, n_groups, kivi, st);
   }
 }
 
@@ -1139,7 +1398,7 @@ extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_str
                                 void* workspace, size_t workspace_bytes, void* stream) {
   return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
                      group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
-                     workspace, workspace_bytes, nullptr, stream);
+                     workspace, workspace_bytes, nullptr, false, stream);
 }
 
 extern "C" int halo_decode_attn_tiered(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
@@ -1155,7 +1414,21 @@ extern "C" int halo_decode_attn_tiered(const void* q, int64_t q_stride_b, int64_
   HALO_CHECK_ARG(sel != nullptr, "selection config is null");
   return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
                      group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
-                     workspace, workspace_bytes, sel, stream);
+                     workspace, workspace_bytes, sel, false, stream);
+}
+
+extern "C" int halo_decode_attn_kivi(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                     int B, int H, int H_kv, int D, int rep_t,
+                                     const halo_chunk_desc* descs, int n_desc,
+                                     const int32_t* work, int n_work,
+                                     const int32_t* group_offsets, int n_groups,
+                                     const int64_t* q_pos, float scale,
+                                     float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                                     void* out, int out_dtype, float* lse,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
+                     group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
+                     workspace, workspace_bytes, nullptr, true, stream);
 }
 
 extern "C" int halo_finalize(const float* m, const float* l, const float* o, int B, int H, int D,

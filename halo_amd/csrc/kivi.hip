@@ -1,0 +1,275 @@
+// KIVI-style 2/4-bit cold-chunk format: quantize and dequantize kernels
+// (gfx950, wave64).  Byte/integer work bound by HBM; nothing here is a GEMM.
+//
+// Arithmetic: baselines/kivi_cache.py:44-78 with every operation rounded to
+// the storage dtype as torch evaluates a chain of fp16/bf16 tensor ops:
+//   scale = dtype(dtype(max(dtype(x_max - x_min), dtype(1e-8))) / qmax)
+//   zero  = x_min
+//   code  = clamp(rint(dtype(dtype(x - zero) / scale)), 0, qmax), NaN -> 0
+//   x'    = dtype(fp32(fp32(code) * fp32(scale)) + fp32(zero))
+// (built with -ffp-contract=off: no fused multiply-add anywhere).
+// K is grouped per channel over 32 consecutive tokens, V per token over 32
+// consecutive channels (the reference groups along the last axis only,
+// kivi_cache.py:56; K per-channel applies the same per-element arithmetic
+// along the token axis).
+//
+// Block layout (one block = 32 tokens of one (b, h_kv); byte offsets):
+//   [0, C)            K codes, token-major rows of D*bits/8 bytes, code of
+//                     channel d at bit (d*bits) % 8 of byte d*bits/8
+//   [C, C+2D)         K scale, D elements of the dtype (per channel)
+//   [C+2D, C+4D)      K zero
+//   [C+4D, 2C+4D)     V codes, same packing
+//   [2C+4D, 2C+6D)    V scale, 32 tokens x D/32 groups (token-major)
+//   [2C+6D, 2C+8D)    V zero
+// with C = 32*D*bits/8.  D=128, bits=2: 3072 bytes per block.
+
+#include "common.hpp"
+
+namespace halo {
+
+constexpr int kKiviG = 32;
+
+__host__ __device__ constexpr int kivi_code_bytes(int D, int bits) { return kKiviG * D * bits / 8; }
+__host__ __device__ constexpr int kivi_block_bytes(int D, int bits) { return 2 * kivi_code_bytes(D, bits) + 8 * D; }
+
+template <int DT>
+__device__ __forceinline__ float round_dt(float x) {
+  if constexpr (DT == HALO_BF16) return __uint_as_float((uint32_t)f32_to_bf16_rne(x) << 16);
+  return f16_bits_to_f32(f32_to_f16_rne(x));
+}
+template <int DT>
+__device__ __forceinline__ uint16_t bits_dt(float x) {
+  if constexpr (DT == HALO_BF16) return f32_to_bf16_rne(x);
+  return f32_to_f16_rne(x);
+}
+template <int DT>
+__device__ __forceinline__ float from_bits(uint16_t h) {
+  if constexpr (DT == HALO_BF16) return __uint_as_float((uint32_t)h << 16);
+  return f16_bits_to_f32(h);
+}
+
+// scale/zero of one group from its (dtype-exact) min and max
+template <int DT, int BITS>
+__device__ __forceinline__ void kivi_params(float mn, float mx, float& scale, float& zero) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const float eps = round_dt<DT>(1e-8f);
+  float rng = round_dt<DT>(opaque(mx - mn));
+  rng = round_dt<DT>(fmaxf(rng, eps));
+  scale = round_dt<DT>(opaque(rng / qmax));
+  zero = mn;
+}
+template <int DT, int BITS>
+__device__ __forceinline__ uint32_t kivi_code(float x, float scale, float zero) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const float diff = round_dt<DT>(opaque(x - zero));
+  float ratio = round_dt<DT>(opaque(diff / scale));
+  if (ratio != ratio) ratio = 0.f;
+  const float c = fminf(fmaxf(rintf(ratio), 0.f), qmax);
+  return (uint32_t)c;
+}
+
+struct KiviQuantParams {
+  const void* k;
+  int64_t ksb, ksh, kst;
+  const void* v;
+  int64_t vsb, vsh, vst;
+  int H_kv, n_blk;
+  uint8_t* blocks;
+  int64_t bsb, bsh;  // bytes
+};
+
+// One workgroup per block: stage the 32 x D K and V tiles in LDS as fp32,
+// per-group min/max, codes, then packed bytes with coalesced stores.
+template <int DT, int D, int BITS>
+__global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
+  constexpr int G = kKiviG;
+  constexpr int C = kivi_code_bytes(D, BITS);
+  constexpr int CPB = 8 / BITS;  // codes per byte
+  constexpr int NG = D / G;      // V groups per token
+  __shared__ float s_k[G][D + 1], s_v[G][D + 1];
+  __shared__ uint8_t s_ck[G * D], s_cv[G * D];
+  __shared__ uint16_t s_ks[D], s_kz[D], s_vs[G * NG], s_vz[G * NG];
+  const int tid = threadIdx.x;
+  const int j = blockIdx.x % P.n_blk;
+  const int bh = blockIdx.x / P.n_blk;
+  const int h = bh % P.H_kv, b = bh / P.H_kv;
+  const uint16_t* kb = reinterpret_cast<const uint16_t*>(P.k) + (int64_t)b * P.ksb + (int64_t)h * P.ksh +
+                       (int64_t)j * G * P.kst;
+  const uint16_t* vb = reinterpret_cast<const uint16_t*>(P.v) + (int64_t)b * P.vsb + (int64_t)h * P.vsh +
+                       (int64_t)j * G * P.vst;
+  for (int e = tid; e < G * D; e += 256) {
+    const int t = e / D, d = e % D;
+    s_k[t][d] = from_bits<DT>(kb[(int64_t)t * P.kst + d]);
+    s_v[t][d] = from_bits<DT>(vb[(int64_t)t * P.vst + d]);
+  }
+  __syncthreads();
+  // K: per channel over the 32 tokens
+  for (int d = tid; d < D; d += 256) {
+    float mn = s_k[0][d], mx = s_k[0][d];
+    for (int t = 1; t < G; ++t) {
+      mn = fminf(mn, s_k[t][d]);
+      mx = fmaxf(mx, s_k[t][d]);
+    }
+    float sc, z;
+    kivi_params<DT, BITS>(mn, mx, sc, z);
+    s_ks[d] = bits_dt<DT>(sc);
+    s_kz[d] = bits_dt<DT>(z);
+    for (int t = 0; t < G; ++t) s_ck[t * D + d] = (uint8_t)kivi_code<DT, BITS>(s_k[t][d], sc, z);
+  }
+  // V: per token over groups of 32 channels
+  for (int i = tid; i < G * NG; i += 256) {
+    const int t = i / NG, g = i % NG;
+    float mn = s_v[t][g * G], mx = mn;
+    for (int c = 1; c < G; ++c) {
+      mn = fminf(mn, s_v[t][g * G + c]);
+      mx = fmaxf(mx, s_v[t][g * G + c]);
+    }
+    float sc, z;
+    kivi_params<DT, BITS>(mn, mx, sc, z);
+    s_vs[i] = bits_dt<DT>(sc);
+    s_vz[i] = bits_dt<DT>(z);
+    for (int c = 0; c < G; ++c) s_cv[t * D + g * G + c] = (uint8_t)kivi_code<DT, BITS>(s_v[t][g * G + c], sc, z);
+  }
+  __syncthreads();
+  uint8_t* out = P.blocks + (int64_t)b * P.bsb + (int64_t)h * P.bsh + (int64_t)j * kivi_block_bytes(D, BITS);
+  for (int q = tid; q < C; q += 256) {
+    uint32_t wk = 0, wv = 0;
+#pragma unroll
+    for (int c = 0; c < CPB; ++c) {
+      wk |= (uint32_t)s_ck[q * CPB + c] << (c * BITS);
+      wv |= (uint32_t)s_cv[q * CPB + c] << (c * BITS);
+    }
+    out[q] = (uint8_t)wk;
+    out[C + 4 * D + q] = (uint8_t)wv;
+  }
+  uint16_t* meta_k = reinterpret_cast<uint16_t*>(out + C);
+  uint16_t* meta_v = reinterpret_cast<uint16_t*>(out + 2 * C + 4 * D);
+  for (int d = tid; d < D; d += 256) {
+    meta_k[d] = s_ks[d];
+    meta_k[D + d] = s_kz[d];
+  }
+  for (int i = tid; i < G * NG; i += 256) {
+    meta_v[i] = s_vs[i];
+    meta_v[G * NG + i] = s_vz[i];
+  }
+}
+
+struct KiviDequantParams {
+  const uint8_t* blocks;
+  int64_t bsb, bsh;
+  int H_kv, n_blk;
+  void* k;
+  int64_t ksb, ksh, kst;
+  void* v;
+  int64_t vsb, vsh, vst;
+};
+
+// One workgroup per block; one thread per (token, 8-channel piece) of K and V.
+template <int DT, int D, int BITS>
+__global__ void __launch_bounds__(256) kivi_dequant_kernel(KiviDequantParams P) {
+  constexpr int G = kKiviG;
+  constexpr int C = kivi_code_bytes(D, BITS);
+  constexpr int NG = D / G;
+  constexpr uint32_t MASK = (1u << BITS) - 1;
+  const int tid = threadIdx.x;
+  const int j = blockIdx.x % P.n_blk;
+  const int bh = blockIdx.x / P.n_blk;
+  const int h = bh % P.H_kv, b = bh / P.H_kv;
+  const uint8_t* blk = P.blocks + (int64_t)b * P.bsb + (int64_t)h * P.bsh + (int64_t)j * kivi_block_bytes(D, BITS);
+  const uint16_t* meta_k = reinterpret_cast<const uint16_t*>(blk + C);
+  const uint16_t* meta_v = reinterpret_cast<const uint16_t*>(blk + 2 * C + 4 * D);
+  uint16_t* ko = reinterpret_cast<uint16_t*>(P.k) + (int64_t)b * P.ksb + (int64_t)h * P.ksh + (int64_t)j * G * P.kst;
+  uint16_t* vo = reinterpret_cast<uint16_t*>(P.v) + (int64_t)b * P.vsb + (int64_t)h * P.vsh + (int64_t)j * G * P.vst;
+  for (int e = tid; e < G * D; e += 256) {
+    const int t = e / D, d = e % D;
+    const int bit = d * BITS;
+    const uint32_t ck = (blk[t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
+    const uint32_t cv = (blk[C + 4 * D + t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
+    const float sk = from_bits<DT>(meta_k[d]), zk = from_bits<DT>(meta_k[D + d]);
+    const float sv = from_bits<DT>(meta_v[t * NG + d / G]), zv = from_bits<DT>(meta_v[G * NG + t * NG + d / G]);
+    // both fp32 results are materialised so the conversion rounds the fp32
+    // sum (no mixed-precision fused add-and-convert)
+    ko[(int64_t)t * P.kst + d] = bits_dt<DT>(opaque(opaque((float)ck * sk) + zk));
+    vo[(int64_t)t * P.vst + d] = bits_dt<DT>(opaque(opaque((float)cv * sv) + zv));
+  }
+}
+
+}  // namespace halo
+
+using namespace halo;
+
+extern "C" size_t halo_kivi_block_bytes(int D, int bits) {
+  if ((bits != 2 && bits != 4) || D <= 0 || D % kKiviG) return 0;
+  return (size_t)kivi_block_bytes(D, bits);
+}
+
+namespace {
+
+template <int DT, int D>
+int quant_bits(const KiviQuantParams& p, int bits, int n, hipStream_t st) {
+  if (bits == 2) hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 2>), dim3(n), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  HALO_CHECK_HIP(hipGetLastError());
+  return HALO_OK;
+}
+template <int DT, int D>
+int dequant_bits(const KiviDequantParams& p, int bits, int n, hipStream_t st) {
+  if (bits == 2) hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 2>), dim3(n), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  HALO_CHECK_HIP(hipGetLastError());
+  return HALO_OK;
+}
+
+}  // namespace
+
+extern "C" int halo_kivi_quantize(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                  const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                  int dtype, int B, int H_kv, int T, int D, int bits,
+                                  void* blocks, int64_t blk_stride_b, int64_t blk_stride_h, void* stream) {
+  HALO_CHECK_ARG(k && v && blocks, "null pointer");
+  HALO_CHECK_ARG(dtype == HALO_F16 || dtype == HALO_BF16, "KIVI storage dtype must be fp16 or bf16");
+  HALO_CHECK_ARG(bits == 2 || bits == 4, "bits must be 2 or 4");
+  HALO_CHECK_ARG(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+  HALO_CHECK_ARG(B >= 0 && H_kv > 0 && T >= 0 && T % kKiviG == 0, "T must be a multiple of the group size 32");
+  const int n_blk = T / kKiviG;
+  const int64_t n = (int64_t)B * H_kv * n_blk;
+  if (n == 0) return HALO_OK;
+  HALO_CHECK_ARG(n < (1ll << 31), "too many blocks");
+  KiviQuantParams p{k, k_stride_b, k_stride_h, k_stride_t, v, v_stride_b, v_stride_h, v_stride_t,
+                    H_kv, n_blk, reinterpret_cast<uint8_t*>(blocks), blk_stride_b, blk_stride_h};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == HALO_F16) {
+    if (D == 64) return quant_bits<HALO_F16, 64>(p, bits, (int)n, st);
+    if (D == 128) return quant_bits<HALO_F16, 128>(p, bits, (int)n, st);
+    return quant_bits<HALO_F16, 256>(p, bits, (int)n, st);
+  }
+  if (D == 64) return quant_bits<HALO_BF16, 64>(p, bits, (int)n, st);
+  if (D == 128) return quant_bits<HALO_BF16, 128>(p, bits, (int)n, st);
+  return quant_bits<HALO_BF16, 256>(p, bits, (int)n, st);
+}
+
+extern "C" int halo_kivi_dequantize(const void* blocks, int64_t blk_stride_b, int64_t blk_stride_h,
+                                    int dtype, int B, int H_kv, int n_blocks, int D, int bits,
+                                    void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                                    void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                                    void* stream) {
+  HALO_CHECK_ARG(k && v && blocks, "null pointer");
+  HALO_CHECK_ARG(dtype == HALO_F16 || dtype == HALO_BF16, "KIVI storage dtype must be fp16 or bf16");
+  HALO_CHECK_ARG(bits == 2 || bits == 4, "bits must be 2 or 4");
+  HALO_CHECK_ARG(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+  HALO_CHECK_ARG(B >= 0 && H_kv > 0 && n_blocks >= 0, "bad sizes");
+  const int64_t n = (int64_t)B * H_kv * n_blocks;
+  if (n == 0) return HALO_OK;
+  HALO_CHECK_ARG(n < (1ll << 31), "too many blocks");
+  KiviDequantParams p{reinterpret_cast<const uint8_t*>(blocks), blk_stride_b, blk_stride_h, H_kv, n_blocks,
+                      k, k_stride_b, k_stride_h, k_stride_t, v, v_stride_b, v_stride_h, v_stride_t};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == HALO_F16) {
+    if (D == 64) return dequant_bits<HALO_F16, 64>(p, bits, (int)n, st);
+    if (D == 128) return dequant_bits<HALO_F16, 128>(p, bits, (int)n, st);
+    return dequant_bits<HALO_F16, 256>(p, bits, (int)n, st);
+  }
+  if (D == 64) return dequant_bits<HALO_BF16, 64>(p, bits, (int)n, st);
+  if (D == 128) return dequant_bits<HALO_BF16, 128>(p, bits, (int)n, st);
+  return dequant_bits<HALO_BF16, 256>(p, bits, (int)n, st);
+}

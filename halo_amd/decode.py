@@ -70,10 +70,14 @@ class DecodePlan:
     rows: int                    # attended K/V rows summed over (b, h_kv)
     keep: list = field(default_factory=list)  # tensors the descriptors point at
     work_host: Optional[np.ndarray] = None
+    kivi: bool = False           # every chunk is a run of 2-bit KIVI blocks
 
     @property
     def kv_bytes(self) -> int:
         """Algorithmic K+V bytes one launch streams (every row read once)."""
+        if self.kivi:
+            from .kivi import GROUP, block_bytes
+            return self.rows // GROUP * block_bytes(self.D)
         esz = torch.tensor([], dtype=self.dtype).element_size()
         return self.rows * 2 * self.D * esz
 
@@ -132,6 +136,9 @@ def pack_descs(chunks: Sequence[ChunkRef], *, B: int, H_kv: int, D: int, dtype: 
     descs = np.zeros(len(chunks), dtype=DESC_DTYPE)
     keep = []
     for i, c in enumerate(chunks):
+        if hasattr(c, "blocks"):
+            keep.append(_pack_kivi(descs[i], c, i, B=B, H_kv=H_kv, D=D, dtype=dtype))
+            continue
         k, v = c.k, c.v
         if k.dtype != dtype or v.dtype != dtype:
             raise AssertionError(f"chunk {i}: dtype {k.dtype}/{v.dtype} != {dtype}")
@@ -165,6 +172,38 @@ def pack_descs(chunks: Sequence[ChunkRef], *, B: int, H_kv: int, D: int, dtype: 
     return descs, keep
 
 
+def _pack_kivi(d, c, i: int, *, B: int, H_kv: int, D: int, dtype: torch.dtype) -> torch.Tensor:
+    """Descriptor of a run of KIVI blocks (kivi.KiviChunkRef): ``k`` is the
+    first block, strides are in bytes, the v fields are unused."""
+    from .kivi import GROUP, block_bytes
+    blk = c.blocks
+    bb = block_bytes(D, c.bits)
+    if c.bits != 2:
+        raise AssertionError(f"chunk {i}: decode attention reads 2-bit KIVI blocks, got bits={c.bits}")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise AssertionError(f"chunk {i}: KIVI chunks need an fp16 or bf16 query, got {dtype}")
+    if blk.dtype != torch.uint8 or blk.shape[-1] != bb or blk.stride(-1) != 1 or blk.stride(-2) != bb:
+        raise AssertionError(f"chunk {i}: blocks must be uint8 (..., n, {bb}) with contiguous blocks")
+    if c.batch < 0:
+        if blk.dim() != 4 or blk.shape[0] != B or blk.shape[1] != H_kv:
+            raise AssertionError(f"chunk {i}: blocks shape {tuple(blk.shape)} != ({B}, {H_kv}, n, {bb})")
+        ssb, ssh = blk.stride(0), blk.stride(1)
+    else:
+        if blk.dim() != 3 or blk.shape[0] != H_kv or not 0 <= c.batch < B:
+            raise AssertionError(f"ragged chunk {i}: expected blocks (H_kv, n, {bb}) of a row in [0, {B})")
+        ssb, ssh = 0, blk.stride(0)
+    if blk.data_ptr() % 16 or ssb % 16 or ssh % 16:
+        raise AssertionError(f"chunk {i}: KIVI blocks must be 16-byte aligned")
+    d["k"], d["v"] = blk.data_ptr(), 0
+    d["ksb"], d["ksh"], d["kst"] = ssb, ssh, bb
+    d["vsb"], d["vsh"], d["vst"] = 0, 0, 0
+    d["start"] = int(c.chunk_start)
+    d["T"] = int(blk.shape[-2]) * GROUP
+    d["flags"] = (nat.CHUNK_CAUSAL if c.causal else 0) | nat.CHUNK_KIVI2
+    d["batch"] = int(c.batch)
+    return blk
+
+
 def descs_to_device(descs: np.ndarray, device) -> torch.Tensor:
     return _to_device(descs.view(np.uint8).copy(), device)
 
@@ -195,6 +234,12 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
     n_groups = B * H_kv * n_sub
 
     descs, keep = pack_descs(chunks, B=B, H_kv=H_kv, D=D, dtype=dtype)
+    kinds = {hasattr(c, "blocks") for c in chunks}
+    if len(kinds) > 1:
+        raise AssertionError("a plan holds either plain or KIVI chunks; merge the two through accumulators")
+    kivi = kinds == {True}
+    if kivi and split is not None and split % 32:
+        raise AssertionError(f"split={split} must be a multiple of the 32-token KIVI block")
 
     def live(c: ChunkRef, b: int) -> bool:
         if c.batch >= 0 and c.batch != b:
@@ -247,7 +292,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
         descs=dev_descs, work=_to_device(work_np.reshape(-1), device),
         offsets=_to_device(np.asarray(offsets, dtype=np.int32), device),
         n_desc=len(chunks), n_work=len(work), n_groups=n_groups,
-        rows=rows_attended, keep=keep, work_host=work_np,
+        rows=rows_attended, keep=keep, work_host=work_np, kivi=kivi,
     )
 
 
@@ -321,7 +366,11 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse),
         ws.data_ptr(), ws.numel(),
     )
-    if select is None:
+    if plan.kivi:
+        if select is not None:
+            raise AssertionError("in-kernel selection is not available for KIVI chunk tables")
+        nat.check(L.halo_decode_attn_kivi(*args, sp), "halo_decode_attn_kivi")
+    elif select is None:
         nat.check(L.halo_decode_attn(*args, sp), "halo_decode_attn")
     else:
         nat.check(L.halo_decode_attn_tiered(*args, ctypes.byref(select), sp), "halo_decode_attn_tiered")

@@ -37,6 +37,8 @@ extern "C" {
 
 /* ---- chunk descriptor flags -------------------------------------------- */
 #define HALO_CHUNK_CAUSAL 1   /* mask rows with chunk_start + t > q_pos[b] */
+#define HALO_CHUNK_KIVI2  2   /* a run of 2-bit KIVI blocks (halo_decode_attn_kivi):
+                                 k = first block, k_stride_b/h in bytes, v unused */
 
 /*
  * One KV chunk: rows [0, T_c) of K and V at global key positions
@@ -61,13 +63,14 @@ typedef struct halo_chunk_desc {
 } halo_chunk_desc; /* 88 bytes */
 
 /*
- * Work decomposition for one decode-attention launch.  Work item i (int32 x4):
- *   { desc index, group, t0, t1 }  -- rows [t0, t1) of chunk `desc` for
- * query-head group `group` = (b * H_kv + h_kv) * n_sub + sub, where sub
- * selects q heads [h_kv*rep + sub*rep_t, ...) of that KV head.  Items of one
- * group are contiguous; group_offsets[g] .. group_offsets[g+1] is group g's
- * item range and every group owns at least one item (an item with t0 == t1
- * is an empty partial).
+ * Work decomposition for one decode-attention launch.  Work record i (int32 x8):
+ *   { desc index, group, t0, t1, slot, 0, 0, 0 }  -- rows [t0, t1) of chunk
+ * `desc` for query-head group `group` = (b * H_kv + h_kv) * n_sub + sub, where
+ * sub selects q heads [h_kv*rep + sub*rep_t, ...) of that KV head; the item's
+ * partial goes to workspace slot `slot`.  Group g's partials occupy slots
+ * group_offsets[g] .. group_offsets[g+1]-1, and every group owns at least one
+ * item (an item with t0 == t1 is an empty partial).  Records are in dispatch
+ * order, which need not follow the slot order.
  */
 
 /* Bytes of workspace a launch with `n_work` items needs (one partial per item). */
@@ -222,6 +225,68 @@ int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int normalize, float alpha, float beta, float gamma,
                           int refresh, int sink_pages, int P_total,
                           void* stream);
+
+/* ---- KIVI 2/4-bit cold-chunk format ------------------------------------ */
+
+/*
+ * Block format: one block = 32 tokens of one (b, h_kv), all in one
+ * contiguous record of halo_kivi_block_bytes(D, bits) bytes:
+ *   K codes   32 token rows of D*bits/8 bytes (code of channel d at bit
+ *             (d*bits) % 8 of byte d*bits/8; K is grouped per channel over
+ *             the block's 32 tokens)
+ *   K scale   D elements of the storage dtype, then K zero (D elements)
+ *   V codes   as K codes (V is grouped per token over 32 channels)
+ *   V scale   32 x D/32 elements (token-major), then V zero (same)
+ * D=128, bits=2: 3072 bytes per block (5.33x smaller than fp16 K+V).
+ * The reference keeps unpacked int8 codes plus separate scale/zero tensors
+ * (baselines/kivi_cache.py:50-69, :121-195); this layout is this library's.
+ */
+size_t halo_kivi_block_bytes(int D, int bits);
+
+/*
+ * Quantise K and V (B, H_kv, T, D) of `dtype` (fp16 or bf16; element strides)
+ * into blocks[b*blk_stride_b + h*blk_stride_h + j*block_bytes] (byte
+ * strides), T % 32 == 0.  Per group: scale = dtype(dtype(max(dtype(x_max -
+ * x_min), dtype(1e-8))) / qmax), zero = x_min, code = clamp(rint(dtype(
+ * dtype(x - zero) / scale)), 0, qmax) with NaN -> 0.  Replaces
+ * _quantize_per_group (baselines/kivi_cache.py:44-69).
+ */
+int halo_kivi_quantize(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                       const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                       int dtype, int B, int H_kv, int T, int D, int bits,
+                       void* blocks, int64_t blk_stride_b, int64_t blk_stride_h, void* stream);
+
+/*
+ * Dequantise n_blocks blocks per (b, h_kv) into K and V of `dtype`:
+ * x = dtype(fp32(fp32(code) * fp32(scale)) + fp32(zero)), bit-exact with
+ * _dequantize_per_group (baselines/kivi_cache.py:72-78).
+ */
+int halo_kivi_dequantize(const void* blocks, int64_t blk_stride_b, int64_t blk_stride_h,
+                         int dtype, int B, int H_kv, int n_blocks, int D, int bits,
+                         void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                         void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                         void* stream);
+
+/*
+ * halo_decode_attn over a table of KIVI chunks (flags HALO_CHUNK_KIVI2, 2-bit
+ * blocks of halo_kivi_quantize, scales in `dtype`, which must be fp16 or
+ * bf16): every block is dequantised in registers with the arithmetic of
+ * halo_kivi_dequantize, so scores and outputs see exactly the dequantised
+ * cache.  Same arguments and accumulator contract as halo_decode_attn; a
+ * layer whose recent rows are unquantised runs this call with acc_mode 2 and
+ * a halo_decode_attn over the recent rows with acc_mode 1.  Work items must
+ * start on 32-token block boundaries.  Replaces the dequantise-and-concat of
+ * KIVICache.update (baselines/kivi_cache.py:187-195) followed by attention.
+ */
+int halo_decode_attn_kivi(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                          int B, int H, int H_kv, int D, int rep_t,
+                          const halo_chunk_desc* descs, int n_desc,
+                          const int32_t* work, int n_work,
+                          const int32_t* group_offsets, int n_groups,
+                          const int64_t* q_pos, float scale,
+                          float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                          void* out, int out_dtype, float* lse,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- build metadata ---------------------------------------------------- */
 const char* halo_last_error(void);

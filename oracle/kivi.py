@@ -96,3 +96,90 @@ def dequant_k(codes, scale, zero, *, group_size: int, dtype: str) -> np.ndarray:
     s = np.repeat(scale, group_size, axis=-2)
     z = np.repeat(zero, group_size, axis=-2)
     return dequantize(codes, s, z, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# Packed block layout of this build (the reference stores unpacked int8 codes,
+# kivi_cache.py:50-53).  One block = 32 tokens of one (b, h_kv):
+#   K codes (32 x D*bits/8), K scale (D), K zero (D), V codes (32 x D*bits/8),
+#   V scale (32 x D/32), V zero (32 x D/32); scales/zeros in the storage dtype;
+#   code of channel d at bit (d*bits) % 8 of byte d*bits/8 of its token row.
+# ---------------------------------------------------------------------------
+GROUP = 32
+
+
+def block_bytes(D: int, bits: int) -> int:
+    return 2 * GROUP * D * bits // 8 + 8 * D
+
+
+def _dtype_bits(x: np.ndarray, dtype: str) -> np.ndarray:
+    from .inputs import f32_to_bf16_bits
+    x = np.asarray(x, np.float32)
+    if dtype == "float16":
+        return x.astype(np.float16).view(np.uint16)
+    return f32_to_bf16_bits(x)
+
+
+def _bits_to_f32(b: np.ndarray, dtype: str) -> np.ndarray:
+    from .inputs import bf16_bits_to_f32
+    b = np.asarray(b, np.uint16)
+    if dtype == "float16":
+        return b.view(np.float16).astype(np.float32)
+    return bf16_bits_to_f32(b)
+
+
+def _pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """codes (..., D) uint8 -> (..., D*bits/8) bytes, low bits = lower index."""
+    per = 8 // bits
+    c = codes.reshape(*codes.shape[:-1], codes.shape[-1] // per, per).astype(np.uint32)
+    out = np.zeros(c.shape[:-1], np.uint32)
+    for i in range(per):
+        out |= c[..., i] << (i * bits)
+    return out.astype(np.uint8)
+
+
+def _unpack_codes(packed: np.ndarray, bits: int) -> np.ndarray:
+    per = 8 // bits
+    p = packed.astype(np.uint32)[..., None]
+    sh = (np.arange(per, dtype=np.uint32) * bits)
+    return ((p >> sh) & ((1 << bits) - 1)).reshape(*packed.shape[:-1], packed.shape[-1] * per).astype(np.uint8)
+
+
+def pack_blocks(k: np.ndarray, v: np.ndarray, *, bits: int, dtype: str) -> np.ndarray:
+    """k, v (B, H_kv, T, D) dtype-exact float32, T % 32 == 0 -> uint8
+    (B, H_kv, T/32, block_bytes): K per-channel and V per-token groups of 32."""
+    B, H, T, D = k.shape
+    nb = T // GROUP
+    ck, sk, zk = quantize_k_per_channel(k, bits=bits, group_size=GROUP, dtype=dtype)   # sk (B,H,nb,D)
+    cv, sv, zv = quantize_v_per_token(v, bits=bits, group_size=GROUP, dtype=dtype)     # sv (B,H,T,D/32)
+    ck = ck.reshape(B, H, nb, GROUP, D)
+    cv = cv.reshape(B, H, nb, GROUP, D)
+    parts = [
+        _pack_codes(ck, bits).reshape(B, H, nb, -1),
+        _dtype_bits(sk, dtype).view(np.uint8).reshape(B, H, nb, -1),
+        _dtype_bits(zk, dtype).view(np.uint8).reshape(B, H, nb, -1),
+        _pack_codes(cv, bits).reshape(B, H, nb, -1),
+        _dtype_bits(sv.reshape(B, H, nb, GROUP * D // GROUP), dtype).view(np.uint8).reshape(B, H, nb, -1),
+        _dtype_bits(zv.reshape(B, H, nb, GROUP * D // GROUP), dtype).view(np.uint8).reshape(B, H, nb, -1),
+    ]
+    out = np.concatenate(parts, axis=-1)
+    assert out.shape[-1] == block_bytes(D, bits)
+    return np.ascontiguousarray(out)
+
+
+def unpack_blocks(blocks: np.ndarray, *, D: int, bits: int, dtype: str):
+    """Inverse of pack_blocks through the dequant arithmetic: returns the
+    dequantised (k, v) (B, H_kv, T, D) as dtype-exact float32."""
+    B, H, nb, nbytes = blocks.shape
+    C = GROUP * D * bits // 8
+    assert nbytes == block_bytes(D, bits)
+    o = 0
+    ck = _unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, GROUP, D * bits // 8), bits); o += C
+    sk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
+    zk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
+    cv = _unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, GROUP, D * bits // 8), bits); o += C
+    sv = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype).reshape(B, H, nb, GROUP, D // GROUP); o += 2 * D
+    zv = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype).reshape(B, H, nb, GROUP, D // GROUP)
+    k = dequantize(ck, sk[:, :, :, None, :], zk[:, :, :, None, :], dtype=dtype)
+    v = dequantize(cv, np.repeat(sv, GROUP, axis=-1), np.repeat(zv, GROUP, axis=-1), dtype=dtype)
+    return k.reshape(B, H, nb * GROUP, D), v.reshape(B, H, nb * GROUP, D)

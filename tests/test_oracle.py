@@ -313,3 +313,40 @@ def test_kivi_per_channel_k_groups_tokens():
     np.testing.assert_array_equal(z[0, 1, 1], k[0, 1, 32:64].min(0))
     dq = KV.dequant_k(codes, s, z, group_size=32, dtype="float32")
     assert np.abs(dq - k).max() <= (s.max() * 0.5 + 1e-6)
+
+
+def test_kivi_block_layout_known_answer():
+    """Block layout pinned by hand-built values: channel 0 of K ramps 0,1,2,3
+    over the tokens (scale 1, zero 0, codes t % 4 in bits 0-1 of each row's
+    first byte); V token 0 channels 0..31 ramp likewise per token group."""
+    from oracle import kivi as K
+    D = 64
+    k = np.zeros((1, 1, 32, D), np.float32)
+    v = np.zeros((1, 1, 32, D), np.float32)
+    k[0, 0, :, 0] = np.arange(32) % 4
+    v[0, 0, 0, :32] = np.arange(32) % 4
+    blk = K.pack_blocks(k, v, bits=2, dtype="float16")
+    assert blk.shape == (1, 1, 1, K.block_bytes(D, 2)) == (1, 1, 1, 2 * 32 * 16 + 8 * D)
+    b = blk[0, 0, 0]
+    rowb = D * 2 // 8
+    assert [int(b[t * rowb]) & 3 for t in range(32)] == [t % 4 for t in range(32)]
+    C = 32 * rowb
+    ks = b[C:C + 2 * D].view(np.float16)
+    assert ks[0] == np.float16(1.0) and ks[1] == np.float16(0.0)   # range 0 -> fp16 floor 0
+    vc = C + 4 * D
+    first = b[vc:vc + 8]                                            # token 0, channels 0..31
+    codes = [(int(first[i // 4]) >> (2 * (i % 4))) & 3 for i in range(32)]
+    assert codes == [i % 4 for i in range(32)]
+    vs = b[2 * C + 4 * D:2 * C + 6 * D].view(np.float16)
+    assert vs[0] == np.float16(1.0)
+
+
+def test_kivi_blocks_roundtrip_equals_dequant():
+    from oracle import kivi as K
+    from oracle.inputs import decode_inputs
+    x = decode_inputs(4, B=1, H=4, H_kv=2, T=96, D=128, dtype="float16", n_planted=2, sigma=10.0)
+    kd, vd = K.unpack_blocks(K.pack_blocks(x.k, x.v, bits=2, dtype="float16"), D=128, bits=2, dtype="float16")
+    ck, sk, zk = K.quantize_k_per_channel(x.k, bits=2, group_size=32, dtype="float16")
+    cv, sv, zv = K.quantize_v_per_token(x.v, bits=2, group_size=32, dtype="float16")
+    assert np.array_equal(kd, K.dequant_k(ck, sk, zk, group_size=32, dtype="float16"))
+    assert np.array_equal(vd, K.dequant_v(cv, sv, zv, group_size=32, dtype="float16"))

@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode attn tokens/s + achieved HBM GB/s, 8B-shape GQA @32k ctx, hot_ratio 0.25"
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def log(msg: str) -> None:
@@ -201,6 +202,122 @@ def pcie_inclusive(torch, layers, qs, *, steps, scale):
     }
 
 
+def bench_prefill_c3(torch, dev, *, reps: int):
+    """Chunked causal prefill, Llama-3-8B GQA shape: a 4096-token query block
+    attends 28 prior chunks of 1024 rows plus itself (causal), bf16 MFMA.
+    Algorithmic work 2,061,617,856,512 FLOP (causal half of the self block)."""
+    from halo_amd.decode import ChunkRef
+    from halo_amd.prefill import prefill_attention
+
+    H, H_kv, D, T_q, T_prior, chunk = 32, 8, 128, 4096, 28672, 1024
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    q = torch.randn((1, H, T_q, D), generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn((1, H_kv, T_prior + T_q, D), generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn((1, H_kv, T_prior + T_q, D), generator=gen, device=dev).to(torch.bfloat16)
+    chunks = [ChunkRef(k[:, :, s:s + chunk], v[:, :, s:s + chunk], s, False) for s in range(0, T_prior, chunk)]
+    chunks.append(ChunkRef(k[:, :, T_prior:], v[:, :, T_prior:], T_prior, True))
+    for _ in range(2):
+        prefill_attention(q, chunks)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        prefill_attention(q, chunks)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flops = 4 * H * D * T_q * T_prior + 2 * H * D * T_q * (T_q + 1)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "workload": "chunked causal prefill, bf16, 32/8 heads, d128, 4096 query rows over 28x1024 prior + "
+                    "4096 self (causal), one launch",
+        "ms_per_call": ms, "flop_per_call": flops, "tflops": tflops,
+        "roofline": {"bound": "mfma", "kernel": "prefill_attn_kernel<bf16,128>", "achieved": tflops,
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / MFMA_BF16_PEAK_TFLOPS},
+    }
+
+
+def bench_kivi_c5(torch, dev, *, steps: int, layers: int = 28):
+    """KIVI 2-bit cold tier, Qwen2-7B shape: 28/4 heads, d128, 131072
+    context; all but the last 128 tokens in 2-bit blocks (K per channel, V per
+    token, group 32, fp16 scale/zero), dequantised inside the decode kernel;
+    the 128 recent tokens fp16.  28 layers with distinct buffers, one HIP
+    graph per step."""
+    from halo_amd import kivi
+    from halo_amd.decode import ChunkRef
+
+    H, H_kv, D, T, resid = 28, 4, 128, 131072, 128
+    T_cold = T - resid
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    lays, qs = [], []
+    for _ in range(layers):
+        k = torch.randn((1, H_kv, T, D), generator=gen, device=dev)
+        ch = torch.randperm(D, generator=gen, device=dev)[:2]
+        k[..., ch] *= 10.0
+        k = k.to(torch.float16)
+        v = torch.randn((1, H_kv, T, D), generator=gen, device=dev).to(torch.float16)
+        blocks = kivi.quantize(k[:, :, :T_cold], v[:, :, :T_cold])
+        kr, vr = k[:, :, T_cold:].clone(), v[:, :, T_cold:].clone()
+        del k, v
+        lays.append(kivi.KiviDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.float16, cold_blocks=blocks,
+                                         recent=[ChunkRef(kr, vr, T_cold, True)], device=dev, chunk_tokens=2048))
+        qs.append(torch.randn((1, H, D), generator=gen, device=dev).to(torch.float16))
+    outs = [torch.empty((1, H, D), device=dev, dtype=torch.float16) for _ in range(layers)]
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        for i in range(layers):
+            lays[i].step(qs[i], scale=scale, out=outs[i])
+
+    def cold_only():
+        from halo_amd.decode import launch
+        for i in range(layers):
+            launch(lays[i].cold_plan, qs[i], scale=scale, m=lays[i].m, l=lays[i].l, o=lays[i].o, acc_mode=2)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graphs = []
+    with torch.cuda.stream(s):
+        for fn in (step, cold_only):
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s):
+                fn()
+            graphs.append(gr)
+    torch.cuda.synchronize()
+
+    def time_graph(gr, n):
+        with torch.cuda.stream(s):
+            gr.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(n):
+                gr.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    step_ms = time_graph(graphs[0], steps)
+    cold_ms = time_graph(graphs[1], steps) / layers
+    nblk = T_cold // 32
+    cold_bytes = nblk * H_kv * kivi.block_bytes(D) + 2 * H * D * 2
+    layer_bytes = cold_bytes + resid * H_kv * D * 2 * 2
+    achieved = cold_bytes / (cold_ms * 1e-3) / 1e9
+    return {
+        "workload": "Qwen2-7B-shaped decode over a KIVI 2-bit cold tier: 28/4 heads, d128, 131072 ctx "
+                    "(130944 quantised in 32-token blocks + 128 fp16 recent), 28 layers looped",
+        "tokens_per_s": 1e3 / step_ms, "ms_per_step": step_ms,
+        "hbm_bytes_per_layer": layer_bytes,
+        "hbm_gbps_end_to_end": layers * layer_bytes / (step_ms * 1e-3) / 1e9,
+        "roofline": {"bound": "hbm", "kernel": "halo_decode_attn_kivi (decode_attn_kivi_kernel<f16,128,8,4> + merge)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                     "bytes_per_launch": cold_bytes, "avg_launch_us": cold_ms * 1e3},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +328,8 @@ def main() -> int:
     ap.add_argument("--no-pcie", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the prefill (MFMA) and KIVI cold-tier measurements")
     ap.add_argument("--unfused", action="store_true",
                     help="select with the standalone scorer kernel instead of in the attention kernel")
     args = ap.parse_args()
@@ -349,6 +468,15 @@ def main() -> int:
             "standalone_scorer_avg_us": score_avg * 1e3,
         },
     }
+    if not args.no_extra:
+        extra = {}
+        log("prefill leg")
+        extra["prefill_c3"] = bench_prefill_c3(torch, dev, reps=max(3, min(args.steps, 10)))
+        log("kivi leg")
+        del g, g_attn, g_score
+        torch.cuda.empty_cache()
+        extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=max(3, min(args.steps, 20)))
+        result["extra"] = extra
     if not args.no_pcie:
         log("pcie-inclusive leg")
         result["pcie_inclusive"] = pcie_inclusive(torch, layers, qs, steps=max(3, min(args.steps, 10)), scale=scale)
@@ -356,6 +484,14 @@ def main() -> int:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, kvs, qs, layers, chunk=chunk, n_hot=n_hot, top_k=top_k, L=L,
                                               budget_s=args.cpu_seconds)
+    # Copy-kernel calibration for hardware byte counters: a 64 MiB
+    # device-to-device copy (reads 64 MiB, writes 64 MiB) run under the same
+    # profiler pass as the kernels above scales FETCH_SIZE / WRITE_SIZE.
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
     print(json.dumps(result), flush=True)
     return 0
 

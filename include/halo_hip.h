@@ -179,6 +179,28 @@ int halo_lse_merge(const float* out_a, const float* lse_a, const float* out_b,
                    const float* lse_b, int64_t n, int D, float* out, float* lse,
                    void* stream);
 
+/* ---- chunked causal prefill -------------------------------------------- */
+
+/*
+ * Prefill attention of T_q query rows per (b, h) over a chunk table, bf16 or
+ * fp16 on MFMA: out[b,h,i,:] = softmax over every attended key row of every
+ * chunk, where row t of chunk c is attended by query row i iff the chunk is
+ * not causal or c.chunk_start + t <= q_start[b] + i; lse[b,h,i] = log of the
+ * softmax denominator of scale*q.k (-inf when nothing is attended, out 0).
+ * q[b*q_stride_b + h*q_stride_h + i*q_stride_t + d] (16-byte aligned rows);
+ * out likewise with its own strides and out_dtype; lse (B,H,T_q) fp32 or
+ * NULL; q_start device int64 [B].  One pass over the table gives the same
+ * result as the reference's per-chunk partials merged by log-sum-exp:
+ * replaces the T_q > 1 route of HALOCacheChunked.compute_attention
+ * (halo/kv_cache_chunked.py:864-964 with _chunk_attention/_lse_merge,
+ * :194-276).  D in {64, 128}.
+ */
+int halo_prefill_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                      int dtype, int B, int H, int H_kv, int T_q, int D, const int64_t* q_start,
+                      const halo_chunk_desc* descs, int n_desc, float scale,
+                      void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_t,
+                      int out_dtype, float* lse, void* stream);
+
 /* ---- chunk-relevance scoring ------------------------------------------- */
 
 /*

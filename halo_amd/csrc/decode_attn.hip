@@ -29,6 +29,21 @@ namespace halo {
 
 constexpr int kWorkInts = 8;  // work record: desc, group, t0, t1, partial slot, 3 x pad
 
+struct MergeParams {
+  const int32_t* group_offsets;
+  int H, H_kv, rep, n_sub;
+  float* m;
+  float* l;
+  float* o;
+  int64_t acc_stride_b;  // elements between batch rows of m/l (H); o uses *D
+  int acc_mode;
+  void* out;
+  int out_dtype;
+  float* lse;
+  const float* ws_o;
+  const float* ws_ml;
+};
+
 struct DecodeParams {
   const void* q;
   int64_t q_stride_b, q_stride_h;
@@ -46,20 +61,6 @@ struct DecodeParams {
   halo_select_cfg sel;
 };
 
-struct MergeParams {
-  const int32_t* group_offsets;
-  int H, H_kv, rep, n_sub;
-  float* m;
-  float* l;
-  float* o;
-  int64_t acc_stride_b;  // elements between batch rows of m/l (H); o uses *D
-  int acc_mode;
-  void* out;
-  int out_dtype;
-  float* lse;
-  const float* ws_o;
-  const float* ws_ml;
-};
 
 template <int DT>
 struct Elem;
@@ -482,6 +483,63 @@ __device__ __forceinline__ void write_partial(const DecodeParams& P, int wslot, 
   }
 }
 
+// Epilogue of the producer/consumer layout: pair j's K-wave holds (m, l)
+// per head, its V-wave the o columns; the NP pair partials are merged
+// through LDS into the work item's partial.
+template <int D, int REP, int NP, int SL, int EP>
+__device__ __forceinline__ void write_partial_pairs(const DecodeParams& P, int wslot, bool kwave, int pair,
+                                                    float (&acc_o)[REP][EP], const float* m_run,
+                                                    const float* l_head, float* s_wo, float (*s_wm)[REP],
+                                                    float (*s_wl)[REP]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  if (!kwave) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int off = SL; off < kWave; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < EP; ++e) acc_o[r][e] += __shfl_xor(acc_o[r][e], off, kWave);
+    if (lane < SL) {
+#pragma unroll
+      for (int r = 0; r < REP; ++r)
+#pragma unroll
+        for (int e = 0; e < EP; ++e) s_wo[(pair * REP + r) * D + lane * EP + e] = acc_o[r][e];
+    }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      s_wm[pair][r] = m_run[r];
+      s_wl[pair][r] = l_head[r];
+    }
+  }
+  __syncthreads();
+  float* wso = P.ws_o + (int64_t)wslot * REP * D;
+  for (int i = tid; i < REP * D; i += 64 * 2 * NP) {
+    const int r = i / D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
+    wso[i] = acc;
+  }
+  if (tid < REP) {
+    const int r = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) acc += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc;
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ float from_bits16(uint16_t h) {
   if constexpr (DT == HALO_BF16) return __uint_as_float((uint32_t)h << 16);
@@ -528,17 +586,23 @@ decode_attn_kernel(DecodeParams P) {
   constexpr int VPB = 16 / RPI;
   static_assert(!kMfma || (REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL), "mfma tile shape");
 
-  constexpr int SZ_Q = kMfma ? 0 : NW * REP * RB;  // VALU path: one copy of the group's q per wave
+  constexpr int NP = NW / 2;  // MFMA path: producer/consumer wave pairs
+  // VALU path: per-wave q copy, K tiles, p tiles; the epilogue reuses the front.
+  // MFMA path: per pair 2 p tiles and 2 rescale vectors, then the pair partials.
+  constexpr int SZ_Q = kMfma ? 0 : NW * REP * RB;
   constexpr int SZ_K = kMfma ? 0 : NW * TILE * KROW;
-  constexpr int SZ_P = NW * TILE * REP * 4;
-  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P;
+  constexpr int SZ_P = kMfma ? NP * 2 * TILE * REP * 4 : NW * TILE * REP * 4;
+  constexpr int SZ_AL = kMfma ? (NP * 2 * REP * 4 + 15) / 16 * 16 : 0;
+  constexpr int SZ_WO = kMfma ? NP * REP * D * 4 : 0;
+  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO;
   constexpr int SZ_A = SZ_A0 > kSelBytes ? SZ_A0 : kSelBytes;
-  constexpr int SZ_B = NW * REP * D * 4;
+  constexpr int SZ_B = kMfma ? 0 : NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
   char* s_q = smem + (threadIdx.x / kWave) * REP * RB;
   char* s_kall = smem + SZ_Q;
   float* s_pall = reinterpret_cast<float*>(smem + SZ_Q + SZ_K);
-  float* s_wo = reinterpret_cast<float*>(smem);
+  float* s_alpha = reinterpret_cast<float*>(smem + SZ_Q + SZ_K + SZ_P);
+  float* s_wo = reinterpret_cast<float*>(kMfma ? smem + SZ_Q + SZ_K + SZ_P + SZ_AL : smem);
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
 
   const int tid = threadIdx.x;
@@ -615,116 +679,157 @@ decode_attn_kernel(DecodeParams P) {
   const int voff0 = my_col * 16;
 
   if constexpr (kMfma) {
-    // ---- q.k on MFMA 16x16x32: A = 16 K rows x 32 elements (lane l holds
-    // row l%16, elements 8*(l/16)..+8 of the k-step), B = q^T (lane l holds
-    // head l%16, same elements), D = scores (lane l: head l%16, rows
-    // 4*(l/16)..+4).  K goes from the buffer loads straight into A operands.
-    const int hl = lane & 15;   // this lane's head in the score layout
-    const int kg = lane >> 4;   // its k-group / row quad
+    // ---- Producer/consumer wave pairs: every wave streams ONE contiguous
+    // row range of ONE tensor (on gfx950 a wave that streams two distant
+    // regions at once pulls markedly less bandwidth than one that streams a
+    // single region).  Waves [0, NP) read K and compute the scores on
+    // v_mfma_f32_16x16x32 (A = 16 K rows x 32 elements: lane l holds row
+    // l%16, elements 8*(l/16)..+8 of the k-step; B = q^T: lane l holds head
+    // l%16; D: lane l holds head l%16, rows 4*(l/16)..+4) and the online
+    // softmax; waves [NP, NW) read V and accumulate P.V with the tile's
+    // probabilities and rescale factors their partner leaves in LDS
+    // (double-buffered by tile parity, one workgroup barrier per tile).
+    // Each wave keeps two tiles of loads in flight.
+    constexpr int NBUF = NB * KS;
+    static_assert(NBUF == PPL, "K and V tiles use the same register budget");
+    const bool kwave = wave < NP;
+    const int pair = kwave ? wave : wave - NP;
+    const int tpp = (ntiles_total + NP - 1) / NP;   // tiles per pair, uniform in the workgroup
+    const int ps = t0 + pair * tpp * TILE;
+    const int pe = min(t1, ps + tpp * TILE);
+    float* pbuf = s_pall + pair * 2 * TILE * REP;
+    float* abuf = s_alpha + pair * 2 * REP;
+    const int hl = lane & 15;   // score layout: head
+    const int kg = lane >> 4;   // score layout: k-group / row quad
     uint4 qb[KS];
-    {
-      const bool live = hl < nvalid_h;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb[s] = make_uint4(0, 0, 0, 0);
+    if (kwave && hl < nvalid_h) {
       const char* qrow = reinterpret_cast<const char*>(P.q) +
-                         ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + (live ? hl : 0)) * P.q_stride_h) * E::size;
+                         ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + hl) * P.q_stride_h) * E::size;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (live) {
-          if (P.q_aligned) {
-            v = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
-          } else {
-            const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
-            v.x = qh[0] | ((uint32_t)qh[1] << 16);
-            v.y = qh[2] | ((uint32_t)qh[3] << 16);
-            v.z = qh[4] | ((uint32_t)qh[5] << 16);
-            v.w = qh[6] | ((uint32_t)qh[7] << 16);
-          }
+        if (P.q_aligned) {
+          qb[s] = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
+        } else {
+          const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
+          qb[s] = make_uint4(qh[0] | ((uint32_t)qh[1] << 16), qh[2] | ((uint32_t)qh[3] << 16),
+                             qh[4] | ((uint32_t)qh[5] << 16), qh[6] | ((uint32_t)qh[7] << 16));
         }
-        qb[s] = v;
       }
     }
-    float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
-    float l_lane = 0.f;        // this lane's share of head hl's denominator
-    uint4 kreg[NB][KS], vreg[PPL];
-    for (int tb = ws; tb < we; tb += TILE) {
-      const int nrows = min(TILE, we - tb);
-      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(we - tb) * kst);
-      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(we - tb) * vst);
-      // issue order K0 V0 K1 V1 ...: block j is processed as soon as its
-      // own loads have landed (the load counter drains in issue order)
+    // The two roles run separate loops with the same number of workgroup
+    // barriers (tpp), so each role's registers are live only in its own loop.
+    if (kwave) {
+      float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
+      float l_lane = 0.f;        // this lane's share of head hl's denominator
+      for (int it = 0; it < tpp; it += 2) {
+        uint4 buf[2][NBUF];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+        for (int u = 0; u < 2; ++u) {
+          const int tb = ps + (it + u) * TILE;
+          const __amdgpu_buffer_rsrc_t rr = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(pe - tb) * kst);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) kreg[nb][s] = buf_ld16(rk, (int)((nb * 16 + hl) * kst) + s * 64 + kg * 16);
+          for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int j = 0; j < VPB; ++j) {
-          const int i = nb * VPB + j;
-          vreg[i] = buf_ld16(rv, (int)((i * RPI + my_row0) * vst) + voff0);
+            for (int s = 0; s < KS; ++s)
+              buf[u][nb * KS + s] = buf_ld16(rr, (int)((nb * 16 + hl) * kst) + s * 64 + kg * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (it + u >= tpp) break;
+          const int tb = ps + (it + u) * TILE;
+          const int nrows = min(TILE, pe - tb);  // <= 0: every row masked
+          float* pt = pbuf + ((it + u) & 1) * TILE * REP;
+          float* at = abuf + ((it + u) & 1) * REP;
+          f32x4 sc[NB];
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            sc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) sc[nb] = MfmaOp<DT>::run(buf[u][nb * KS + s], qb[s], sc[nb]);
+          }
+          float sv[NB][4], bm = -INFINITY;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const bool valid = nb * 16 + kg * 4 + c < nrows;
+              sv[nb][c] = valid ? sc[nb][c] * P.scale2 : -INFINITY;
+              bm = fmaxf(bm, sv[nb][c]);
+            }
+          bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+          bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+          const float m_new = fmaxf(m_lane, bm);
+          const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+          const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+          m_lane = m_new;
+          float psum = 0.f;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const float p = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
+              psum += p;
+              if (hl < REP) pt[(nb * 16 + kg * 4 + c) * REP + hl] = p;
+            }
+          l_lane = l_lane * alpha + psum;
+          if (lane < REP) at[lane] = alpha;
+          __syncthreads();  // hand the tile's p and rescale factors to the V-wave
         }
       }
+      float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
+      lsum += __shfl_xor(lsum, 32, kWave);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < REP; ++r) {
+        m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
+        l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
+      }
+    } else {
+      for (int it = 0; it < tpp; it += 2) {
+        uint4 buf[2][NBUF];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) sc = MfmaOp<DT>::run(kreg[nb][s], qb[s], sc);
-        float sv[4], bm = -INFINITY;
+        for (int u = 0; u < 2; ++u) {
+          const int tb = ps + (it + u) * TILE;
+          const __amdgpu_buffer_rsrc_t rr = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(pe - tb) * vst);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bool valid = nb * 16 + kg * 4 + c < nrows;
-          sv[c] = valid ? sc[c] * P.scale2 : -INFINITY;
-          bm = fmaxf(bm, sv[c]);
+          for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * vst) + voff0);
         }
-        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-        const float m_new = fmaxf(m_lane, bm);
-        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
-        m_lane = m_new;
-        float psum = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float p = __builtin_amdgcn_exp2f(sv[c] - ms);
-          psum += p;
-          if (hl < REP) pl[(nb * 16 + kg * 4 + c) * REP + hl] = p;
-        }
-        l_lane = l_lane * alpha + psum;
-        float al[REP];
-        bool rescale = false;
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-          al[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
-          rescale |= al[r] != 1.f;
-        }
-        if (rescale) {
-#pragma unroll
-          for (int r = 0; r < REP; ++r)
-#pragma unroll
-            for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
-        }
-        wave_lds_fence();
-        // P.V over the block's row pairs (VALU, V straight from registers)
-#pragma unroll
-        for (int j = 0; j < VPB; j += 2) {
-          const int i = nb * VPB + j;
-          const int ra = i * RPI + my_row0, rbw = (i + 1) * RPI + my_row0;
-          float pa[REP], pb[REP];
+        for (int u = 0; u < 2; ++u) {
+          if (it + u >= tpp) break;
+          const float* pt = pbuf + ((it + u) & 1) * TILE * REP;
+          const float* at = abuf + ((it + u) & 1) * REP;
+          __syncthreads();  // the K-wave's p and rescale factors for this tile are in LDS
+          float al[REP];
+          bool rescale = false;
 #pragma unroll
           for (int r = 0; r < REP; ++r) {
-            pa[r] = pl[ra * REP + r];
-            pb[r] = pl[rbw * REP + r];
+            al[r] = at[r];
+            rescale |= al[r] != 1.f;
           }
-          pv_pair<DT, REP, EP>(vreg[i], vreg[i + 1], pa, pb, acc_o);
+          if (rescale) {
+#pragma unroll
+            for (int r = 0; r < REP; ++r)
+#pragma unroll
+              for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
+          }
+#pragma unroll
+          for (int j = 0; j < PPL; j += 2) {
+            const int ra = j * RPI + my_row0, rbw = (j + 1) * RPI + my_row0;
+            float pa[REP], pb[REP];
+#pragma unroll
+            for (int r = 0; r < REP; ++r) {
+              pa[r] = pt[ra * REP + r];
+              pb[r] = pt[rbw * REP + r];
+            }
+            pv_pair<DT, REP, EP>(buf[u][j], buf[u][j + 1], pa, pb, acc_o);
+          }
         }
       }
-      wave_lds_fence();  // the next tile rewrites pl
     }
-    float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
-      l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
-    }
+    write_partial_pairs<D, REP, NP, SL, EP>(P, wslot, kwave, pair, acc_o, m_run, l_head, s_wo, s_wm, s_wl);
+    return;
   } else {
     // ---- VALU path (fp32): K transposed through LDS, lane groups per head.
     float l_lane = 0.f;  // this lane's share of its head's softmax denominator

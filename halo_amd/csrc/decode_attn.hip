@@ -238,10 +238,11 @@ __device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const 
 // the chosen descriptors are left in LDS at s_cat.
 // ---------------------------------------------------------------------------
 constexpr int kSelMaxCold = 64;
+constexpr int kSelTPT = 2;  // (page, row, head) triples per thread: at most 2 x 256 per selection
 static_assert(sizeof(halo_chunk_desc) % 8 == 0, "descriptors are copied as 8-byte words");
 constexpr int kSelMaxQbar = 2048;
 constexpr int kSelQbarLds = kSelMaxQbar + 4 * 64;  // padded rows: at most 2048 / 64 rows of +4 floats
-constexpr int kSelBytes = kSelQbarLds * 4 + 4 * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
+constexpr int kSelBytes = kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
 
 __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
   halo_chunk_desc u;
@@ -289,23 +290,29 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
   const int triples = n * nrh;
   float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
   float* s_dot = s_qbar + kSelQbarLds;
-  int* s_pick = reinterpret_cast<int*>(s_dot + 3 * 256);
+  int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
   halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
 
   // Every global load below is issued before the first wait: the page-mean
-  // row of this thread's (page, row, head) triple, its share of the
-  // candidate descriptors and its query pieces.
-  uint4 kb[PIECES];
-  int my_r = 0, my_h = 0;
-  if (tid < triples) {
-    const int i = tid / nrh, rh = tid % nrh;
-    my_r = rh / H_kv;
-    my_h = rh % H_kv;
-    const char* row = reinterpret_cast<const char*>(S.kmean) +
-                      ((int64_t)(b0 + my_r) * S.km_stride_b + (int64_t)my_h * S.km_stride_h + (int64_t)i * S.km_stride_p) *
-                          E::size;
+  // rows of this thread's (page, row, head) triples (at most kSelTPT),
+  // its share of the candidate descriptors and its query pieces.
+  uint4 kb[kSelTPT][PIECES];
+  int my_r[kSelTPT], my_h[kSelTPT];
 #pragma unroll
-    for (int c = 0; c < PIECES; ++c) kb[c] = *reinterpret_cast<const uint4*>(row + c * 16);
+  for (int u = 0; u < kSelTPT; ++u) {
+    const int t = tid + u * NT;
+    my_r[u] = 0;
+    my_h[u] = 0;
+    if (t < triples) {
+      const int i = t / nrh, rh = t % nrh;
+      my_r[u] = rh / H_kv;
+      my_h[u] = rh % H_kv;
+      const char* row = reinterpret_cast<const char*>(S.kmean) +
+                        ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
+                         (int64_t)i * S.km_stride_p) * E::size;
+#pragma unroll
+      for (int c = 0; c < PIECES; ++c) kb[u][c] = *reinterpret_cast<const uint4*>(row + c * 16);
+    }
   }
   const uint2* cat = reinterpret_cast<const uint2*>(S.catalog + (int64_t)sel * S.catalog_stride);
   uint2 cw[CW];
@@ -379,17 +386,21 @@ __device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, 
   }
   __syncthreads();
 
-  if (tid < triples) {
-    const float* qg = s_qbar + (my_r * H_kv + my_h) * QS;
-    float acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < PIECES; ++c) {
-      float f[EP];
-      E::unpack(kb[c], f);
+  for (int u = 0; u < kSelTPT; ++u) {
+    const int t = tid + u * NT;
+    if (t < triples) {
+      const float* qg = s_qbar + (my_r[u] * H_kv + my_h[u]) * QS;
+      float acc = 0.f;
 #pragma unroll
-      for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
+      for (int c = 0; c < PIECES; ++c) {
+        float f[EP];
+        E::unpack(kb[u][c], f);
+#pragma unroll
+        for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
+      }
+      s_dot[t] = acc;
     }
-    s_dot[tid] = acc;
   }
   __syncthreads();
   // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
@@ -631,7 +642,7 @@ decode_attn_kernel(DecodeParams P) {
     const bool writer = (P.sel.per_row || b == 0) && h_kv == 0 && sub == 0 && item.x == P.sel.slot0 && item.z == 0;
     const int pick = fused_select<DT, D, 64 * NW>(P, b, smem, item.x - P.sel.slot0, writer);
     if (pick >= 0) {
-      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelQbarLds * 4 + 4 * 256 * 4)[pick]);
+      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4)[pick]);
     } else {
       dsc = P.descs[item.x];
       dsc.T_c = 0;
@@ -1459,7 +1470,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
     HALO_CHECK_ARG(S.top_k >= 1 && S.slot0 >= 0 && S.slot0 + S.top_k <= n_desc,
                    "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
     HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");
-    HALO_CHECK_ARG(S.n_cold * rows * H_kv <= 256, "n_cold * rows * H_kv must be <= 256");
+    HALO_CHECK_ARG(S.n_cold * rows * H_kv <= kSelTPT * 256, "n_cold * rows * H_kv must be <= 512");
     HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
     HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(S.kmean) % 16 == 0 && (S.km_stride_b * esz) % 16 == 0 &&
                        (S.km_stride_h * esz) % 16 == 0 && (S.km_stride_p * esz) % 16 == 0,

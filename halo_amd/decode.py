@@ -54,6 +54,19 @@ class ChunkRef:
 
 
 @dataclass
+class SlotRef:
+    """A chunk-table slot whose chunk is chosen on the device (by the
+    in-kernel selection or by ``halo_chunk_score_topk`` writing the table):
+    it holds no tensor until then; ``T`` is the largest chunk it may receive,
+    so the planner covers that many rows."""
+
+    T: int
+    chunk_start: int = 0
+    causal: bool = False
+    batch: int = -1
+
+
+@dataclass
 class DecodePlan:
     B: int
     H: int
@@ -138,6 +151,12 @@ def pack_descs(chunks: Sequence[ChunkRef], *, B: int, H_kv: int, D: int, dtype: 
     for i, c in enumerate(chunks):
         if hasattr(c, "blocks"):
             keep.append(_pack_kivi(descs[i], c, i, B=B, H_kv=H_kv, D=D, dtype=dtype))
+            continue
+        if isinstance(c, SlotRef):
+            d = descs[i]
+            d["start"], d["T"] = int(c.chunk_start), int(c.T)
+            d["flags"] = nat.CHUNK_CAUSAL if c.causal else 0
+            d["batch"] = int(c.batch)
             continue
         k, v = c.k, c.v
         if k.dtype != dtype or v.dtype != dtype:
@@ -234,7 +253,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
     n_groups = B * H_kv * n_sub
 
     descs, keep = pack_descs(chunks, B=B, H_kv=H_kv, D=D, dtype=dtype)
-    kinds = {hasattr(c, "blocks") for c in chunks}
+    kinds = {hasattr(c, "blocks") for c in chunks if not isinstance(c, SlotRef)}
     if len(kinds) > 1:
         raise AssertionError("a plan holds either plain or KIVI chunks; merge the two through accumulators")
     kivi = kinds == {True}

@@ -32,7 +32,7 @@ from .decode import ChunkRef, DecodePlan, build_plan, descs_to_device, launch, p
 
 # In-kernel selection limits of halo_decode_attn_tiered (include/halo_hip.h).
 _SEL_MAX_COLD = 64
-_SEL_MAX_TRIPLES = 256
+_SEL_MAX_TRIPLES = 512
 _SEL_MAX_QBAR = 2048
 
 
@@ -112,3 +112,77 @@ class TieredDecodeLayer:
         self.select(q)
         self.attend(q, scale=scale, out=out, lse=lse, q_pos=q_pos)
 
+
+
+class RaggedTieredDecodeLayer:
+    """Batched decode over per-sequence chunk tables (ragged contexts).
+
+    ``rows[b] = (hot, cold)``: row b's hot chunks and cold chunks, each a
+    ``ChunkRef`` with ``batch=b`` and ``(H_kv, T_c, D)`` tensors.  Every row
+    selects its own ``top_k`` cold chunks by the mean-key score inside the
+    attention launch (per-row selection over a ragged catalog), so one step
+    is one ``halo_decode_attn_tiered`` plus its merge for the whole batch.
+
+    Reference: the batch-uniform Triton kernel needs one call per sequence
+    for ragged batches (halo/triton_chunked.py:171-177); here the chunk table
+    carries per-row chunks (int32 work records) and a per-row selection.
+    """
+
+    def __init__(self, *, H: int, H_kv: int, D: int, dtype: torch.dtype, rows, top_k: int, device,
+                 split: Optional[int] = None) -> None:
+        from .decode import SlotRef
+        B = len(rows)
+        n_cold = [len(cold) for _, cold in rows]
+        max_cold = max(n_cold)
+        if max_cold > _SEL_MAX_COLD or max_cold * H_kv > _SEL_MAX_TRIPLES or H_kv * D > _SEL_MAX_QBAR:
+            raise AssertionError(f"per-row selection over {max_cold} cold chunks x {H_kv} KV heads exceeds the "
+                                 f"in-kernel limits ({_SEL_MAX_COLD} chunks, {_SEL_MAX_TRIPLES} rows)")
+        if top_k < 1:
+            raise AssertionError("top_k must be >= 1")
+        for b, (hot, cold) in enumerate(rows):
+            for c in list(hot) + list(cold):
+                if c.batch != b:
+                    raise AssertionError(f"row {b}: chunks must carry batch={b}")
+        self.B, self.H, self.H_kv, self.D, self.dtype, self.top_k = B, H, H_kv, D, dtype, top_k
+        self.rows = rows
+        widest = max(c.T for _, cold in rows for c in cold) if max_cold else 0
+        slots = [SlotRef(widest) for _ in range(top_k)]
+        hot_all = [c for hot, _ in rows for c in hot]
+        self.plan: DecodePlan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=slots + hot_all,
+                                           device=device, split=split, first=range(top_k))
+        import numpy as np
+
+        from .decode import DESC_DTYPE
+        cat = np.zeros(B * max(max_cold, 1), dtype=DESC_DTYPE)
+        for b, (_, cold) in enumerate(rows):
+            if cold:
+                d, keep = pack_descs(cold, B=B, H_kv=H_kv, D=D, dtype=dtype)
+                cat[b * max_cold: b * max_cold + len(cold)] = d
+                self.plan.keep += keep
+        self.catalog = descs_to_device(cat, device)
+        self.kmean = torch.zeros((B, H_kv, max(max_cold, 1), D), device=device, dtype=dtype)
+        for b, (_, cold) in enumerate(rows):
+            for j, c in enumerate(cold):
+                chunk_means(c.k.unsqueeze(0), c.T, row0=0, n_pages=1, out=self.kmean[b:b + 1], page_offset=j)
+        self.n_cold = torch.tensor(n_cold, dtype=torch.int32, device=device)
+        self.idx = torch.empty((B, top_k), device=device, dtype=torch.int32)
+        self.scores = torch.empty((B, max(max_cold, 1)), device=device, dtype=torch.float32)
+        km = self.kmean
+        self.select_cfg = nat.SelectCfg(
+            kmean=km.data_ptr(), km_stride_b=km.stride(0), km_stride_h=km.stride(1), km_stride_p=km.stride(2),
+            catalog=self.catalog.data_ptr(), catalog_stride=max(max_cold, 1), n_cold_per_sel=self.n_cold.data_ptr(),
+            n_cold=max(max_cold, 1), top_k=top_k, slot0=0, per_row=1,
+            idx_out=self.idx.data_ptr(), score_out=self.scores.data_ptr())
+
+    def attended_rows(self) -> int:
+        """K/V rows one step reads per KV head, summed over the batch (hot +
+        the selected chunks, assuming each row fills its top_k)."""
+        total = 0
+        for hot, cold in self.rows:
+            sizes = sorted((c.T for c in cold), reverse=True)
+            total += sum(c.T for c in hot) + sum(sizes[: self.top_k])
+        return total
+
+    def step(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse: Optional[torch.Tensor] = None,
+             q_pos: Optional[torch.Tensor] = None) -> None:
+        launch(self.plan, q, scale=scale, q_pos=q_pos, out=out, lse=lse, select=self.select_cfg)

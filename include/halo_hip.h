@@ -128,7 +128,7 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
  * descending, then index ascending); a slot past the number of eligible
  * chunks attends nothing.  idx_out[s*top_k + j] / score_out[s*n_cold + p]
  * receive the selection when non-NULL.  Limits: n_cold <= 64,
- * n_cold * rows * H_kv <= 256 and rows * H_kv * D <= 2048 per selection
+ * n_cold * rows * H_kv <= 512 and rows * H_kv * D <= 2048 per selection
  * (rows = 1 when per_row).  The work items of a slot must cover as many rows
  * as the largest catalog chunk (rows past a chunk's T_c are skipped).
  */

@@ -233,3 +233,53 @@ def test_tiered_layer_in_hip_graph(dev, fused):
         torch.cuda.synchronize()
         assert torch.equal(got_i, layer.idx)
         assert torch.equal(got_o, out) and torch.equal(got_l, lse)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_ragged_batched_decode(dev, dtype):
+    """Per-sequence chunk tables of different lengths in one launch: each
+    row scores its own cold chunks (bit-exact top-k against the oracle's
+    selector, margin-checked), a row with fewer cold chunks than top_k leaves
+    -1 slots, and every row's output matches the float64 closed form over its
+    hot + selected rows."""
+    from halo_amd.decode import ChunkRef
+    from halo_amd.tiered import RaggedTieredDecodeLayer
+    H, H_kv, D, c, top_k = 8, 2, 128, 256, 4
+    ctx = [1024, 2560, 1536]
+    rng = np.random.default_rng(17)
+    rows, host = [], []
+    for b, T in enumerate(ctx):
+        k = rng.standard_normal((H_kv, T, D), dtype=np.float32)
+        k[:, :, [3, 77]] *= 6.0
+        v = rng.standard_normal((H_kv, T, D), dtype=np.float32)
+        from oracle.inputs import round_to
+        k, v = round_to(k, dtype), round_to(v, dtype)
+        kg, vg = _gpu(k, dtype, dev), _gpu(v, dtype, dev)
+        n = T // c
+        n_hot = max(1, n // 4)
+        refs = [ChunkRef(kg[:, i * c:(i + 1) * c], vg[:, i * c:(i + 1) * c], i * c, True, batch=b) for i in range(n)]
+        rows.append((refs[n - n_hot:], refs[:n - n_hot]))
+        host.append((k, v, n, n_hot))
+    q = round_to(rng.standard_normal((len(ctx), H, D), dtype=np.float32), dtype)
+    layer = RaggedTieredDecodeLayer(H=H, H_kv=H_kv, D=D, dtype=TDT[dtype], rows=rows, top_k=top_k, device=dev)
+    out = torch.empty((len(ctx), H, D), device=dev, dtype=TDT[dtype])
+    lse = torch.empty((len(ctx), H), device=dev)
+    q_pos = torch.tensor([T - 1 for T in ctx], device=dev, dtype=torch.int64)
+    layer.step(_gpu(q, dtype, dev), scale=1 / math.sqrt(D), out=out, lse=lse, q_pos=q_pos)
+    torch.cuda.synchronize()
+    km = layer.kmean.float().cpu().numpy()
+    for b, (k, v, n, n_hot) in enumerate(host):
+        n_cold = n - n_hot
+        ref_sc = S.mean_key_scores(q[b:b + 1, :, None], km[b:b + 1, :, :n_cold], dtype)
+        srt = np.sort(ref_sc.astype(np.float64))[::-1]
+        assert len(srt) <= top_k or srt[top_k - 1] - srt[top_k] > 1e-4, "fixture seed lost its margin"
+        want = S.select_chunks(q[b:b + 1, :, None], km[b:b + 1, :, :n_cold], np.arange(n_cold), top_k, dtype).tolist()
+        assert layer.idx[b].cpu().tolist() == want + [-1] * (top_k - len(want))
+        keep = np.zeros(k.shape[1], bool)
+        keep[(n - n_hot) * c:] = True
+        for j in want:
+            keep[j * c:(j + 1) * c] = True
+        ro, rl = A.attention_f64(q[b:b + 1], k[None], v[None], scale=1 / math.sqrt(D), keep=keep)
+        tol = 1e-5 if dtype == "float32" else 2e-2
+        assert np.abs(out[b:b + 1].float().cpu().numpy() - ro).max() <= tol
+        assert np.abs(lse[b:b + 1].cpu().numpy() - rl).max() <= (1e-5 if dtype == "float32" else 1e-3)

@@ -9,6 +9,12 @@ kernels for gfx950 (``halo_amd/csrc``) behind the C-ABI in
 ``include/halo_hip.h``.
 """
 from . import _native
+from .demoter import HALODemoter  # noqa: F401
+from .kv_cache_chunked import HALOCacheChunked  # noqa: F401
+from .memory_tier import MemoryTier, TieredStorage  # noqa: F401
+from .policy import HALOConfig, parse_overrides, wrap_with_halo  # noqa: F401
+from .refetcher import HALORefetcher  # noqa: F401
+from .scorer import HALOScorer  # noqa: F401
 from .triton_chunked import (  # noqa: F401
     HAS_HIP,
     HAS_TRITON,

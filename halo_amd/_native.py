@@ -77,6 +77,8 @@ _SIGNATURES = {
                               _c_void_p, _c_void_p, _c_void_p]),
     "halo_prefill_attn": (_i32, [_c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_void_p,
                                  _c_void_p, _i32, _f32, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+    "halo_halo_score": (_i32, [_c_void_p, _i32, _i32, _f32, _f32, _f32, _i32, _i32, _c_void_p, _c_void_p]),
+    "halo_topk_sorted": (_i32, [_c_void_p, _i32, _i32, _c_void_p, _c_void_p]),
     "halo_kivi_block_bytes": (_size_t, [_i32, _i32]),
     "halo_kivi_quantize": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _i64,
                                   _i32, _i32, _i32, _i32, _i32, _i32, _c_void_p, _i64, _i64, _c_void_p]),

@@ -40,6 +40,128 @@ class MemoryTier(str, Enum):
         return cls(str(name).lower())
 
 
+@dataclass
+class _BlockBuffer:
+    """One tier's block store: keys/values (L, max_blocks, H_kv, block_size, D)."""
+
+    keys: torch.Tensor
+    values: torch.Tensor
+
+    def block(self, layer: int, block: int):
+        return self.keys[layer, block], self.values[layer, block]
+
+    def write(self, layer: int, block: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        # pinned host <-> device copies are hipMemcpyAsync on the current stream
+        self.keys[layer, block].copy_(keys, non_blocking=True)
+        self.values[layer, block].copy_(values, non_blocking=True)
+
+
+class _FileBuffer:
+    """NVMe tier: one byte-addressed numpy memmap per K and V; blocks are
+    read into host memory and written from it (halo/memory_tier.py:61-102)."""
+
+    def __init__(self, shape, dtype: torch.dtype, path: str) -> None:
+        import os
+
+        import numpy as np
+        self.shape = tuple(shape)
+        self.dtype = dtype
+        self.itemsize = torch.tensor([], dtype=dtype).element_size()
+        per_block = int(np.prod(self.shape[2:])) * self.itemsize
+        self.per_block = per_block
+        total = self.shape[0] * self.shape[1] * per_block
+        os.makedirs(path, exist_ok=True)
+        self._k = np.memmap(os.path.join(path, "keys.bin"), dtype=np.uint8, mode="w+", shape=(total,))
+        self._v = np.memmap(os.path.join(path, "values.bin"), dtype=np.uint8, mode="w+", shape=(total,))
+
+    def _span(self, layer: int, block: int):
+        s = (layer * self.shape[1] + block) * self.per_block
+        return s, s + self.per_block
+
+    def block(self, layer: int, block: int):
+        s, e = self._span(layer, block)
+        out = []
+        for mm in (self._k, self._v):
+            buf = torch.frombuffer(bytearray(mm[s:e].tobytes()), dtype=self.dtype)
+            out.append(buf.view(*self.shape[2:]))
+        return out[0], out[1]
+
+    def write(self, layer: int, block: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        s, e = self._span(layer, block)
+        for mm, src in ((self._k, keys), (self._v, values)):
+            host = src.detach().contiguous().cpu()
+            mm[s:e] = host.view(torch.uint8).numpy().reshape(-1)
+        self._k.flush()
+        self._v.flush()
+
+
+class TieredStorage:
+    """Per-tier block stores and a per-(layer, block) tier directory
+    (halo/memory_tier.py:105-226).  Tier buffers are allocated on first use;
+    the DRAM tier is pinned when the GPU tier is a device, so block moves are
+    asynchronous copies on the caller's stream.  The default tier of an
+    unknown block is GPU."""
+
+    def __init__(self, *, tiers, num_layers: int, num_kv_heads: int, head_dim: int, block_size: int,
+                 dtype: torch.dtype, device, nvme_path: Optional[str] = None, max_blocks: int = 4096) -> None:
+        self.tiers = [MemoryTier.from_name(t) for t in tiers]
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.dtype = dtype
+        self.gpu_device = torch.device(device)
+        self.max_blocks = max_blocks
+        self._shape = (num_layers, max_blocks, num_kv_heads, block_size, head_dim)
+        self._nvme_path = nvme_path
+        self._directory: dict = {}
+        self._buffers: dict = {}
+
+    def move_block(self, *, layer: int, block: int, src, dst) -> None:
+        s, d = MemoryTier.from_name(src), MemoryTier.from_name(dst)
+        if s == d:
+            return
+        k, v = self._buffer(s).block(layer, block)
+        self._buffer(d).write(layer, block, k, v)
+        self._directory[(layer, block)] = d
+
+    def locate_block(self, *, layer: int, block: int) -> str:
+        return self._directory.get((layer, block), MemoryTier.GPU).value
+
+    def write_new_block(self, *, layer: int, block: int, keys: torch.Tensor, values: torch.Tensor,
+                        tier: str = "gpu") -> None:
+        t = MemoryTier.from_name(tier)
+        self._buffer(t).write(layer, block, keys, values)
+        self._directory[(layer, block)] = t
+
+    def read_block(self, *, layer: int, block: int):
+        t = self._directory.get((layer, block), MemoryTier.GPU)
+        return self._buffer(t).block(layer, block)
+
+    def _buffer(self, tier: MemoryTier):
+        buf = self._buffers.get(tier)
+        if buf is not None:
+            return buf
+        if tier not in self.tiers:
+            raise ValueError(f"Tier {tier} not requested at construction time.")
+        if tier is MemoryTier.GPU:
+            buf = _BlockBuffer(torch.empty(self._shape, dtype=self.dtype, device=self.gpu_device),
+                               torch.empty(self._shape, dtype=self.dtype, device=self.gpu_device))
+        elif tier is MemoryTier.DRAM:
+            pin = self.gpu_device.type == "cuda" and torch.cuda.is_available()
+            buf = _BlockBuffer(torch.empty(self._shape, dtype=self.dtype, pin_memory=pin),
+                               torch.empty(self._shape, dtype=self.dtype, pin_memory=pin))
+        else:
+            import os
+            path = self._nvme_path or os.environ.get("HALO_NVME_PATH") or "/tmp/halo_nvme"
+            buf = _FileBuffer(self._shape, self.dtype, path)
+        self._buffers[tier] = buf
+        return buf
+
+    def __repr__(self) -> str:  # pragma: no cover
+        return f"TieredStorage(tiers=[{','.join(t.value for t in self.tiers)}], blocks={self.max_blocks})"
+
+
 _COPY_STREAMS: dict = {}
 
 

@@ -248,6 +248,28 @@ int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int refresh, int sink_pages, int P_total,
                           void* stream);
 
+/* ---- HALOScorer: closed-form hotness and sorted top-k -------------------- */
+
+/*
+ * score[p] for p < K from the head-mean attention snapshot attention[p]
+ * (fp32): a = attention/(sum + 1e-12), r = exp(-max(step - p, 0) /
+ * max(refresh_window, 1)), r /= (sum r + 1e-12), s = 1 for p <
+ * sink_tokens, score = (alpha*a + beta*r + gamma*s) / (max + 1e-12).
+ * Sums run in index order (deterministic).  Replaces HALOScorer.score
+ * (halo/scorer.py:36-72).  K <= 2^24.
+ */
+int halo_halo_score(const float* attention, int K, int step, float alpha, float beta, float gamma,
+                    int sink_tokens, int refresh_window, float* score, void* stream);
+
+/*
+ * Indices of the k largest of score[0..K) (fp32), written ascending to
+ * idx_out (int64, k entries); ties go to the lower index, NaN ranks as -inf.
+ * Replaces torch.topk(score, k).indices.sort() of HALOScorer.topk_hot and
+ * HALORefetcher.predict_hot (halo/scorer.py:74-88, halo/refetcher.py:38-57),
+ * whose tie order torch leaves undefined.  1 <= k <= K <= 2^24.
+ */
+int halo_topk_sorted(const float* score, int K, int k, int64_t* idx_out, void* stream);
+
 /* ---- KIVI 2/4-bit cold-chunk format ------------------------------------ */
 
 /*

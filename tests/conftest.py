@@ -45,3 +45,18 @@ def fake_attention():
         return torch.softmax(torch.randn(K, generator=g), dim=0)
 
     return _make
+
+
+@pytest.fixture
+def storage_factory(small_config):
+    """TieredStorage on the CPU (reference tests/conftest.py:43-63): the
+    directory and tier copies are host logic and run without a GPU."""
+    import torch
+    from halo_amd import MemoryTier, TieredStorage
+
+    def _make(num_layers: int = 2, num_kv_heads: int = 2, head_dim: int = 8, max_blocks: int = 16):
+        return TieredStorage(tiers=[MemoryTier.GPU, MemoryTier.DRAM], num_layers=num_layers,
+                             num_kv_heads=num_kv_heads, head_dim=head_dim, block_size=small_config.block_size,
+                             dtype=torch.float32, device=torch.device("cpu"), max_blocks=max_blocks)
+
+    return _make

@@ -1,0 +1,157 @@
+"""Host-side components on the CPU: configuration and overrides, tier
+storage, refetch/demote bookkeeping, the Path-D cache's peel and the model
+wrapper (expectations of the reference's own tests: test_policy.py,
+test_overrides.py, test_memory_tier.py, test_refetcher.py:22-43,
+test_demoter.py).  No kernel is launched here."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+
+def test_default_config_matches_reference_defaults():
+    from halo_amd import HALOConfig
+    cfg = HALOConfig()
+    assert cfg.hot_ratio == 0.10 and cfg.refresh_window == 64 and cfg.sink_tokens == 4
+    assert "gpu" in cfg.tiers and "dram" in cfg.tiers
+    assert (cfg.score_alpha, cfg.score_beta, cfg.score_gamma) == (1.0, 0.5, 2.0)
+    assert (cfg.block_size, cfg.chunk_size, cfg.recent_window, cfg.lookahead) == (32, 512, 64, 1)
+
+
+def test_make_storage_returns_tiered_storage():
+    from halo_amd import HALOConfig, TieredStorage
+    cfg = HALOConfig(tiers=("gpu", "dram"))
+    st = cfg.make_storage(num_layers=2, num_kv_heads=2, head_dim=8, dtype=torch.float32, device=torch.device("cpu"))
+    assert isinstance(st, TieredStorage) and st.num_layers == 2 and st.block_size == cfg.block_size
+
+
+@pytest.mark.parametrize("text,want", [
+    ("hot_ratio=0.05,score_alpha=1.0", {"hot_ratio": 0.05, "score_alpha": 1.0}),
+    ("tiers=['gpu','dram','nvme'],async_refetch=False", {"tiers": ["gpu", "dram", "nvme"], "async_refetch": False}),
+    ("layerwise_budget=pyramid", {"layerwise_budget": "pyramid"}),
+    ("", {}), ("   ", {}),
+    ("extra={'a': 1, 'b': [2, 3]},note='x,y'", {"extra": {"a": 1, "b": [2, 3]}, "note": "x,y"}),
+])
+def test_parse_overrides(text, want):
+    from halo_amd import parse_overrides
+    assert parse_overrides(text) == want
+
+
+def test_with_overrides_and_env(monkeypatch):
+    from halo_amd import HALOConfig, parse_overrides
+    cfg = HALOConfig()
+    new = cfg.with_overrides({"hot_ratio": 0.30, "lookahead": 4, "some_research_knob": 0.5})
+    assert new.hot_ratio == 0.30 and new.lookahead == 4 and new.extra == {"some_research_knob": 0.5}
+    assert cfg.hot_ratio == 0.10 and cfg.extra == {}
+    monkeypatch.setenv("HALO_OVERRIDES", "hot_ratio=0.20,sink_tokens=8")
+    assert parse_overrides() == {"hot_ratio": 0.20, "sink_tokens": 8}
+
+
+def test_storage_directory_and_moves(storage_factory):
+    st = storage_factory()
+    assert st.locate_block(layer=0, block=0) == "gpu"
+    bs = st.block_size
+    keys = torch.arange(2 * bs * 8, dtype=torch.float32).reshape(2, bs, 8)
+    values = torch.zeros_like(keys) - 1
+    st.write_new_block(layer=0, block=1, keys=keys, values=values, tier="gpu")
+    st.move_block(layer=0, block=1, src="gpu", dst="dram")
+    assert st.locate_block(layer=0, block=1) == "dram"
+    rk, rv = st.read_block(layer=0, block=1)
+    torch.testing.assert_close(rk, keys)
+    torch.testing.assert_close(rv, values)
+    st.move_block(layer=0, block=0, src="gpu", dst="gpu")
+    assert st.locate_block(layer=0, block=0) == "gpu"
+    with pytest.raises(ValueError):
+        st.write_new_block(layer=0, block=2, keys=keys, values=values, tier="nvme")
+
+
+def test_nvme_tier_round_trip(tmp_path):
+    from halo_amd import MemoryTier, TieredStorage
+    st = TieredStorage(tiers=[MemoryTier.GPU, MemoryTier.DRAM, MemoryTier.NVME], num_layers=2, num_kv_heads=2,
+                       head_dim=8, block_size=4, dtype=torch.bfloat16, device=torch.device("cpu"),
+                       nvme_path=str(tmp_path), max_blocks=8)
+    keys = torch.randn(2, 4, 8).to(torch.bfloat16)
+    values = torch.randn(2, 4, 8).to(torch.bfloat16)
+    st.write_new_block(layer=1, block=5, keys=keys, values=values, tier="gpu")
+    st.move_block(layer=1, block=5, src="gpu", dst="nvme")
+    assert st.locate_block(layer=1, block=5) == "nvme"
+    rk, rv = st.read_block(layer=1, block=5)
+    assert torch.equal(rk, keys) and torch.equal(rv, values)
+
+
+def test_refetch_schedule_counts_hits_and_misses(small_config, storage_factory):
+    from halo_amd import HALORefetcher
+    st = storage_factory()
+    bs = st.block_size
+    for blk, tier in ((0, "gpu"), (1, "dram")):
+        st.write_new_block(layer=0, block=blk, keys=torch.randn(2, bs, 8), values=torch.randn(2, bs, 8), tier=tier)
+    r = HALORefetcher(small_config, storage=st)
+    r.schedule(layer=0, predicted_indices=[0, 1, 4, 5])
+    assert (r.hits, r.misses) == (1, 1)
+    assert st.locate_block(layer=0, block=1) == "gpu"
+    r.schedule(layer=0, predicted_indices=torch.tensor([0, 4]))
+    assert (r.hits, r.misses) == (3, 1)
+
+
+def test_demote_flush_and_tensor_indices(small_config, storage_factory):
+    from halo_amd import HALODemoter
+    st = storage_factory()
+    bs = st.block_size
+    for blk in (0, 1, 2):
+        st.write_new_block(layer=0, block=blk, keys=torch.randn(2, bs, 8), values=torch.randn(2, bs, 8), tier="gpu")
+    d = HALODemoter(small_config, storage=st)
+    d.demote(layer=0, block_indices=[0, 1], src="gpu", dst="dram")
+    d.demote(layer=0, block_indices=torch.tensor([2]), src="gpu", dst="dram")
+    assert [st.locate_block(layer=0, block=b) for b in (0, 1, 2)] == ["dram"] * 3
+
+
+def test_chunked_cache_peels_and_counts():
+    """Warm-up keeps everything; the first 1-token step past 2*chunk_size
+    peels all but recent_window rows into chunk_size host chunks; later steps
+    peel once the recent rows exceed recent_window + chunk_size."""
+    from halo_amd import HALOCacheChunked, HALOConfig
+    cfg = HALOConfig(chunk_size=16, recent_window=4, block_size=4)
+    cache = HALOCacheChunked(config=cfg, chunk_size=16, recent_window=4)
+    k = torch.randn(1, 2, 40, 8)
+    v = torch.randn(1, 2, 40, 8)
+    K, _ = cache.update(k, v, 0)
+    assert K.shape[-2] == 40 and cache._mode == "warmup"
+    K, _ = cache.update(torch.randn(1, 2, 1, 8), torch.randn(1, 2, 1, 8), 0)
+    assert cache._mode == "chunked" and K.shape[-2] == 4
+    assert cache.get_seq_length(0) == 41
+    cold = cache._cold[0]
+    assert cold.rows == 37 and [c.shape[-2] for c, _, _ in cold.chunks()] == [16, 16, 5]
+    got = torch.cat([c for c, _, _ in cold.chunks()], dim=-2)
+    assert torch.equal(got, k[..., :37, :])
+    for _ in range(16):
+        cache.update(torch.randn(1, 2, 1, 8), torch.randn(1, 2, 1, 8), 0)
+    assert cache.get_seq_length(0) == 57 and cache._k[0].shape[-2] <= 4 + 16
+    assert cache.demoted_blocks_total > 0
+    cache.reset()
+    assert cache.get_seq_length(0) == 0 and cache._mode == "warmup"
+
+
+def test_wrap_with_halo_attaches_components():
+    from halo_amd import HALOCacheChunked, HALOConfig, wrap_with_halo
+
+    class Cfg:
+        num_hidden_layers, num_key_value_heads, num_attention_heads, hidden_size = 2, 2, 4, 32
+
+    class Attn(torch.nn.Module):
+        def __init__(self, i):
+            super().__init__()
+            self.layer_idx = i
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.config = Cfg()
+            self.w = torch.nn.Linear(4, 4)
+            self.layers = torch.nn.ModuleList([Attn(0), Attn(1)])
+
+    m = wrap_with_halo(Model(), HALOConfig(chunked=True))
+    assert isinstance(m._halo_cache, HALOCacheChunked)
+    assert m._halo_storage.num_layers == 2 and m._halo_storage.head_dim == 8
+    assert all(getattr(a, "_halo_cache", None) is m._halo_cache for a in m.layers)
+    with pytest.raises(ValueError):
+        wrap_with_halo(Model(), HALOConfig(chunked=True, eviction=True))

@@ -50,6 +50,7 @@ class SelectCfg(ctypes.Structure):
         ("n_cold", _i32), ("top_k", _i32), ("slot0", _i32), ("per_row", _i32),
         ("idx_out", _c_void_p),
         ("score_out", _c_void_p),
+        ("lead_items", _i32), ("reserved", _i32),
     ]
 
 

@@ -229,13 +229,10 @@ __device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const 
 }
 
 // ---------------------------------------------------------------------------
-// Fused chunk selection (selection-slot workgroups only).  Same arithmetic
-// as halo_chunk_score_topk: GQA-mean query rounded to the q dtype, ordered
-// fp32 dot products with the page means (products and sums rounded
-// separately), max over (row, KV head), rank by (score desc, index asc).
-// Every load is issued before the first barrier: one memory round trip.
-// Returns the chunk index for `slot` (-1: slot past the eligible count);
-// the chosen descriptors are left in LDS at s_cat.
+// Fused chunk selection (selection-slot workgroups only): every global load
+// is issued before the first wait, so the selection costs one memory round
+// trip; workgroups the launch marks as leading slot items issue those loads
+// before reading their work record.
 // ---------------------------------------------------------------------------
 constexpr int kSelMaxCold = 64;
 constexpr int kSelTPT = 2;  // (page, row, head) triples per thread: at most 2 x 256 per selection
@@ -269,170 +266,215 @@ __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d
 }
 
 template <int DT, int D, int NT>
-__device__ int fused_select(const DecodeParams& P, int b, char* smem, int slot, bool writer) {
+struct Selector {
   using E = Elem<DT>;
-  constexpr int EP = E::per16;
-  constexpr int PIECES = D / EP;                               // 16-byte pieces per row
-  constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
-  constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
-  constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
-  constexpr int QB = 8;                                        // query heads summed per load batch
-  constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
-  const halo_select_cfg& S = P.sel;
-  const int tid = threadIdx.x;
-  const int rows = S.per_row ? 1 : P.B;
-  const int b0 = S.per_row ? b : 0;
-  const int sel = S.per_row ? b : 0;
-  const int n = __builtin_amdgcn_readfirstlane(S.n_cold_per_sel ? min(S.n_cold_per_sel[sel], S.n_cold) : S.n_cold);
-  const int kk = min(S.top_k, n);
-  const int H_kv = P.H_kv, rep = P.rep;
-  const int nrh = rows * H_kv;
-  const int triples = n * nrh;
-  float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
-  float* s_dot = s_qbar + kSelQbarLds;
-  int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
-  halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
-
-  // Every global load below is issued before the first wait: the page-mean
-  // rows of this thread's (page, row, head) triples (at most kSelTPT),
-  // its share of the candidate descriptors and its query pieces.
-  uint4 kb[kSelTPT][PIECES];
+  static constexpr int EP = E::per16;
+  static constexpr int PIECES = D / EP;                               // 16-byte pieces per row
+  static constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
+  static constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
+  static constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
+  static constexpr int QB = 8;                                        // query heads summed per load batch
+  static constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
+  // triples whose page-mean rows are loaded up front (the rest, only with
+  // rows wider than 256 bytes, are loaded where they are used)
+  static constexpr int TE = PIECES <= 16 ? kSelTPT : 1;
+  uint4 kb[TE][PIECES];       // page-mean rows of this thread's (page, row, head) triples
   int my_r[kSelTPT], my_h[kSelTPT];
+  uint2 cw[CW];               // this thread's share of the candidate descriptors
+  uint4 qv[QP][QB];           // first QB query heads of this thread's q-bar pieces (aligned q)
+  int n, kk, rows, b0, sel, nrh, triples;
+
+  // Issue every global load of the selection (no waits): page-mean rows,
+  // candidate descriptors, the first batch of query pieces.
+  __device__ __forceinline__ void issue(const DecodeParams& P, int b) {
+    const halo_select_cfg& S = P.sel;
+    const int tid = threadIdx.x;
+    rows = S.per_row ? 1 : P.B;
+    b0 = S.per_row ? b : 0;
+    sel = S.per_row ? b : 0;
+    n = __builtin_amdgcn_readfirstlane(S.n_cold_per_sel ? min(S.n_cold_per_sel[sel], S.n_cold) : S.n_cold);
+    kk = min(S.top_k, n);
+    nrh = rows * P.H_kv;
+    triples = n * nrh;
 #pragma unroll
-  for (int u = 0; u < kSelTPT; ++u) {
-    const int t = tid + u * NT;
-    my_r[u] = 0;
-    my_h[u] = 0;
-    if (t < triples) {
-      const int i = t / nrh, rh = t % nrh;
-      my_r[u] = rh / H_kv;
-      my_h[u] = rh % H_kv;
-      const char* row = reinterpret_cast<const char*>(S.kmean) +
-                        ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
-                         (int64_t)i * S.km_stride_p) * E::size;
+    for (int u = 0; u < kSelTPT; ++u) {
+      const int t = tid + u * NT;
+      my_r[u] = 0;
+      my_h[u] = 0;
+      if (t < triples) {
+        const int i = t / nrh, rh = t % nrh;
+        my_r[u] = rh / P.H_kv;
+        my_h[u] = rh % P.H_kv;
+        if (u < TE) {
+          const char* row = reinterpret_cast<const char*>(S.kmean) +
+                            ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
+                             (int64_t)i * S.km_stride_p) * E::size;
 #pragma unroll
-      for (int c = 0; c < PIECES; ++c) kb[u][c] = *reinterpret_cast<const uint4*>(row + c * 16);
+          for (int c = 0; c < PIECES; ++c) kb[u < TE ? u : 0][c] = *reinterpret_cast<const uint4*>(row + c * 16);
+        }
+      }
+    }
+    const uint2* cat = reinterpret_cast<const uint2*>(S.catalog + (int64_t)sel * S.catalog_stride);
+#pragma unroll
+    for (int k = 0; k < CW; ++k) {
+      const int w = tid + k * NT;
+      if (w < n * DW2) cw[k] = cat[w];
+    }
+    if (P.q_aligned) {
+      const int npieces = rows * P.H_kv * PIECES;
+#pragma unroll
+      for (int k = 0; k < QP; ++k) {
+        const int pc = tid + k * NT;
+        if (pc < npieces) {
+          const int c = pc % PIECES, h = (pc / PIECES) % P.H_kv, r = pc / (PIECES * P.H_kv);
+          const char* qrow = reinterpret_cast<const char*>(P.q) +
+                             ((int64_t)(b0 + r) * P.q_stride_b + (int64_t)h * P.rep * P.q_stride_h) * E::size + c * 16;
+#pragma unroll
+          for (int j = 0; j < QB; ++j)
+            if (j < P.rep) qv[k][j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)j * P.q_stride_h * E::size);
+        }
+      }
     }
   }
-  const uint2* cat = reinterpret_cast<const uint2*>(S.catalog + (int64_t)sel * S.catalog_stride);
-  uint2 cw[CW];
+
+  // Same arithmetic as halo_chunk_score_topk: GQA-mean query rounded to the
+  // q dtype, ordered fp32 dot products with the page means (products and
+  // sums rounded separately), max over (row, KV head), rank by (score desc,
+  // index asc).  Returns the chunk index for `slot` (-1: slot past the
+  // eligible count); the chosen descriptors are left in LDS at s_cat.
+  __device__ __forceinline__ int finish(const DecodeParams& P, char* smem, int slot, bool writer) {
+    const halo_select_cfg& S = P.sel;
+    const int tid = threadIdx.x;
+    const int H_kv = P.H_kv, rep = P.rep;
+    float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
+    float* s_dot = s_qbar + kSelQbarLds;
+    int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
+    halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
+    // GQA-mean query rows: fp32 sum over the rep heads in head order, times
+    // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
+    if (P.q_aligned) {
+      const int npieces = rows * H_kv * PIECES;
 #pragma unroll
-  for (int k = 0; k < CW; ++k) {
-    const int w = tid + k * NT;
-    if (w < n * DW2) cw[k] = cat[w];
-  }
-  // GQA-mean query rows: fp32 sum over the rep heads in head order, times
-  // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
-  if (P.q_aligned) {
-    const int npieces = rows * H_kv * PIECES;
+      for (int k = 0; k < QP; ++k) {
+        const int pc = tid + k * NT;
+        if (pc >= npieces) break;
+        const int c = pc % PIECES, h = (pc / PIECES) % H_kv, r = pc / (PIECES * H_kv);
+        const char* qrow = reinterpret_cast<const char*>(P.q) +
+                           ((int64_t)(b0 + r) * P.q_stride_b + (int64_t)h * rep * P.q_stride_h) * E::size + c * 16;
+        float acc[EP];
 #pragma unroll
-    for (int k = 0; k < QP; ++k) {
-      const int pc = tid + k * NT;
-      if (pc >= npieces) break;
-      const int c = pc % PIECES, h = (pc / PIECES) % H_kv, r = pc / (PIECES * H_kv);
-      const char* qrow = reinterpret_cast<const char*>(P.q) +
-                         ((int64_t)(b0 + r) * P.q_stride_b + (int64_t)h * rep * P.q_stride_h) * E::size + c * 16;
-      float acc[EP];
-#pragma unroll
-      for (int e = 0; e < EP; ++e) acc[e] = 0.f;
-      for (int j0 = 0; j0 < rep; j0 += QB) {
-        uint4 qv[QB];
-#pragma unroll
-        for (int j = 0; j < QB; ++j)
-          if (j0 + j < rep) qv[j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)(j0 + j) * P.q_stride_h * E::size);
+        for (int e = 0; e < EP; ++e) acc[e] = 0.f;
 #pragma unroll
         for (int j = 0; j < QB; ++j) {
-          if (j0 + j < rep) {
+          if (j < rep) {
             float f[EP];
-            E::unpack(qv[j], f);
+            E::unpack(qv[k][j], f);
 #pragma unroll
             for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
           }
         }
-      }
-      float* dst = s_qbar + (r * H_kv + h) * QS + c * EP;
+        for (int j0 = QB; j0 < rep; j0 += QB) {
+          uint4 qx[QB];
 #pragma unroll
-      for (int e = 0; e < EP; ++e) {
-        float v = acc[e];
+          for (int j = 0; j < QB; ++j)
+            if (j0 + j < rep) qx[j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)(j0 + j) * P.q_stride_h * E::size);
+#pragma unroll
+          for (int j = 0; j < QB; ++j) {
+            if (j0 + j < rep) {
+              float f[EP];
+              E::unpack(qx[j], f);
+#pragma unroll
+              for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
+            }
+          }
+        }
+        float* dst = s_qbar + (r * H_kv + h) * QS + c * EP;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+          float v = acc[e];
+          if (rep != 1) {
+            v = opaque(v * P.inv_rep);
+            v = DT == HALO_F32 ? v
+                : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
+                                   : f16_bits_to_f32(f32_to_f16_rne(v)));
+          }
+          dst[e] = v;
+        }
+      }
+    } else {
+      for (int e = tid; e < rows * H_kv * D; e += NT) {
+        const int d = e % D, h = (e / D) % H_kv, r = e / (D * H_kv);
+        const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
+        float acc = 0.f;
+        for (int j = 0; j < rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * rep + j) * P.q_stride_h + d, DT);
+        float v = acc;
         if (rep != 1) {
           v = opaque(v * P.inv_rep);
           v = DT == HALO_F32 ? v
               : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
                                  : f16_bits_to_f32(f32_to_f16_rne(v)));
         }
-        dst[e] = v;
+        s_qbar[(e / D) * QS + d] = v;
       }
     }
-  } else {
-    for (int e = tid; e < rows * H_kv * D; e += NT) {
-      const int d = e % D, h = (e / D) % H_kv, r = e / (D * H_kv);
-      const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
-      float acc = 0.f;
-      for (int j = 0; j < rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * rep + j) * P.q_stride_h + d, DT);
-      float v = acc;
-      if (rep != 1) {
-        v = opaque(v * P.inv_rep);
-        v = DT == HALO_F32 ? v
-            : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
-                               : f16_bits_to_f32(f32_to_f16_rne(v)));
-      }
-      s_qbar[(e / D) * QS + d] = v;
-    }
-  }
 #pragma unroll
-  for (int k = 0; k < CW; ++k) {
-    const int w = tid + k * NT;
-    if (w < n * DW2) reinterpret_cast<uint2*>(s_cat)[w] = cw[k];
-  }
-  __syncthreads();
+    for (int k = 0; k < CW; ++k) {
+      const int w = tid + k * NT;
+      if (w < n * DW2) reinterpret_cast<uint2*>(s_cat)[w] = cw[k];
+    }
+    __syncthreads();
 
 #pragma unroll
-  for (int u = 0; u < kSelTPT; ++u) {
-    const int t = tid + u * NT;
-    if (t < triples) {
-      const float* qg = s_qbar + (my_r[u] * H_kv + my_h[u]) * QS;
-      float acc = 0.f;
+    for (int u = 0; u < kSelTPT; ++u) {
+      const int t = tid + u * NT;
+      if (t < triples) {
+        const float* qg = s_qbar + (my_r[u] * H_kv + my_h[u]) * QS;
+        const char* row = reinterpret_cast<const char*>(S.kmean) +
+                          ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
+                           (int64_t)(t / nrh) * S.km_stride_p) * E::size;
+        float acc = 0.f;
 #pragma unroll
-      for (int c = 0; c < PIECES; ++c) {
-        float f[EP];
-        E::unpack(kb[u][c], f);
+        for (int c = 0; c < PIECES; ++c) {
+          float f[EP];
+          E::unpack(u < TE ? kb[u < TE ? u : 0][c] : *reinterpret_cast<const uint4*>(row + c * 16), f);
 #pragma unroll
-        for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
+          for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
+        }
+        s_dot[t] = acc;
       }
-      s_dot[t] = acc;
     }
-  }
-  __syncthreads();
-  // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
-  // over (row, KV head), NaN -> -inf; rank by (score desc, index asc) with
-  // readlane broadcasts; the chosen chunks are listed in ascending index
-  // order with a ballot prefix count.
-  if (tid < kWave) {
-    const int i = tid;
-    float sc = -INFINITY;
-    if (i < n) {
-      float best = -INFINITY;
+    __syncthreads();
+    // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
+    // over (row, KV head), NaN -> -inf; rank by (score desc, index asc) with
+    // readlane broadcasts; the chosen chunks are listed in ascending index
+    // order with a ballot prefix count.
+    if (tid < kWave) {
+      const int i = tid;
+      float sc = -INFINITY;
+      if (i < n) {
+        float best = -INFINITY;
 #pragma unroll 8
-      for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
-      sc = (best != best) ? -INFINITY : best;
+        for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
+        sc = (best != best) ? -INFINITY : best;
+      }
+      int rank = 0;
+      for (int j = 0; j < n; ++j) {
+        const float sj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), j));
+        rank += (sj > sc || (sj == sc && j < i)) ? 1 : 0;
+      }
+      const bool chosen = i < n && rank < kk;
+      const uint64_t mask = __ballot(chosen);
+      const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+      if (chosen) s_pick[pos] = i;
+      if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
     }
-    int rank = 0;
-    for (int j = 0; j < n; ++j) {
-      const float sj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), j));
-      rank += (sj > sc || (sj == sc && j < i)) ? 1 : 0;
+    __syncthreads();
+    if (writer && S.idx_out) {
+      for (int j = tid; j < S.top_k; j += NT) S.idx_out[(int64_t)sel * S.top_k + j] = j < kk ? s_pick[j] : -1;
     }
-    const bool chosen = i < n && rank < kk;
-    const uint64_t mask = __ballot(chosen);
-    const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-    if (chosen) s_pick[pos] = i;
-    if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
+    return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
   }
-  __syncthreads();
-  if (writer && S.idx_out) {
-    for (int j = tid; j < S.top_k; j += NT) S.idx_out[(int64_t)sel * S.top_k + j] = j < kk ? s_pick[j] : -1;
-  }
-  return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
-}
+};
 
 // ---------------------------------------------------------------------------
 // Work-item epilogue shared by the decode kernels: reduce each wave's o over
@@ -551,6 +593,58 @@ __device__ __forceinline__ void write_partial_pairs(const DecodeParams& P, int w
   }
 }
 
+// Same, with the V-wave's o held as MFMA accumulators: lane l owns heads
+// 4*(l/16)..+4 of columns 16*db + l%16, so no cross-lane reduction is needed.
+template <int D, int REP, int NP, int DB>
+__device__ __forceinline__ void write_partial_pairs_mfma(const DecodeParams& P, int wslot, bool kwave, int pair,
+                                                         const f32x4 (&acc)[DB], const float* m_run,
+                                                         const float* l_head, float* s_wo, float (*s_wm)[REP],
+                                                         float (*s_wl)[REP]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  if (!kwave) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * (lane >> 4) + e;
+      if (h < REP) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) s_wo[(pair * REP + h) * D + db * 16 + (lane & 15)] = acc[db][e];
+      }
+    }
+  } else if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      s_wm[pair][r] = m_run[r];
+      s_wl[pair][r] = l_head[r];
+    }
+  }
+  __syncthreads();
+  float* wso = P.ws_o + (int64_t)wslot * REP * D;
+  for (int i = tid; i < REP * D; i += 64 * 2 * NP) {
+    const int r = i / D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc_o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) acc_o += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
+    wso[i] = acc_o;
+  }
+  if (tid < REP) {
+    const int r = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc_l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NP; ++w) acc_l += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc_l;
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ float from_bits16(uint16_t h) {
   if constexpr (DT == HALO_BF16) return __uint_as_float((uint32_t)h << 16);
@@ -573,6 +667,46 @@ struct MfmaOp<HALO_F16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
 };
+
+// Two fp32 values rounded to the K/V dtype and packed (lower index in the
+// low half): the probabilities enter the P.V product in that dtype.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == HALO_BF16) {
+    const bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    const f16x2_t v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+// V tile in LDS: row r holds its 16-byte pieces at positions piece ^ vswz(r)
+// (an even XOR, so the piece pairs the transposed reads use stay adjacent).
+// Four consecutive rows (one 16-lane transposed read) then cover distinct
+// 32-byte bank ranges, and rows 8 apart (the next lane group) are offset by
+// a further 128 bytes.
+template <int SL>
+__device__ __forceinline__ int vswz(int r) {
+  return (2 * (r & 3) + 8 * ((r >> 3) & 1)) & (SL - 1);
+}
+// K tile in LDS: row r holds piece c at position c ^ kswz(r), so the 16 rows
+// one MFMA operand read touches (same piece) land on distinct bank ranges.
+template <int SL>
+__device__ __forceinline__ int kswz(int r) {
+  return r & ((SL < 16 ? SL : 16) - 1);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
+// of the 8-byte reads of lanes 4e + i/4 (e = 0..3).  With lane p reading 4
+// consecutive columns 4(p%4).. of row p/4 of a 4-row block, lane i gets
+// column i of rows 0..3: the K-major operand layout of the MFMA.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)(__attribute__((address_space(3))) char*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
 
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
@@ -598,14 +732,18 @@ decode_attn_kernel(DecodeParams P) {
   static_assert(!kMfma || (REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL), "mfma tile shape");
 
   constexpr int NP = NW / 2;  // MFMA path: producer/consumer wave pairs
+  constexpr int DB = D / 16;  // MFMA path: 16-column blocks of the P.V product
+  constexpr int KS2 = TILE / 32;  // MFMA path: 32-row k-steps of the P.V product
   // VALU path: per-wave q copy, K tiles, p tiles; the epilogue reuses the front.
-  // MFMA path: per pair 2 p tiles and 2 rescale vectors, then the pair partials.
+  // MFMA path: per pair 2 p tiles (K/V dtype, [head][row]) and 2 rescale
+  // vectors, the pair partials, then one V tile per V-wave.
   constexpr int SZ_Q = kMfma ? 0 : NW * REP * RB;
   constexpr int SZ_K = kMfma ? 0 : NW * TILE * KROW;
-  constexpr int SZ_P = kMfma ? NP * 2 * TILE * REP * 4 : NW * TILE * REP * 4;
+  constexpr int SZ_P = kMfma ? NP * 2 * REP * TILE * 2 : NW * TILE * REP * 4;
   constexpr int SZ_AL = kMfma ? (NP * 2 * REP * 4 + 15) / 16 * 16 : 0;
   constexpr int SZ_WO = kMfma ? NP * REP * D * 4 : 0;
-  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO;
+  constexpr int SZ_VT = kMfma ? NP * TILE * RB : 0;  // one V tile per V-wave, one K tile per K-wave
+  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO + 2 * SZ_VT;
   constexpr int SZ_A = SZ_A0 > kSelBytes ? SZ_A0 : kSelBytes;
   constexpr int SZ_B = kMfma ? 0 : NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
@@ -614,6 +752,8 @@ decode_attn_kernel(DecodeParams P) {
   float* s_pall = reinterpret_cast<float*>(smem + SZ_Q + SZ_K);
   float* s_alpha = reinterpret_cast<float*>(smem + SZ_Q + SZ_K + SZ_P);
   float* s_wo = reinterpret_cast<float*>(kMfma ? smem + SZ_Q + SZ_K + SZ_P + SZ_AL : smem);
+  char* s_vt = smem + SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO;
+  char* s_kt = s_vt + SZ_VT;
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
 
   const int tid = threadIdx.x;
@@ -622,6 +762,11 @@ decode_attn_kernel(DecodeParams P) {
   // derived from them (buffer descriptors, row ranges) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int witem = blockIdx.x;
+  // Leading selection-slot items start the selection's loads at once (the
+  // selection does not depend on the record unless it is per batch row).
+  Selector<DT, D, 64 * NW> selr;
+  const bool early_sel = P.sel_on && !P.sel.per_row && witem < P.sel.lead_items;
+  if (early_sel) selr.issue(P, 0);
 
   const int32_t* wrec = P.work + (int64_t)witem * kWorkInts;
   int4 item = *reinterpret_cast<const int4*>(wrec);
@@ -640,7 +785,8 @@ decode_attn_kernel(DecodeParams P) {
   if (P.sel_on && item.x >= P.sel.slot0 && item.x < P.sel.slot0 + P.sel.top_k) {
     // selection slot: choose the chunk first (workgroup-uniform branch)
     const bool writer = (P.sel.per_row || b == 0) && h_kv == 0 && sub == 0 && item.x == P.sel.slot0 && item.z == 0;
-    const int pick = fused_select<DT, D, 64 * NW>(P, b, smem, item.x - P.sel.slot0, writer);
+    if (!early_sel) selr.issue(P, b);
+    const int pick = selr.finish(P, smem, item.x - P.sel.slot0, writer);
     if (pick >= 0) {
       dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4)[pick]);
     } else {
@@ -677,6 +823,7 @@ decode_attn_kernel(DecodeParams P) {
   const int we = min(t1, ws + tiles_per_wave * TILE);
 
   float m_run[REP], acc_o[REP][EP], l_head[REP];
+  f32x4 acc_pv[kMfma ? D / 16 : 1];  // MFMA path: P.V accumulators (heads x columns)
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m_run[r] = -INFINITY;
@@ -693,22 +840,27 @@ decode_attn_kernel(DecodeParams P) {
     // ---- Producer/consumer wave pairs: every wave streams ONE contiguous
     // row range of ONE tensor (on gfx950 a wave that streams two distant
     // regions at once pulls markedly less bandwidth than one that streams a
-    // single region).  Waves [0, NP) read K and compute the scores on
-    // v_mfma_f32_16x16x32 (A = 16 K rows x 32 elements: lane l holds row
-    // l%16, elements 8*(l/16)..+8 of the k-step; B = q^T: lane l holds head
-    // l%16; D: lane l holds head l%16, rows 4*(l/16)..+4) and the online
-    // softmax; waves [NP, NW) read V and accumulate P.V with the tile's
-    // probabilities and rescale factors their partner leaves in LDS
-    // (double-buffered by tile parity, one workgroup barrier per tile).
-    // Each wave keeps two tiles of loads in flight.
+    // single region), 1 KiB of consecutive rows per load instruction (whole
+    // 128-byte lines; the MFMA operand layout read straight from memory
+    // would split every line over two instructions).  Each tile is staged
+    // in the wave's own LDS slot and read back in operand layout.  Waves
+    // [0, NP) read K and compute the scores on v_mfma_f32_16x16x32 (A = 16 K
+    // rows x 32 elements: lane l holds row l%16, elements 8*(l/16)..+8 of
+    // the k-step; B = q^T: lane l holds head l%16; D: lane l holds head
+    // l%16, rows 4*(l/16)..+4) and the online softmax; waves [NP, NW) read V
+    // and accumulate P.V with the tile's probabilities and rescale factors
+    // their partner leaves in LDS (double-buffered by tile parity, one
+    // workgroup barrier per tile).  Each wave keeps two tiles of loads in
+    // flight (one at D = 256).
     constexpr int NBUF = NB * KS;
     static_assert(NBUF == PPL, "K and V tiles use the same register budget");
+    constexpr int TIF = D > 128 ? 1 : 2;  // tiles in flight per wave (register budget)
     const bool kwave = wave < NP;
     const int pair = kwave ? wave : wave - NP;
     const int tpp = (ntiles_total + NP - 1) / NP;   // tiles per pair, uniform in the workgroup
     const int ps = t0 + pair * tpp * TILE;
     const int pe = min(t1, ps + tpp * TILE);
-    float* pbuf = s_pall + pair * 2 * TILE * REP;
+    uint16_t* pbuf = reinterpret_cast<uint16_t*>(s_pall) + pair * 2 * REP * TILE;
     float* abuf = s_alpha + pair * 2 * REP;
     const int hl = lane & 15;   // score layout: head
     const int kg = lane >> 4;   // score layout: k-group / row quad
@@ -734,31 +886,40 @@ decode_attn_kernel(DecodeParams P) {
     if (kwave) {
       float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
       float l_lane = 0.f;        // this lane's share of head hl's denominator
-      for (int it = 0; it < tpp; it += 2) {
-        uint4 buf[2][NBUF];
+      char* kt = s_kt + pair * TILE * RB;
+      for (int it = 0; it < tpp; it += TIF) {
+        uint4 buf[TIF][NBUF];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < TIF; ++u) {
           const int tb = ps + (it + u) * TILE;
           const __amdgpu_buffer_rsrc_t rr = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(pe - tb) * kst);
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-              buf[u][nb * KS + s] = buf_ld16(rr, (int)((nb * 16 + hl) * kst) + s * 64 + kg * 16);
+          for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * kst) + voff0);
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < TIF; ++u) {
           if (it + u >= tpp) break;
           const int tb = ps + (it + u) * TILE;
           const int nrows = min(TILE, pe - tb);  // <= 0: every row masked
-          float* pt = pbuf + ((it + u) & 1) * TILE * REP;
+          uint16_t* pt = pbuf + ((it + u) & 1) * REP * TILE;
           float* at = abuf + ((it + u) & 1) * REP;
+          // stage the tile (rows past the slice arrived as zeros), read it
+          // back as MFMA A operands (this wave's own slot: no barrier)
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const int r = i * RPI + my_row0;
+            *reinterpret_cast<uint4*>(kt + r * RB + ((my_col ^ kswz<SL>(r)) << 4)) = buf[u][i];
+          }
           f32x4 sc[NB];
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             sc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int r = nb * 16 + hl;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) sc[nb] = MfmaOp<DT>::run(buf[u][nb * KS + s], qb[s], sc[nb]);
+            for (int s = 0; s < KS; ++s) {
+              const uint4 a = *reinterpret_cast<const uint4*>(kt + r * RB + (((s * 4 + kg) ^ kswz<SL>(r)) << 4));
+              sc[nb] = MfmaOp<DT>::run(a, qb[s], sc[nb]);
+            }
           }
           float sv[NB][4], bm = -INFINITY;
 #pragma unroll
@@ -777,13 +938,18 @@ decode_attn_kernel(DecodeParams P) {
           m_lane = m_new;
           float psum = 0.f;
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
+          for (int nb = 0; nb < NB; ++nb) {
+            float p4[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-              const float p = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
-              psum += p;
-              if (hl < REP) pt[(nb * 16 + kg * 4 + c) * REP + hl] = p;
+              p4[c] = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
+              psum += p4[c];
             }
+            // rows nb*16 + 4kg .. +3 of head hl: one 8-byte store
+            if (hl < REP)
+              *reinterpret_cast<uint2*>(pt + hl * TILE + nb * 16 + kg * 4) =
+                  make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
+          }
           l_lane = l_lane * alpha + psum;
           if (lane < REP) at[lane] = alpha;
           __syncthreads();  // hand the tile's p and rescale factors to the V-wave
@@ -797,49 +963,64 @@ decode_attn_kernel(DecodeParams P) {
         l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
       }
     } else {
-      for (int it = 0; it < tpp; it += 2) {
-        uint4 buf[2][NBUF];
+      // P.V on v_mfma_f32_16x16x32: A = P^T (lane l: head l%16, rows
+      // 8*(l/16)..+8 of the 32-row k-step, read from the K-wave's [head][row]
+      // tile), B = V (lane l: column l%16 of the 16-column block, the same 8
+      // rows, gathered from the LDS copy of the tile with two transposed
+      // reads), D: lane l holds heads 4*(l/16)..+4 of column l%16.
+      char* vt = s_vt + pair * TILE * RB;
+      const int hA = lane & 15;           // A operand head
+      const int gq = lane >> 4;           // lane group: 8-row slab of the k-step
+      const int prow = (lane & 15) >> 2;  // transposed read: row within the 4-row block
+      const int pcol = lane & 3;          // transposed read: 4-column group
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+      for (int db = 0; db < DB; ++db) acc_pv[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int it = 0; it < tpp; it += TIF) {
+        uint4 buf[TIF][NBUF];
+#pragma unroll
+        for (int u = 0; u < TIF; ++u) {
           const int tb = ps + (it + u) * TILE;
           const __amdgpu_buffer_rsrc_t rr = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(pe - tb) * vst);
 #pragma unroll
           for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * vst) + voff0);
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < TIF; ++u) {
           if (it + u >= tpp) break;
-          const float* pt = pbuf + ((it + u) & 1) * TILE * REP;
+          // stage the tile (rows past the slice arrived as zeros)
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const int r = i * RPI + my_row0;
+            *reinterpret_cast<uint4*>(vt + r * RB + ((my_col ^ vswz<SL>(r)) << 4)) = buf[u][i];
+          }
+          const uint16_t* pt = reinterpret_cast<const uint16_t*>(s_pall) + pair * 2 * REP * TILE +
+                               ((it + u) & 1) * REP * TILE;
           const float* at = abuf + ((it + u) & 1) * REP;
           __syncthreads();  // the K-wave's p and rescale factors for this tile are in LDS
-          float al[REP];
-          bool rescale = false;
 #pragma unroll
-          for (int r = 0; r < REP; ++r) {
-            al[r] = at[r];
-            rescale |= al[r] != 1.f;
-          }
-          if (rescale) {
+          for (int e = 0; e < 4; ++e) {
+            const float a = at[min(4 * gq + e, REP - 1)];
 #pragma unroll
-            for (int r = 0; r < REP; ++r)
-#pragma unroll
-              for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
+            for (int db = 0; db < DB; ++db) acc_pv[db][e] *= a;
           }
 #pragma unroll
-          for (int j = 0; j < PPL; j += 2) {
-            const int ra = j * RPI + my_row0, rbw = (j + 1) * RPI + my_row0;
-            float pa[REP], pb[REP];
+          for (int s2 = 0; s2 < KS2; ++s2) {
+            const uint4 pa = hA < REP ? *reinterpret_cast<const uint4*>(pt + hA * TILE + s2 * 32 + gq * 8)
+                                      : make_uint4(0, 0, 0, 0);
+            const int r0 = s2 * 32 + gq * 8 + prow;
 #pragma unroll
-            for (int r = 0; r < REP; ++r) {
-              pa[r] = pt[ra * REP + r];
-              pb[r] = pt[rbw * REP + r];
+            for (int db = 0; db < DB; ++db) {
+              const int pc = 2 * db + (pcol >> 1);
+              const int bo = (pcol & 1) * 8;
+              const uint2 lo = lds_read_tr16(vt + r0 * RB + ((pc ^ vswz<SL>(r0)) << 4) + bo);
+              const uint2 hi = lds_read_tr16(vt + (r0 + 4) * RB + ((pc ^ vswz<SL>(r0 + 4)) << 4) + bo);
+              acc_pv[db] = MfmaOp<DT>::run(pa, make_uint4(lo.x, lo.y, hi.x, hi.y), acc_pv[db]);
             }
-            pv_pair<DT, REP, EP>(buf[u][j], buf[u][j + 1], pa, pb, acc_o);
           }
         }
       }
     }
-    write_partial_pairs<D, REP, NP, SL, EP>(P, wslot, kwave, pair, acc_o, m_run, l_head, s_wo, s_wm, s_wl);
+    write_partial_pairs_mfma<D, REP, NP, DB>(P, wslot, kwave, pair, acc_pv, m_run, l_head, s_wo, s_wm, s_wl);
     return;
   } else {
     // ---- VALU path (fp32): K transposed through LDS, lane groups per head.
@@ -1470,6 +1651,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
     HALO_CHECK_ARG(S.top_k >= 1 && S.slot0 >= 0 && S.slot0 + S.top_k <= n_desc,
                    "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
     HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");
+    HALO_CHECK_ARG(S.lead_items >= 0, "lead_items must be >= 0");
     HALO_CHECK_ARG(S.n_cold * rows * H_kv <= kSelTPT * 256, "n_cold * rows * H_kv must be <= 512");
     HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
     HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(S.kmean) % 16 == 0 && (S.km_stride_b * esz) % 16 == 0 &&

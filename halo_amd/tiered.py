@@ -78,7 +78,18 @@ class TieredDecodeLayer:
                 kmean=km.data_ptr(), km_stride_b=km.stride(0), km_stride_h=km.stride(1), km_stride_p=km.stride(2),
                 catalog=self.catalog.data_ptr(), catalog_stride=n_cold, n_cold_per_sel=None,
                 n_cold=n_cold, top_k=top_k, slot0=self.slot0, per_row=0,
-                idx_out=self.idx.data_ptr(), score_out=self.scores.data_ptr())
+                idx_out=self.idx.data_ptr(), score_out=self.scores.data_ptr(),
+                lead_items=self._lead_items())
+
+    def _lead_items(self) -> int:
+        """Number of leading work records (dispatch order) that are selection
+        slots: those workgroups start the selection before reading their record."""
+        d = self.plan.work_host[:, 0]
+        slot = (d >= self.slot0) & (d < self.slot0 + self.top_k)
+        n = 0
+        while n < len(slot) and slot[n]:
+            n += 1
+        return n
 
     def build_means(self, cold: Sequence[ChunkRef]) -> torch.Tensor:
         """One mean key per cold chunk (B, H_kv, n_cold, D)."""

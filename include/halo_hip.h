@@ -141,6 +141,11 @@ typedef struct halo_select_cfg {
   int32_t n_cold, top_k, slot0, per_row;
   int32_t* idx_out;
   float* score_out;
+  /* The first lead_items work records (dispatch order) are selection-slot
+   * items (0 = not stated).  Those workgroups start the selection's loads
+   * before reading their record; a wrong count costs loads, not results. */
+  int32_t lead_items;
+  int32_t reserved;
 } halo_select_cfg;
 
 /*

@@ -43,10 +43,11 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_select_cfg_layout_matches_header():
-    """halo_select_cfg: 4 pointers + 4 int64 + ... = 88 bytes, field order as declared."""
+    """halo_select_cfg: 5 pointers + 4 int64 + 6 int32 = 96 bytes, field order as declared."""
     from halo_amd import _native as nat
-    assert ctypes.sizeof(nat.SelectCfg) == 88
+    assert ctypes.sizeof(nat.SelectCfg) == 96
     assert nat.SelectCfg.n_cold.offset == 56 and nat.SelectCfg.idx_out.offset == 72
+    assert nat.SelectCfg.lead_items.offset == 88
 
 
 def test_descriptor_record_size():

@@ -82,6 +82,22 @@ __device__ __forceinline__ void store_elem(void* base, int64_t idx, int dtype, f
   }
 }
 
+// Store four consecutive fp32 values as elements `dtype` (idx a multiple of
+// 4 and the row base 8-byte aligned for 16-bit types, 16-byte for fp32).
+__device__ __forceinline__ void store_elem4(void* base, int64_t idx, int dtype, const float* v) {
+  if (dtype == HALO_F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (dtype == HALO_BF16) {
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(base) + idx) =
+        make_uint2((uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+                   (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16));
+  } else {
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(base) + idx) =
+        make_uint2((uint32_t)f32_to_f16_rne(v[0]) | ((uint32_t)f32_to_f16_rne(v[1]) << 16),
+                   (uint32_t)f32_to_f16_rne(v[2]) | ((uint32_t)f32_to_f16_rne(v[3]) << 16));
+  }
+}
+
 __device__ __forceinline__ float load_elem(const void* base, int64_t idx, int dtype) {
   if (dtype == HALO_F32) return reinterpret_cast<const float*>(base)[idx];
   uint16_t h = reinterpret_cast<const uint16_t*>(base)[idx];

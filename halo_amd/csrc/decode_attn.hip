@@ -39,6 +39,7 @@ struct MergeParams {
   int acc_mode;
   void* out;
   int out_dtype;
+  int out_vec;  // out is aligned for 4-element vector stores
   float* lse;
   const float* ws_o;
   const float* ws_ml;
@@ -1417,30 +1418,31 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
   const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4 + col;
   const float* wml = P.ws_ml + ((int64_t)gbeg * REP + r) * 2;
   constexpr int MB = 8;  // partials per thread whose loads are issued together
+  // Loads are unconditional (the slot index is clamped into the group) so
+  // the batch is issued back to back; slots past the group are masked in
+  // the merge arithmetic.
   for (int p0 = phase; p0 < np; p0 += MB * TPC) {
-    float mp[MB], lp[MB];
+    float2 ml[MB];
     float4 op[MB];
 #pragma unroll
     for (int k = 0; k < MB; ++k) {
-      const int pp = p0 + k * TPC;
-      if (pp < np) {
-        mp[k] = wml[(int64_t)pp * REP * 2];
-        lp[k] = wml[(int64_t)pp * REP * 2 + 1];
-        op[k] = wo4[(int64_t)pp * REP * C4];
-      }
+      const int pp = min(p0 + k * TPC, np - 1);
+      ml[k] = *reinterpret_cast<const float2*>(wml + (int64_t)pp * REP * 2);
+      op[k] = wo4[(int64_t)pp * REP * C4];
     }
 #pragma unroll
     for (int k = 0; k < MB; ++k) {
-      if (p0 + k * TPC >= np) break;
-      const float mn = fmaxf(mt, mp[k]);
-      const float ms = (mn == -INFINITY) ? 0.f : mn;
-      const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(mp[k] - ms);
-      lt = lt * a + lp[k] * c;
-      ot.x = ot.x * a + op[k].x * c;
-      ot.y = ot.y * a + op[k].y * c;
-      ot.z = ot.z * a + op[k].z * c;
-      ot.w = ot.w * a + op[k].w * c;
-      mt = mn;
+      if (p0 + k * TPC < np) {
+        const float mn = fmaxf(mt, ml[k].x);
+        const float ms = (mn == -INFINITY) ? 0.f : mn;
+        const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(ml[k].x - ms);
+        lt = lt * a + ml[k].y * c;
+        ot.x = ot.x * a + op[k].x * c;
+        ot.y = ot.y * a + op[k].y * c;
+        ot.z = ot.z * a + op[k].z * c;
+        ot.w = ot.w * a + op[k].w * c;
+        mt = mn;
+      }
     }
   }
   // The incoming accumulator is read by every thread before the barrier:
@@ -1452,20 +1454,30 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
   s_o[tid] = ot;
   __syncthreads();
   if (phase != 0) return;
-  // combine the TPC partial merges of this column in phase order
+  // combine the TPC partial merges of this column in phase order (every LDS
+  // read issued first)
+  float pm[TPC], pl[TPC];
+  float4 po[TPC];
+#pragma unroll
+  for (int ph = 0; ph < TPC; ++ph) {
+    pm[ph] = s_m[ph * C4 + col];
+    pl[ph] = s_l[ph * C4 + col];
+    po[ph] = s_o[ph * C4 + col];
+  }
   float M = am;
-  for (int ph = 0; ph < TPC; ++ph) M = fmaxf(M, s_m[ph * C4 + col]);
+#pragma unroll
+  for (int ph = 0; ph < TPC; ++ph) M = fmaxf(M, pm[ph]);
   const float Ms = (M == -INFINITY) ? 0.f : M;
   float lsum = 0.f;
   float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
   for (int ph = 0; ph < TPC; ++ph) {
-    const float w = __builtin_amdgcn_exp2f(s_m[ph * C4 + col] - Ms);
-    const float4 v = s_o[ph * C4 + col];
-    lsum += w * s_l[ph * C4 + col];
-    o4[0] += w * v.x;
-    o4[1] += w * v.y;
-    o4[2] += w * v.z;
-    o4[3] += w * v.w;
+    const float w = __builtin_amdgcn_exp2f(pm[ph] - Ms);
+    lsum += w * pl[ph];
+    o4[0] += w * po[ph].x;
+    o4[1] += w * po[ph].y;
+    o4[2] += w * po[ph].z;
+    o4[3] += w * po[ph].w;
   }
   const int d0 = col * 4;
   const int64_t obase = aidx * D + d0;
@@ -1480,9 +1492,16 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
     for (int e = 0; e < 4; ++e) P.o[obase + e] = o4[e];
   }
   if (P.out != nullptr) {
+    float ov[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      store_elem(P.out, ((int64_t)b * P.H + hq) * D + d0 + e, P.out_dtype, lsum > 0.f ? o4[e] / lsum : 0.f);
+    for (int e = 0; e < 4; ++e) ov[e] = lsum > 0.f ? o4[e] / lsum : 0.f;
+    const int64_t oi = ((int64_t)b * P.H + hq) * D + d0;
+    if (P.out_vec) {
+      store_elem4(P.out, oi, P.out_dtype, ov);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_elem(P.out, oi + e, P.out_dtype, ov[e]);
+    }
   }
   if (d0 == 0) {
     if (P.lse != nullptr) P.lse[(int64_t)b * P.H + hq] = lsum > 0.f ? (M + log2f(lsum)) * kLn2 : -INFINITY;
@@ -1672,6 +1691,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
   mp.acc_mode = acc_mode;
   mp.out = out;
   mp.out_dtype = out_dtype;
+  mp.out_vec = out != nullptr && reinterpret_cast<uintptr_t>(out) % (4 * elem_size(out_dtype)) == 0;
   mp.lse = lse;
   mp.ws_o = p.ws_o;
   mp.ws_ml = p.ws_ml;

@@ -200,6 +200,26 @@ def test_strided_views_need_no_copy(dev):
     assert torch.equal(out, out_b)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_misaligned_output_rows(dev, dtype):
+    """An output view that is not 8/16-byte aligned takes the per-element
+    store path and gives the same values as an aligned one."""
+    from halo_amd.decode import ChunkRef, build_plan, launch
+    x = decode_inputs(11, B=1, H=8, H_kv=2, T=512, D=64, dtype=dtype)
+    q, k, v = (_gpu(a, dtype, dev) for a in (x.q, x.k, x.v))
+    chunks = [ChunkRef(k[..., c:c + 256, :], v[..., c:c + 256, :], c, True) for c in range(0, 512, 256)]
+    plan = build_plan(B=1, H=8, H_kv=2, D=64, dtype=TDT[dtype], chunks=chunks, device=dev)
+    flat = torch.zeros(8 * 64 + 1, device=dev, dtype=TDT[dtype])
+    out_mis = flat[1:].view(1, 8, 64)
+    out = torch.empty(1, 8, 64, device=dev, dtype=TDT[dtype])
+    launch(plan, q[:, :, 0], scale=0.125, out=out)
+    launch(plan, q[:, :, 0], scale=0.125, out=out_mis)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_mis) and flat[0].item() == 0
+    ref, _ = A.attention_f64(x.q[:, :, 0], x.k, x.v, scale=0.125)
+    _check(out_mis, None, ref, None, dtype)
+
+
 def test_ragged_batch_rows(dev):
     """Per-row chunk tables (varlen): row b attends only its own chunks."""
     from halo_amd.decode import ChunkRef, build_plan, launch

@@ -1154,65 +1154,149 @@ decode_attn_kernel(DecodeParams P) {
 
 // ---------------------------------------------------------------------------
 // Decode attention over KIVI 2-bit blocks (halo_decode_attn_kivi).  Each wave
-// takes one 32-token block per tile: the raw block (K codes, K scale/zero,
-// V codes, V scale/zero; 3 KiB at D=128) arrives with three 16-byte loads
-// per lane into this wave's LDS slot, K is dequantised straight into MFMA A
-// operands (dtype(fp32(code*scale) + zero), the dequant arithmetic of
-// baselines/kivi_cache.py:72-78) and V into the P.V pieces, so the values the
-// scores and the output see are exactly the dequantised cache.
+// streams a contiguous run of blocks (one tile = TB blocks of 3 KiB at D=128,
+// two tiles of loads in flight) and stages each tile in its own LDS slot.
+// The dequantisation x = code * scale + zero (baselines/kivi_cache.py:72-78)
+// is folded into the two products instead of being applied per element:
+//   q.k_t   = sum_d code_td (q_d s_d)     + sum_d q_d z_d          (K per channel)
+//   (P V)_d = sum_t (p_t s_tg) code_td    + sum_t p_t z_tg         (V per token group g)
+// so each MFMA takes the raw codes (exact small integers in the K/V dtype)
+// against a scaled q or p, and the zero terms are one more MFMA each with
+// the zeros broadcast across the tile.  The products differ from attention
+// over the dequantised cache only by the rounding of q*s and p*s (fp16: one
+// fp16 rounding; bf16: a head + remainder pair, about 2^-17).
 // ---------------------------------------------------------------------------
+// 8 consecutive 2-bit codes (16 bits) -> 8 small integers in the K/V dtype
 template <int DT>
-__device__ __forceinline__ uint32_t pack2_dt(float a, float b) {
-  if constexpr (DT == HALO_BF16) return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
-  return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
-}
-// 8 consecutive 2-bit codes (16 bits) with their scales/zeros -> 8 elements
-template <int DT>
-__device__ __forceinline__ uint4 kivi_deq8(uint32_t c16, const float* s, const float* z) {
+__device__ __forceinline__ uint4 kivi_codes8(uint32_t c16) {
   uint32_t w[4];
+  if constexpr (DT == HALO_F16) {
+    // 1024 + c is 0x6400 | c in fp16; subtracting 1024 (packed) is exact
+    typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+    const h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const float x0 = opaque(opaque((float)((c16 >> (4 * p)) & 3u) * s[2 * p]) + z[2 * p]);
-    const float x1 = opaque(opaque((float)((c16 >> (4 * p + 2)) & 3u) * s[2 * p + 1]) + z[2 * p + 1]);
-    w[p] = pack2_dt<DT>(x0, x1);
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t v = 0x64006400u | ((c16 >> (4 * p)) & 3u) | (((c16 >> (4 * p + 2)) & 3u) << 16);
+      w[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v) - off);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const bf16x2_t v = {(__bf16)(float)((c16 >> (4 * p)) & 3u), (__bf16)(float)((c16 >> (4 * p + 2)) & 3u)};
+      w[p] = __builtin_bit_cast(uint32_t, v);
+    }
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
-// 8 codes sharing one scale/zero
+// bf16 products are split into a bf16 head and the bf16 rounding of the
+// remainder (the fp32 product of two bf16 values is exact), so the MFMA
+// pair sees the product to about 2^-17 instead of bf16's 2^-9
+__device__ __forceinline__ void mul8_bf16_split(const uint4& a, const uint4& b, uint4& hi, uint4& lo) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float p0 = bf16_lo(x[p]) * bf16_lo(y[p]), p1 = bf16_hi(x[p]) * bf16_hi(y[p]);
+    h[p] = pack2<HALO_BF16>(p0, p1);
+    l[p] = pack2<HALO_BF16>(p0 - bf16_lo(h[p]), p1 - bf16_hi(h[p]));
+  }
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+// elementwise product of two 8-element K/V-dtype pieces, rounded to the dtype
 template <int DT>
-__device__ __forceinline__ uint4 kivi_deq8_1(uint32_t c16, float s, float z) {
+__device__ __forceinline__ uint4 mul8(const uint4& a, const uint4& b) {
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w}, y[4] = {b.x, b.y, b.z, b.w};
   uint32_t w[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const float x0 = opaque(opaque((float)((c16 >> (4 * p)) & 3u) * s) + z);
-    const float x1 = opaque(opaque((float)((c16 >> (4 * p + 2)) & 3u) * s) + z);
-    w[p] = pack2_dt<DT>(x0, x1);
+    if constexpr (DT == HALO_F16) {
+      typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+      w[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, x[p]) * __builtin_bit_cast(h2, y[p]));
+    } else {
+      w[p] = pack2<DT>(bf16_lo(x[p]) * bf16_lo(y[p]), bf16_hi(x[p]) * bf16_hi(y[p]));
+    }
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
+
+// Epilogue for o held as MFMA accumulators (lane l: heads 4*(l/16)..+4 of
+// columns 16*db + l%16) by NS partial owners: owner j contributes o (has_o)
+// and/or its (m, l) per head (has_ml); the NS partials are merged through
+// LDS into the work item's partial.
+template <int D, int REP, int NS, int DB>
+__device__ __forceinline__ void write_partial_owners(const DecodeParams& P, int wslot, int owner, bool has_o,
+                                                     bool has_ml, const f32x4 (&acc)[DB], const float* m_run,
+                                                     const float* l_head, float* s_wo, float (*s_wm)[REP],
+                                                     float (*s_wl)[REP]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  if (has_o) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * (lane >> 4) + e;
+      if (h < REP) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) s_wo[(owner * REP + h) * D + db * 16 + (lane & 15)] = acc[db][e];
+      }
+    }
+  }
+  if (has_ml && lane == 0) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      s_wm[owner][r] = m_run[r];
+      s_wl[owner][r] = l_head[r];
+    }
+  }
+  __syncthreads();
+  float* wso = P.ws_o + (int64_t)wslot * REP * D;
+  for (int i = tid; i < REP * D; i += blockDim.x) {
+    const int r = i / D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc_o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) acc_o += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
+    wso[i] = acc_o;
+  }
+  if (tid < REP) {
+    const int r = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) M = fmaxf(M, s_wm[w][r]);
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float acc_l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) acc_l += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wl[w][r];
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 0] = M;
+    P.ws_ml[((int64_t)wslot * REP + r) * 2 + 1] = acc_l;
+  }
+}
+
 
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kivi_kernel(DecodeParams P) {
   using E = Elem<DT>;
-  constexpr int EP = 8;
-  constexpr int SL = D / EP;           // 16-byte pieces per dequantised row
-  constexpr int RPI = kWave / SL;      // rows per piece layer
-  constexpr int TILE = 32;             // one block per wave tile
-  constexpr int PPL = TILE / RPI;      // V pieces per lane per tile
-  constexpr int NB = TILE / 16;        // 16-row MFMA blocks per tile
-  constexpr int KS = D / 32;           // MFMA k-steps
-  constexpr int VPB = 16 / RPI;
-  constexpr int RB2 = D / 4;           // code bytes per token row (2 bits)
-  constexpr int CB = 32 * RB2;         // code bytes of K (or V) per block
-  constexpr int BB = 2 * CB + 8 * D;   // block bytes
-  constexpr int NG = D / 32;           // V groups per token
-  constexpr int RAW16 = BB / 16;
-  constexpr int LPR = (RAW16 + kWave - 1) / kWave;  // raw 16-byte loads per lane
-  static_assert(REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL && BB % 16 == 0, "kivi tile shape");
+  constexpr int RB2 = D / 4;                   // K code bytes per token row (2 bits)
+  constexpr int CB = 32 * RB2;                 // code bytes of K (or V) per block
+  constexpr int BB = 2 * CB + 8 * D;           // block bytes
+  constexpr int NG = D / 32;                   // V groups per token
+  constexpr int KS = D / 32;                   // q.k k-steps
+  constexpr int DB = D / 16;                   // P.V column blocks
+  constexpr int TB = D > 128 ? 2 : 4;         // blocks per wave tile (12 KiB at D = 128, 256)
+  constexpr int TBYTES = TB * BB;
+  constexpr int LPT = TBYTES / (16 * kWave);   // 16-byte loads per lane per tile
+  static_assert(TBYTES % (16 * kWave) == 0 && REP <= 16, "kivi tile shape");
+  // K side of a block at offset 0: codes [0, CB), scale [CB, CB+2D), zero [CB+2D, CB+4D)
+  // V side: codes (channel-major, 8 bytes per channel) at CB+4D, scale/zero (group-major)
+  constexpr int VC = CB + 4 * D, VS = 2 * CB + 4 * D, VZ = 2 * CB + 6 * D;
 
-  __shared__ __attribute__((aligned(16))) char s_raw[NW][BB];
-  __shared__ float s_pall[NW][TILE * REP];
+  __shared__ __attribute__((aligned(16))) char s_raw[NW][TBYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][REP * 32];  // p of one block, [head][token]
+  __shared__ float s_al[NW][REP];
   __shared__ float s_wo[NW * REP * D];
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
 
@@ -1247,27 +1331,18 @@ decode_attn_kivi_kernel(DecodeParams P) {
   const char* base = reinterpret_cast<const char*>(dsc.k) +
                      (dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h;
 
-  const int nrows_total = max(t1 - t0, 0);
-  const int ntiles_total = (nrows_total + TILE - 1) / TILE;
-  const int tiles_per_wave = (ntiles_total + NW - 1) / NW;
-  const int ws = t0 + wave * tiles_per_wave * TILE;
-  const int we = min(t1, ws + tiles_per_wave * TILE);
+  // this wave's run of tiles (token offsets relative to the chunk)
+  const int nblk = (max(t1 - t0, 0) + 31) / 32;
+  const int ntiles = (nblk + TB - 1) / TB;
+  const int tpw = (ntiles + NW - 1) / NW;
+  const int wt0 = wave * tpw;
+  const int wt1 = min(ntiles, wt0 + tpw);
+  const int64_t wbyte0 = (int64_t)(t0 / 32 + wt0 * TB) * BB;               // first byte of the run
+  const int64_t wbytes = (int64_t)max(min(nblk, wt1 * TB) - wt0 * TB, 0) * BB;  // bytes of the run
 
-  float m_run[REP], acc_o[REP][EP], l_head[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    m_run[r] = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < EP; ++e) acc_o[r][e] = 0.f;
-  }
-  char* raw = s_raw[wave];
-  float* pl = s_pall[wave];
-  const int my_col = lane % SL;
-  const int my_row0 = lane / SL;
-  const int hl = lane & 15;
-  const int kg = lane >> 4;
-
-  uint4 qb[KS];
+  const int hl = lane & 15;   // score layout: head / A-operand head
+  const int kg = lane >> 4;   // score layout: row quad / lane group (8-element slab)
+  uint4 qb[KS];               // B operand of q.k: q of head hl, channels 32s + 8kg ..
   {
     const bool live = hl < nvalid_h;
     const char* qrow = reinterpret_cast<const char*>(P.q) +
@@ -1289,86 +1364,118 @@ decode_attn_kivi_kernel(DecodeParams P) {
       qb[s] = v;
     }
   }
-  float m_lane = -INFINITY, l_lane = 0.f;
-  for (int tb = ws; tb < we; tb += TILE) {
-    const int nrows = min(TILE, we - tb);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + (int64_t)(tb / 32) * BB, BB);
+  f32x4 acc[DB];
 #pragma unroll
-    for (int k = 0; k < LPR; ++k) {
-      const int idx = lane + k * kWave;
-      if (idx < RAW16) reinterpret_cast<uint4*>(raw)[idx] = buf_ld16(rr, idx * 16);
+  for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
+  float l_lane = 0.f;        // this lane's share of head hl's denominator
+  char* raw = s_raw[wave];
+  uint16_t* pw = s_p[wave];
+  float* alw = s_al[wave];
+
+  for (int it = wt0; it < wt1; it += 2) {
+    uint4 buf[2][LPT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t off = (int64_t)(it + u - wt0) * TBYTES;
+      const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + wbyte0 + off, wbytes - off);
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) buf[u][i] = buf_ld16(rr, (i * kWave + lane) * 16);
     }
-    wave_lds_fence();
-    const uint16_t* meta_v = reinterpret_cast<const uint16_t*>(raw + 2 * CB + 4 * D);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 2; ++u) {
+      if (it + u >= wt1) break;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slice
-        const uint32_t c16 = *reinterpret_cast<const uint16_t*>(raw + (nb * 16 + hl) * RB2 + c0 / 4);
-        float sk[8], zk[8];
-        E::unpack(*reinterpret_cast<const uint4*>(raw + CB + 2 * c0), sk);
-        E::unpack(*reinterpret_cast<const uint4*>(raw + CB + 2 * D + 2 * c0), zk);
-        sc = MfmaOp<DT>::run(kivi_deq8<DT>(c16, sk, zk), qb[s], sc);
-      }
-      float sv[4], bm = -INFINITY;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bool valid = nb * 16 + kg * 4 + c < nrows;
-        sv[c] = valid ? sc[c] * P.scale2 : -INFINITY;
-        bm = fmaxf(bm, sv[c]);
-      }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-      const float m_new = fmaxf(m_lane, bm);
-      const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
-      m_lane = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float p = __builtin_amdgcn_exp2f(sv[c] - ms);
-        psum += p;
-        if (hl < REP) pl[(nb * 16 + kg * 4 + c) * REP + hl] = p;
-      }
-      l_lane = l_lane * alpha + psum;
-      float al[REP];
-      bool rescale = false;
-#pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        al[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
-        rescale |= al[r] != 1.f;
-      }
-      if (rescale) {
-#pragma unroll
-        for (int r = 0; r < REP; ++r)
-#pragma unroll
-          for (int e = 0; e < EP; ++e) acc_o[r][e] *= al[r];
-      }
+      for (int i = 0; i < LPT; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[u][i];
       wave_lds_fence();
+      const int tok0 = t0 + (it + u) * TB * 32;  // first token of the tile
+      for (int blk = 0; blk < TB; ++blk) {
+        const int nrows = min(32, t1 - (tok0 + blk * 32));  // <= 0: block past the range
+        if (nrows <= 0) break;
+        const char* bk = raw + blk * BB;
+        // ---- scores: 2 row blocks of 16 tokens, code MFMAs + one zero-term MFMA per k-step
+        f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 sz = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < VPB; j += 2) {
-        const int i = nb * VPB + j;
-        const int ra = i * RPI + my_row0, rbw = (i + 1) * RPI + my_row0;
-        const int grp = my_col * EP / 32;
-        const uint32_t ca = *reinterpret_cast<const uint16_t*>(raw + CB + 4 * D + ra * RB2 + my_col * 2);
-        const uint32_t cb = *reinterpret_cast<const uint16_t*>(raw + CB + 4 * D + rbw * RB2 + my_col * 2);
-        const uint4 va = kivi_deq8_1<DT>(ca, from_bits16<DT>(meta_v[ra * NG + grp]),
-                                         from_bits16<DT>(meta_v[32 * NG + ra * NG + grp]));
-        const uint4 vb = kivi_deq8_1<DT>(cb, from_bits16<DT>(meta_v[rbw * NG + grp]),
-                                         from_bits16<DT>(meta_v[32 * NG + rbw * NG + grp]));
-        float pa[REP], pb[REP];
+        for (int s = 0; s < KS; ++s) {
+          const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slab
+          const uint4 sk = *reinterpret_cast<const uint4*>(bk + CB + 2 * c0);
+          const uint4 zk = *reinterpret_cast<const uint4*>(bk + CB + 2 * D + 2 * c0);
+          uint4 qs, qs_lo;
+          if constexpr (DT == HALO_BF16) mul8_bf16_split(qb[s], sk, qs, qs_lo);
+          else qs = mul8<DT>(qb[s], sk);
 #pragma unroll
-        for (int r = 0; r < REP; ++r) {
-          pa[r] = pl[ra * REP + r];
-          pb[r] = pl[rbw * REP + r];
+          for (int nb = 0; nb < 2; ++nb) {
+            const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
+            const uint4 cd = kivi_codes8<DT>(c16);
+            sc[nb] = MfmaOp<DT>::run(cd, qs, sc[nb]);
+            if constexpr (DT == HALO_BF16) sc[nb] = MfmaOp<DT>::run(cd, qs_lo, sc[nb]);
+          }
+          sz = MfmaOp<DT>::run(zk, qb[s], sz);
         }
-        pv_pair<DT, REP, EP>(va, vb, pa, pb, acc_o);
+        // ---- online softmax (lane: head hl, tokens 16nb + 4kg + c)
+        float sv[2][4], bm = -INFINITY;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const bool valid = nb * 16 + kg * 4 + c < nrows;
+            sv[nb][c] = valid ? (sc[nb][c] + sz[c]) * P.scale2 : -INFINITY;
+            bm = fmaxf(bm, sv[nb][c]);
+          }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        const float m_new = fmaxf(m_lane, bm);
+        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+        m_lane = m_new;
+        float psum = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          float p4[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            p4[c] = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
+            psum += p4[c];
+          }
+          if (hl < REP)
+            *reinterpret_cast<uint2*>(pw + hl * 32 + nb * 16 + kg * 4) =
+                make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
+        }
+        l_lane = l_lane * alpha + psum;
+        if (lane < REP) alw[lane] = alpha;
+        wave_lds_fence();
+        // ---- P.V: per group, codes against p*s and the zeros against p
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = alw[min(4 * kg + e, REP - 1)];
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[db][e] *= a;
+        }
+        const uint4 pa = hl < REP ? *reinterpret_cast<const uint4*>(pw + hl * 32 + kg * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int gg = 0; gg < NG; ++gg) {
+          const uint4 sv8 = *reinterpret_cast<const uint4*>(bk + VS + 2 * (gg * 32 + kg * 8));
+          const uint4 zv8 = *reinterpret_cast<const uint4*>(bk + VZ + 2 * (gg * 32 + kg * 8));
+          uint4 ps, ps_lo;
+          if constexpr (DT == HALO_BF16) mul8_bf16_split(pa, sv8, ps, ps_lo);
+          else ps = mul8<DT>(pa, sv8);
+#pragma unroll
+          for (int d2 = 0; d2 < 2; ++d2) {
+            const int db = 2 * gg + d2;
+            const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
+            const uint4 cd = kivi_codes8<DT>(c16);
+            acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
+            if constexpr (DT == HALO_BF16) acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
+            acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
+          }
+        }
+        wave_lds_fence();  // the next block rewrites p and the rescale factors
       }
+      wave_lds_fence();  // the next tile rewrites raw
     }
-    wave_lds_fence();  // the next tile rewrites raw and pl
   }
+  float m_run[REP], l_head[REP];
   float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
   lsum += __shfl_xor(lsum, 32, kWave);
 #pragma unroll
@@ -1376,7 +1483,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
     m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
     l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
   }
-  write_partial<D, REP, NW, SL, EP>(P, wslot, acc_o, m_run, l_head, s_wo, s_wm, s_wl);
+  write_partial_owners<D, REP, NW, DB>(P, wslot, wave, true, true, acc, m_run, l_head, s_wo, s_wm, s_wl);
 }
 
 // ---------------------------------------------------------------------------

@@ -18,10 +18,14 @@
 //                     channel d at bit (d*bits) % 8 of byte d*bits/8
 //   [C, C+2D)         K scale, D elements of the dtype (per channel)
 //   [C+2D, C+4D)      K zero
-//   [C+4D, 2C+4D)     V codes, same packing
-//   [2C+4D, 2C+6D)    V scale, 32 tokens x D/32 groups (token-major)
+//   [C+4D, 2C+4D)     V codes, channel-major rows of 32*bits/8 bytes, code
+//                     of token t at bit (t*bits) % 8 of byte t*bits/8
+//   [2C+4D, 2C+6D)    V scale, D/32 groups x 32 tokens (group-major)
 //   [2C+6D, 2C+8D)    V zero
-// with C = 32*D*bits/8.  D=128, bits=2: 3072 bytes per block.
+// with C = 32*D*bits/8.  D=128, bits=2: 3072 bytes per block.  The V side
+// is transposed so that 8 consecutive tokens of one channel (the P.V
+// operand of one lane) are 16 contiguous bits, and 8 consecutive tokens'
+// scales (or zeros) of one group are 16 contiguous bytes.
 
 #include "common.hpp"
 
@@ -126,18 +130,20 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
     }
     float sc, z;
     kivi_params<DT, BITS>(mn, mx, sc, z);
-    s_vs[i] = bits_dt<DT>(sc);
-    s_vz[i] = bits_dt<DT>(z);
+    s_vs[g * G + t] = bits_dt<DT>(sc);
+    s_vz[g * G + t] = bits_dt<DT>(z);
     for (int c = 0; c < G; ++c) s_cv[t * D + g * G + c] = (uint8_t)kivi_code<DT, BITS>(s_v[t][g * G + c], sc, z);
   }
   __syncthreads();
   uint8_t* out = P.blocks + (int64_t)b * P.bsb + (int64_t)h * P.bsh + (int64_t)j * kivi_block_bytes(D, BITS);
+  constexpr int VRB = G * BITS / 8;  // V code bytes per channel row
   for (int q = tid; q < C; q += 256) {
     uint32_t wk = 0, wv = 0;
+    const int d = q / VRB, t0 = (q % VRB) * CPB;
 #pragma unroll
     for (int c = 0; c < CPB; ++c) {
       wk |= (uint32_t)s_ck[q * CPB + c] << (c * BITS);
-      wv |= (uint32_t)s_cv[q * CPB + c] << (c * BITS);
+      wv |= (uint32_t)s_cv[(t0 + c) * D + d] << (c * BITS);
     }
     out[q] = (uint8_t)wk;
     out[C + 4 * D + q] = (uint8_t)wv;
@@ -184,9 +190,10 @@ __global__ void __launch_bounds__(256) kivi_dequant_kernel(KiviDequantParams P) 
     const int t = e / D, d = e % D;
     const int bit = d * BITS;
     const uint32_t ck = (blk[t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
-    const uint32_t cv = (blk[C + 4 * D + t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
+    const int tbit = t * BITS;
+    const uint32_t cv = (blk[C + 4 * D + d * (G * BITS / 8) + tbit / 8] >> (tbit % 8)) & MASK;
     const float sk = from_bits<DT>(meta_k[d]), zk = from_bits<DT>(meta_k[D + d]);
-    const float sv = from_bits<DT>(meta_v[t * NG + d / G]), zv = from_bits<DT>(meta_v[G * NG + t * NG + d / G]);
+    const float sv = from_bits<DT>(meta_v[(d / G) * G + t]), zv = from_bits<DT>(meta_v[G * NG + (d / G) * G + t]);
     // both fp32 results are materialised so the conversion rounds the fp32
     // sum (no mixed-precision fused add-and-convert)
     ko[(int64_t)t * P.kst + d] = bits_dt<DT>(opaque(opaque((float)ck * sk) + zk));

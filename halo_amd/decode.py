@@ -127,9 +127,16 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
     return t
 
 
-def choose_split(total_rows: int, n_cu: int) -> int:
+def choose_split(total_rows: int, n_cu: int, *, kivi: bool = False) -> int:
     """Rows per work item: aim for about 4 workgroups per CU, in whole
-    4-wave x 64-row tiles, between 256 and 4096 rows."""
+    4-wave x 64-row tiles, between 256 and 4096 rows.  KIVI items: about 2
+    per CU (the LDS-staged tiles allow 2 resident workgroups per CU), in
+    whole 4-wave x 128-token tiles."""
+    if kivi:
+        unit = _WAVES_PER_GROUP * 128
+        target = max(1, total_rows // max(1, 2 * n_cu))
+        split = unit * max(1, math.ceil(target / unit))
+        return int(min(max(split, unit), 16 * unit))
     unit = _WAVES_PER_GROUP * _TILE_ROWS
     target = max(1, total_rows // max(1, 4 * n_cu))
     split = unit * max(1, math.ceil(target / unit))
@@ -278,7 +285,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                     rows = min(rows, int(q_pos_host[b]) - c.chunk_start + 1)
                 total_rows += rows * H_kv * n_sub
     if split is None:
-        split = choose_split(total_rows, _num_cus(device))
+        split = choose_split(total_rows, _num_cus(device), kivi=kivi)
 
     work = []
     offsets = [0]

@@ -101,9 +101,10 @@ def dequant_k(codes, scale, zero, *, group_size: int, dtype: str) -> np.ndarray:
 # ---------------------------------------------------------------------------
 # Packed block layout of this build (the reference stores unpacked int8 codes,
 # kivi_cache.py:50-53).  One block = 32 tokens of one (b, h_kv):
-#   K codes (32 x D*bits/8), K scale (D), K zero (D), V codes (32 x D*bits/8),
-#   V scale (32 x D/32), V zero (32 x D/32); scales/zeros in the storage dtype;
-#   code of channel d at bit (d*bits) % 8 of byte d*bits/8 of its token row.
+#   K codes (32 token rows x D*bits/8), K scale (D), K zero (D),
+#   V codes (D channel rows x 32*bits/8), V scale (D/32 groups x 32 tokens),
+#   V zero (D/32 x 32); scales/zeros in the storage dtype; within a row,
+#   element e of the row sits at bit (e*bits) % 8 of byte e*bits/8.
 # ---------------------------------------------------------------------------
 GROUP = 32
 
@@ -154,13 +155,16 @@ def pack_blocks(k: np.ndarray, v: np.ndarray, *, bits: int, dtype: str) -> np.nd
     cv, sv, zv = quantize_v_per_token(v, bits=bits, group_size=GROUP, dtype=dtype)     # sv (B,H,T,D/32)
     ck = ck.reshape(B, H, nb, GROUP, D)
     cv = cv.reshape(B, H, nb, GROUP, D)
+    NG = D // GROUP
+    sv = np.swapaxes(sv.reshape(B, H, nb, GROUP, NG), -1, -2)   # (.., NG, 32 tokens)
+    zv = np.swapaxes(zv.reshape(B, H, nb, GROUP, NG), -1, -2)
     parts = [
         _pack_codes(ck, bits).reshape(B, H, nb, -1),
         _dtype_bits(sk, dtype).view(np.uint8).reshape(B, H, nb, -1),
         _dtype_bits(zk, dtype).view(np.uint8).reshape(B, H, nb, -1),
-        _pack_codes(cv, bits).reshape(B, H, nb, -1),
-        _dtype_bits(sv.reshape(B, H, nb, GROUP * D // GROUP), dtype).view(np.uint8).reshape(B, H, nb, -1),
-        _dtype_bits(zv.reshape(B, H, nb, GROUP * D // GROUP), dtype).view(np.uint8).reshape(B, H, nb, -1),
+        _pack_codes(np.ascontiguousarray(np.swapaxes(cv, -1, -2)), bits).reshape(B, H, nb, -1),
+        _dtype_bits(np.ascontiguousarray(sv), dtype).view(np.uint8).reshape(B, H, nb, -1),
+        _dtype_bits(np.ascontiguousarray(zv), dtype).view(np.uint8).reshape(B, H, nb, -1),
     ]
     out = np.concatenate(parts, axis=-1)
     assert out.shape[-1] == block_bytes(D, bits)
@@ -177,9 +181,11 @@ def unpack_blocks(blocks: np.ndarray, *, D: int, bits: int, dtype: str):
     ck = _unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, GROUP, D * bits // 8), bits); o += C
     sk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
     zk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
-    cv = _unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, GROUP, D * bits // 8), bits); o += C
-    sv = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype).reshape(B, H, nb, GROUP, D // GROUP); o += 2 * D
-    zv = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype).reshape(B, H, nb, GROUP, D // GROUP)
+    cv = np.swapaxes(_unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, D, GROUP * bits // 8), bits), -1, -2); o += C
+    sv = np.swapaxes(_bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype)
+                     .reshape(B, H, nb, D // GROUP, GROUP), -1, -2); o += 2 * D
+    zv = np.swapaxes(_bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype)
+                     .reshape(B, H, nb, D // GROUP, GROUP), -1, -2)
     k = dequantize(ck, sk[:, :, :, None, :], zk[:, :, :, None, :], dtype=dtype)
     v = dequantize(cv, np.repeat(sv, GROUP, axis=-1), np.repeat(zv, GROUP, axis=-1), dtype=dtype)
     return k.reshape(B, H, nb * GROUP, D), v.reshape(B, H, nb * GROUP, D)

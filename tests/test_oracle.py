@@ -317,14 +317,16 @@ def test_kivi_per_channel_k_groups_tokens():
 
 def test_kivi_block_layout_known_answer():
     """Block layout pinned by hand-built values: channel 0 of K ramps 0,1,2,3
-    over the tokens (scale 1, zero 0, codes t % 4 in bits 0-1 of each row's
-    first byte); V token 0 channels 0..31 ramp likewise per token group."""
+    over the tokens (scale 1, zero 0, codes t % 4 in bits 0-1 of each token
+    row's first byte); every V token ramps 0..3 over channels 0..31 (group 0:
+    scale 1, zero 0, channel c coded c % 4 for all 32 tokens in its
+    channel-major row), group 1 is all zero (scale at the fp16 floor 0)."""
     from oracle import kivi as K
     D = 64
     k = np.zeros((1, 1, 32, D), np.float32)
     v = np.zeros((1, 1, 32, D), np.float32)
     k[0, 0, :, 0] = np.arange(32) % 4
-    v[0, 0, 0, :32] = np.arange(32) % 4
+    v[0, 0, :, :32] = np.arange(32) % 4
     blk = K.pack_blocks(k, v, bits=2, dtype="float16")
     assert blk.shape == (1, 1, 1, K.block_bytes(D, 2)) == (1, 1, 1, 2 * 32 * 16 + 8 * D)
     b = blk[0, 0, 0]
@@ -334,11 +336,12 @@ def test_kivi_block_layout_known_answer():
     ks = b[C:C + 2 * D].view(np.float16)
     assert ks[0] == np.float16(1.0) and ks[1] == np.float16(0.0)   # range 0 -> fp16 floor 0
     vc = C + 4 * D
-    first = b[vc:vc + 8]                                            # token 0, channels 0..31
-    codes = [(int(first[i // 4]) >> (2 * (i % 4))) & 3 for i in range(32)]
-    assert codes == [i % 4 for i in range(32)]
-    vs = b[2 * C + 4 * D:2 * C + 6 * D].view(np.float16)
-    assert vs[0] == np.float16(1.0)
+    vrow = 32 * 2 // 8                                              # 8 bytes per channel row
+    for c in range(D):
+        want = (c % 4) * 0x55 if c < 32 else 0                      # code c % 4 for all 32 tokens
+        assert [int(x) for x in b[vc + c * vrow:vc + (c + 1) * vrow]] == [want] * vrow
+    vs = b[2 * C + 4 * D:2 * C + 6 * D].view(np.float16)            # group-major: D/32 x 32 tokens
+    assert (vs[:32] == np.float16(1.0)).all() and (vs[32:] == np.float16(0.0)).all()
 
 
 def test_kivi_blocks_roundtrip_equals_dequant():

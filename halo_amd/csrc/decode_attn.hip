@@ -709,6 +709,249 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// LDS bytes of the plain-row MFMA path (bf16/f16 K/V): per pair 2 p tiles
+// (K/V dtype, [head][row]) and 2 rescale vectors, the pair partials, then one
+// V tile per V-wave and one K tile per K-wave.
+template <int D, int REP, int NW>
+struct PlainMfmaLds {
+  static constexpr int RB = D * 2;
+  static constexpr int SL = RB / 16;
+  static constexpr int TILE = SL <= 16 ? kWave : kWave * 16 / SL;
+  static constexpr int NP = NW / 2;
+  static constexpr int SZ_P = NP * 2 * REP * TILE * 2;
+  static constexpr int SZ_AL = (NP * 2 * REP * 4 + 15) / 16 * 16;
+  static constexpr int SZ_WO = NP * REP * D * 4;
+  static constexpr int SZ_VT = NP * TILE * RB;
+  static constexpr int bytes = SZ_P + SZ_AL + SZ_WO + 2 * SZ_VT;
+};
+
+// One work item's rows [t0, t1) of a plain bf16/f16 K/V chunk on the matrix
+// cores; writes the item's partial at workspace slot wslot.
+template <int DT, int D, int REP, int NW>
+__device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, char* smem, float (*s_wm)[REP],
+                                                float (*s_wl)[REP], const char* kbase, const char* vbase,
+                                                int64_t kst, int64_t vst, int t0, int t1, int b, int hq0,
+                                                int nvalid_h, int wslot) {
+  using E = Elem<DT>;
+  using L = PlainMfmaLds<D, REP, NW>;
+  constexpr int EP = E::per16;          // elements per 16-byte piece
+  constexpr int SL = D / EP;            // pieces per row
+  constexpr int RPI = kWave / SL;       // rows covered by one load instruction
+  constexpr int RB = D * E::size;       // bytes per row
+  constexpr int TILE = L::TILE;         // rows per wave tile
+  constexpr int PPL = TILE / RPI;       // 16-byte pieces per lane per tile (K and V each)
+  constexpr int NB = TILE / 16;         // 16-row MFMA blocks
+  constexpr int KS = D / 32;            // q.k k-steps
+  constexpr int VPB = 16 / RPI;
+  constexpr int NP = L::NP;             // producer/consumer wave pairs
+  constexpr int DB = D / 16;            // 16-column blocks of the P.V product
+  constexpr int KS2 = TILE / 32;        // 32-row k-steps of the P.V product
+  static_assert(SL * RPI == kWave && PPL * RPI == TILE && REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL,
+                "mfma tile shape");
+  float* s_pall = reinterpret_cast<float*>(smem);
+  float* s_alpha = reinterpret_cast<float*>(smem + L::SZ_P);
+  float* s_wo = reinterpret_cast<float*>(smem + L::SZ_P + L::SZ_AL);
+  char* s_vt = smem + L::SZ_P + L::SZ_AL + L::SZ_WO;
+  char* s_kt = s_vt + L::SZ_VT;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int nrows_total = max(t1 - t0, 0);
+  const int ntiles_total = (nrows_total + TILE - 1) / TILE;
+  float m_run[REP], l_head[REP];
+  f32x4 acc_pv[DB];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) m_run[r] = -INFINITY;
+  const int my_col = lane % SL;
+  const int my_row0 = lane / SL;
+  const int voff0 = my_col * 16;
+
+  // ---- Producer/consumer wave pairs: every wave streams ONE contiguous
+  // row range of ONE tensor (on gfx950 a wave that streams two distant
+  // regions at once pulls markedly less bandwidth than one that streams a
+  // single region), 1 KiB of consecutive rows per load instruction (whole
+  // 128-byte lines; the MFMA operand layout read straight from memory
+  // would split every line over two instructions).  Each tile is staged
+  // in the wave's own LDS slot and read back in operand layout.  Waves
+  // [0, NP) read K and compute the scores on v_mfma_f32_16x16x32 (A = 16 K
+  // rows x 32 elements: lane l holds row l%16, elements 8*(l/16)..+8 of
+  // the k-step; B = q^T: lane l holds head l%16; D: lane l holds head
+  // l%16, rows 4*(l/16)..+4) and the online softmax; waves [NP, NW) read V
+  // and accumulate P.V with the tile's probabilities and rescale factors
+  // their partner leaves in LDS (double-buffered by tile parity, one
+  // workgroup barrier per tile).  Each wave keeps two tiles of loads in
+  // flight (one at D = 256).
+  constexpr int NBUF = NB * KS;
+  static_assert(NBUF == PPL, "K and V tiles use the same register budget");
+  constexpr int TIF = D > 128 ? 1 : 2;  // tiles in flight per wave (register budget)
+  const bool kwave = wave < NP;
+  const int pair = kwave ? wave : wave - NP;
+  const int tpp = (ntiles_total + NP - 1) / NP;   // tiles per pair, uniform in the workgroup
+  const int ps = t0 + pair * tpp * TILE;
+  const int pe = min(t1, ps + tpp * TILE);
+  uint16_t* pbuf = reinterpret_cast<uint16_t*>(s_pall) + pair * 2 * REP * TILE;
+  float* abuf = s_alpha + pair * 2 * REP;
+  const int hl = lane & 15;   // score layout: head
+  const int kg = lane >> 4;   // score layout: k-group / row quad
+  uint4 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qb[s] = make_uint4(0, 0, 0, 0);
+  if (kwave && hl < nvalid_h) {
+    const char* qrow = reinterpret_cast<const char*>(P.q) +
+                       ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + hl) * P.q_stride_h) * E::size;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (P.q_aligned) {
+        qb[s] = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
+      } else {
+        const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
+        qb[s] = make_uint4(qh[0] | ((uint32_t)qh[1] << 16), qh[2] | ((uint32_t)qh[3] << 16),
+                           qh[4] | ((uint32_t)qh[5] << 16), qh[6] | ((uint32_t)qh[7] << 16));
+      }
+    }
+  }
+  // The two roles run separate loops with the same number of workgroup
+  // barriers (tpp), so each role's registers are live only in its own loop.
+  if (kwave) {
+    float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
+    float l_lane = 0.f;        // this lane's share of head hl's denominator
+    char* kt = s_kt + pair * TILE * RB;
+    for (int it = 0; it < tpp; it += TIF) {
+      uint4 buf[TIF][NBUF];
+#pragma unroll
+      for (int u = 0; u < TIF; ++u) {
+        const int tb = ps + (it + u) * TILE;
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(pe - tb) * kst);
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * kst) + voff0);
+      }
+#pragma unroll
+      for (int u = 0; u < TIF; ++u) {
+        if (it + u >= tpp) break;
+        const int tb = ps + (it + u) * TILE;
+        const int nrows = min(TILE, pe - tb);  // <= 0: every row masked
+        uint16_t* pt = pbuf + ((it + u) & 1) * REP * TILE;
+        float* at = abuf + ((it + u) & 1) * REP;
+        // stage the tile (rows past the slice arrived as zeros), read it
+        // back as MFMA A operands (this wave's own slot: no barrier)
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+          const int r = i * RPI + my_row0;
+          *reinterpret_cast<uint4*>(kt + r * RB + ((my_col ^ kswz<SL>(r)) << 4)) = buf[u][i];
+        }
+        f32x4 sc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          sc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          const int r = nb * 16 + hl;
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            const uint4 a = *reinterpret_cast<const uint4*>(kt + r * RB + (((s * 4 + kg) ^ kswz<SL>(r)) << 4));
+            sc[nb] = MfmaOp<DT>::run(a, qb[s], sc[nb]);
+          }
+        }
+        float sv[NB][4], bm = -INFINITY;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const bool valid = nb * 16 + kg * 4 + c < nrows;
+            sv[nb][c] = valid ? sc[nb][c] * P.scale2 : -INFINITY;
+            bm = fmaxf(bm, sv[nb][c]);
+          }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        const float m_new = fmaxf(m_lane, bm);
+        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+        m_lane = m_new;
+        float psum = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          float p4[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            p4[c] = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
+            psum += p4[c];
+          }
+          // rows nb*16 + 4kg .. +3 of head hl: one 8-byte store
+          if (hl < REP)
+            *reinterpret_cast<uint2*>(pt + hl * TILE + nb * 16 + kg * 4) =
+                make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
+        }
+        l_lane = l_lane * alpha + psum;
+        if (lane < REP) at[lane] = alpha;
+        __syncthreads();  // hand the tile's p and rescale factors to the V-wave
+      }
+    }
+    float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
+      l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
+    }
+  } else {
+    // P.V on v_mfma_f32_16x16x32: A = P^T (lane l: head l%16, rows
+    // 8*(l/16)..+8 of the 32-row k-step, read from the K-wave's [head][row]
+    // tile), B = V (lane l: column l%16 of the 16-column block, the same 8
+    // rows, gathered from the LDS copy of the tile with two transposed
+    // reads), D: lane l holds heads 4*(l/16)..+4 of column l%16.
+    char* vt = s_vt + pair * TILE * RB;
+    const int hA = lane & 15;           // A operand head
+    const int gq = lane >> 4;           // lane group: 8-row slab of the k-step
+    const int prow = (lane & 15) >> 2;  // transposed read: row within the 4-row block
+    const int pcol = lane & 3;          // transposed read: 4-column group
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_pv[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < tpp; it += TIF) {
+      uint4 buf[TIF][NBUF];
+#pragma unroll
+      for (int u = 0; u < TIF; ++u) {
+        const int tb = ps + (it + u) * TILE;
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(pe - tb) * vst);
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * vst) + voff0);
+      }
+#pragma unroll
+      for (int u = 0; u < TIF; ++u) {
+        if (it + u >= tpp) break;
+        // stage the tile (rows past the slice arrived as zeros)
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+          const int r = i * RPI + my_row0;
+          *reinterpret_cast<uint4*>(vt + r * RB + ((my_col ^ vswz<SL>(r)) << 4)) = buf[u][i];
+        }
+        const uint16_t* pt = reinterpret_cast<const uint16_t*>(s_pall) + pair * 2 * REP * TILE +
+                             ((it + u) & 1) * REP * TILE;
+        const float* at = abuf + ((it + u) & 1) * REP;
+        __syncthreads();  // the K-wave's p and rescale factors for this tile are in LDS
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = at[min(4 * gq + e, REP - 1)];
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc_pv[db][e] *= a;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < KS2; ++s2) {
+          const uint4 pa = hA < REP ? *reinterpret_cast<const uint4*>(pt + hA * TILE + s2 * 32 + gq * 8)
+                                    : make_uint4(0, 0, 0, 0);
+          const int r0 = s2 * 32 + gq * 8 + prow;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const int pc = 2 * db + (pcol >> 1);
+            const int bo = (pcol & 1) * 8;
+            const uint2 lo = lds_read_tr16(vt + r0 * RB + ((pc ^ vswz<SL>(r0)) << 4) + bo);
+            const uint2 hi = lds_read_tr16(vt + (r0 + 4) * RB + ((pc ^ vswz<SL>(r0 + 4)) << 4) + bo);
+            acc_pv[db] = MfmaOp<DT>::run(pa, make_uint4(lo.x, lo.y, hi.x, hi.y), acc_pv[db]);
+          }
+        }
+      }
+    }
+  }
+  write_partial_pairs_mfma<D, REP, NP, DB>(P, wslot, kwave, pair, acc_pv, m_run, l_head, s_wo, s_wm, s_wl);
+}
+
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kernel(DecodeParams P) {
@@ -726,35 +969,20 @@ decode_attn_kernel(DecodeParams P) {
   constexpr int RPL = TILE / LPH;       // rows per lane in the VALU q.k phase
   static_assert(SL * RPI == kWave && PPL * RPI == TILE && PPL % 2 == 0, "tile shape");
   static_assert(LPH == 8 || LPH == 16 || LPH == 32 || LPH == 64, "lane groups");
-  // MFMA path: 16-row blocks, k-steps of 32 elements, V pieces per block
-  constexpr int NB = TILE / 16;
-  constexpr int KS = D / 32;
-  constexpr int VPB = 16 / RPI;
-  static_assert(!kMfma || (REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL), "mfma tile shape");
-
-  constexpr int NP = NW / 2;  // MFMA path: producer/consumer wave pairs
-  constexpr int DB = D / 16;  // MFMA path: 16-column blocks of the P.V product
-  constexpr int KS2 = TILE / 32;  // MFMA path: 32-row k-steps of the P.V product
   // VALU path: per-wave q copy, K tiles, p tiles; the epilogue reuses the front.
   // MFMA path: per pair 2 p tiles (K/V dtype, [head][row]) and 2 rescale
   // vectors, the pair partials, then one V tile per V-wave.
   constexpr int SZ_Q = kMfma ? 0 : NW * REP * RB;
   constexpr int SZ_K = kMfma ? 0 : NW * TILE * KROW;
-  constexpr int SZ_P = kMfma ? NP * 2 * REP * TILE * 2 : NW * TILE * REP * 4;
-  constexpr int SZ_AL = kMfma ? (NP * 2 * REP * 4 + 15) / 16 * 16 : 0;
-  constexpr int SZ_WO = kMfma ? NP * REP * D * 4 : 0;
-  constexpr int SZ_VT = kMfma ? NP * TILE * RB : 0;  // one V tile per V-wave, one K tile per K-wave
-  constexpr int SZ_A0 = SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO + 2 * SZ_VT;
+  constexpr int SZ_P = kMfma ? 0 : NW * TILE * REP * 4;
+  constexpr int SZ_A0 = kMfma ? PlainMfmaLds<D, REP, NW>::bytes : SZ_Q + SZ_K + SZ_P;
   constexpr int SZ_A = SZ_A0 > kSelBytes ? SZ_A0 : kSelBytes;
   constexpr int SZ_B = kMfma ? 0 : NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
   char* s_q = smem + (threadIdx.x / kWave) * REP * RB;
   char* s_kall = smem + SZ_Q;
   float* s_pall = reinterpret_cast<float*>(smem + SZ_Q + SZ_K);
-  float* s_alpha = reinterpret_cast<float*>(smem + SZ_Q + SZ_K + SZ_P);
-  float* s_wo = reinterpret_cast<float*>(kMfma ? smem + SZ_Q + SZ_K + SZ_P + SZ_AL : smem);
-  char* s_vt = smem + SZ_Q + SZ_K + SZ_P + SZ_AL + SZ_WO;
-  char* s_kt = s_vt + SZ_VT;
+  float* s_wo = reinterpret_cast<float*>(smem);
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
 
   const int tid = threadIdx.x;
@@ -824,7 +1052,6 @@ decode_attn_kernel(DecodeParams P) {
   const int we = min(t1, ws + tiles_per_wave * TILE);
 
   float m_run[REP], acc_o[REP][EP], l_head[REP];
-  f32x4 acc_pv[kMfma ? D / 16 : 1];  // MFMA path: P.V accumulators (heads x columns)
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m_run[r] = -INFINITY;
@@ -838,190 +1065,7 @@ decode_attn_kernel(DecodeParams P) {
   const int voff0 = my_col * 16;
 
   if constexpr (kMfma) {
-    // ---- Producer/consumer wave pairs: every wave streams ONE contiguous
-    // row range of ONE tensor (on gfx950 a wave that streams two distant
-    // regions at once pulls markedly less bandwidth than one that streams a
-    // single region), 1 KiB of consecutive rows per load instruction (whole
-    // 128-byte lines; the MFMA operand layout read straight from memory
-    // would split every line over two instructions).  Each tile is staged
-    // in the wave's own LDS slot and read back in operand layout.  Waves
-    // [0, NP) read K and compute the scores on v_mfma_f32_16x16x32 (A = 16 K
-    // rows x 32 elements: lane l holds row l%16, elements 8*(l/16)..+8 of
-    // the k-step; B = q^T: lane l holds head l%16; D: lane l holds head
-    // l%16, rows 4*(l/16)..+4) and the online softmax; waves [NP, NW) read V
-    // and accumulate P.V with the tile's probabilities and rescale factors
-    // their partner leaves in LDS (double-buffered by tile parity, one
-    // workgroup barrier per tile).  Each wave keeps two tiles of loads in
-    // flight (one at D = 256).
-    constexpr int NBUF = NB * KS;
-    static_assert(NBUF == PPL, "K and V tiles use the same register budget");
-    constexpr int TIF = D > 128 ? 1 : 2;  // tiles in flight per wave (register budget)
-    const bool kwave = wave < NP;
-    const int pair = kwave ? wave : wave - NP;
-    const int tpp = (ntiles_total + NP - 1) / NP;   // tiles per pair, uniform in the workgroup
-    const int ps = t0 + pair * tpp * TILE;
-    const int pe = min(t1, ps + tpp * TILE);
-    uint16_t* pbuf = reinterpret_cast<uint16_t*>(s_pall) + pair * 2 * REP * TILE;
-    float* abuf = s_alpha + pair * 2 * REP;
-    const int hl = lane & 15;   // score layout: head
-    const int kg = lane >> 4;   // score layout: k-group / row quad
-    uint4 qb[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qb[s] = make_uint4(0, 0, 0, 0);
-    if (kwave && hl < nvalid_h) {
-      const char* qrow = reinterpret_cast<const char*>(P.q) +
-                         ((int64_t)b * P.q_stride_b + (int64_t)(hq0 + hl) * P.q_stride_h) * E::size;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        if (P.q_aligned) {
-          qb[s] = *reinterpret_cast<const uint4*>(qrow + (s * 32 + kg * 8) * 2);
-        } else {
-          const uint16_t* qh = reinterpret_cast<const uint16_t*>(qrow) + s * 32 + kg * 8;
-          qb[s] = make_uint4(qh[0] | ((uint32_t)qh[1] << 16), qh[2] | ((uint32_t)qh[3] << 16),
-                             qh[4] | ((uint32_t)qh[5] << 16), qh[6] | ((uint32_t)qh[7] << 16));
-        }
-      }
-    }
-    // The two roles run separate loops with the same number of workgroup
-    // barriers (tpp), so each role's registers are live only in its own loop.
-    if (kwave) {
-      float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
-      float l_lane = 0.f;        // this lane's share of head hl's denominator
-      char* kt = s_kt + pair * TILE * RB;
-      for (int it = 0; it < tpp; it += TIF) {
-        uint4 buf[TIF][NBUF];
-#pragma unroll
-        for (int u = 0; u < TIF; ++u) {
-          const int tb = ps + (it + u) * TILE;
-          const __amdgpu_buffer_rsrc_t rr = make_rsrc(kbase + (int64_t)tb * kst, (int64_t)(pe - tb) * kst);
-#pragma unroll
-          for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * kst) + voff0);
-        }
-#pragma unroll
-        for (int u = 0; u < TIF; ++u) {
-          if (it + u >= tpp) break;
-          const int tb = ps + (it + u) * TILE;
-          const int nrows = min(TILE, pe - tb);  // <= 0: every row masked
-          uint16_t* pt = pbuf + ((it + u) & 1) * REP * TILE;
-          float* at = abuf + ((it + u) & 1) * REP;
-          // stage the tile (rows past the slice arrived as zeros), read it
-          // back as MFMA A operands (this wave's own slot: no barrier)
-#pragma unroll
-          for (int i = 0; i < PPL; ++i) {
-            const int r = i * RPI + my_row0;
-            *reinterpret_cast<uint4*>(kt + r * RB + ((my_col ^ kswz<SL>(r)) << 4)) = buf[u][i];
-          }
-          f32x4 sc[NB];
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            sc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const int r = nb * 16 + hl;
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-              const uint4 a = *reinterpret_cast<const uint4*>(kt + r * RB + (((s * 4 + kg) ^ kswz<SL>(r)) << 4));
-              sc[nb] = MfmaOp<DT>::run(a, qb[s], sc[nb]);
-            }
-          }
-          float sv[NB][4], bm = -INFINITY;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const bool valid = nb * 16 + kg * 4 + c < nrows;
-              sv[nb][c] = valid ? sc[nb][c] * P.scale2 : -INFINITY;
-              bm = fmaxf(bm, sv[nb][c]);
-            }
-          bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-          bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-          const float m_new = fmaxf(m_lane, bm);
-          const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-          const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
-          m_lane = m_new;
-          float psum = 0.f;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            float p4[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              p4[c] = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
-              psum += p4[c];
-            }
-            // rows nb*16 + 4kg .. +3 of head hl: one 8-byte store
-            if (hl < REP)
-              *reinterpret_cast<uint2*>(pt + hl * TILE + nb * 16 + kg * 4) =
-                  make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
-          }
-          l_lane = l_lane * alpha + psum;
-          if (lane < REP) at[lane] = alpha;
-          __syncthreads();  // hand the tile's p and rescale factors to the V-wave
-        }
-      }
-      float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
-      lsum += __shfl_xor(lsum, 32, kWave);
-#pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
-        l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
-      }
-    } else {
-      // P.V on v_mfma_f32_16x16x32: A = P^T (lane l: head l%16, rows
-      // 8*(l/16)..+8 of the 32-row k-step, read from the K-wave's [head][row]
-      // tile), B = V (lane l: column l%16 of the 16-column block, the same 8
-      // rows, gathered from the LDS copy of the tile with two transposed
-      // reads), D: lane l holds heads 4*(l/16)..+4 of column l%16.
-      char* vt = s_vt + pair * TILE * RB;
-      const int hA = lane & 15;           // A operand head
-      const int gq = lane >> 4;           // lane group: 8-row slab of the k-step
-      const int prow = (lane & 15) >> 2;  // transposed read: row within the 4-row block
-      const int pcol = lane & 3;          // transposed read: 4-column group
-#pragma unroll
-      for (int db = 0; db < DB; ++db) acc_pv[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int it = 0; it < tpp; it += TIF) {
-        uint4 buf[TIF][NBUF];
-#pragma unroll
-        for (int u = 0; u < TIF; ++u) {
-          const int tb = ps + (it + u) * TILE;
-          const __amdgpu_buffer_rsrc_t rr = make_rsrc(vbase + (int64_t)tb * vst, (int64_t)(pe - tb) * vst);
-#pragma unroll
-          for (int i = 0; i < PPL; ++i) buf[u][i] = buf_ld16(rr, (int)((i * RPI + my_row0) * vst) + voff0);
-        }
-#pragma unroll
-        for (int u = 0; u < TIF; ++u) {
-          if (it + u >= tpp) break;
-          // stage the tile (rows past the slice arrived as zeros)
-#pragma unroll
-          for (int i = 0; i < PPL; ++i) {
-            const int r = i * RPI + my_row0;
-            *reinterpret_cast<uint4*>(vt + r * RB + ((my_col ^ vswz<SL>(r)) << 4)) = buf[u][i];
-          }
-          const uint16_t* pt = reinterpret_cast<const uint16_t*>(s_pall) + pair * 2 * REP * TILE +
-                               ((it + u) & 1) * REP * TILE;
-          const float* at = abuf + ((it + u) & 1) * REP;
-          __syncthreads();  // the K-wave's p and rescale factors for this tile are in LDS
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = at[min(4 * gq + e, REP - 1)];
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc_pv[db][e] *= a;
-          }
-#pragma unroll
-          for (int s2 = 0; s2 < KS2; ++s2) {
-            const uint4 pa = hA < REP ? *reinterpret_cast<const uint4*>(pt + hA * TILE + s2 * 32 + gq * 8)
-                                      : make_uint4(0, 0, 0, 0);
-            const int r0 = s2 * 32 + gq * 8 + prow;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-              const int pc = 2 * db + (pcol >> 1);
-              const int bo = (pcol & 1) * 8;
-              const uint2 lo = lds_read_tr16(vt + r0 * RB + ((pc ^ vswz<SL>(r0)) << 4) + bo);
-              const uint2 hi = lds_read_tr16(vt + (r0 + 4) * RB + ((pc ^ vswz<SL>(r0 + 4)) << 4) + bo);
-              acc_pv[db] = MfmaOp<DT>::run(pa, make_uint4(lo.x, lo.y, hi.x, hi.y), acc_pv[db]);
-            }
-          }
-        }
-      }
-    }
-    write_partial_pairs_mfma<D, REP, NP, DB>(P, wslot, kwave, pair, acc_pv, m_run, l_head, s_wo, s_wm, s_wl);
+    plain_rows_mfma<DT, D, REP, NW>(P, smem, s_wm, s_wl, kbase, vbase, kst, vst, t0, t1, b, hq0, nvalid_h, wslot);
     return;
   } else {
     // ---- VALU path (fp32): K transposed through LDS, lane groups per head.
@@ -1171,12 +1215,15 @@ template <int DT>
 __device__ __forceinline__ uint4 kivi_codes8(uint32_t c16) {
   uint32_t w[4];
   if constexpr (DT == HALO_F16) {
-    // 1024 + c is 0x6400 | c in fp16; subtracting 1024 (packed) is exact
+    // t = c16 | c16 << 14 puts code 2p at bits 4p and code 2p+1 at bits
+    // 4p + 16 of (t >> 4p); 1024 + c is 0x6400 | c in fp16, and subtracting
+    // 1024 (packed) is exact
     typedef __attribute__((ext_vector_type(2))) _Float16 h2;
     const h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t t = c16 | (c16 << 14);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const uint32_t v = 0x64006400u | ((c16 >> (4 * p)) & 3u) | (((c16 >> (4 * p + 2)) & 3u) << 16);
+      const uint32_t v = ((t >> (4 * p)) & 0x00030003u) | 0x64006400u;
       w[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v) - off);
     }
   } else {
@@ -1203,6 +1250,16 @@ __device__ __forceinline__ void mul8_bf16_split(const uint4& a, const uint4& b, 
   hi = make_uint4(h[0], h[1], h[2], h[3]);
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
+// fp16 only: 8 consecutive 2-bit codes as the fp16 bit patterns 0..3, i.e.
+// the subnormals c * 2^-24 (exact; the matrix cores keep fp16 subnormal
+// inputs), so one shift and one mask place two codes.  Products against
+// them carry a factor 2^-24 that the caller removes exactly.
+__device__ __forceinline__ uint4 kivi_codes8_sub(uint32_t c16) {
+  const uint32_t t = c16 | (c16 << 14);
+  return make_uint4(t & 0x00030003u, (t >> 4) & 0x00030003u, (t >> 8) & 0x00030003u, (t >> 12) & 0x00030003u);
+}
+constexpr float kSub16Scale = 16777216.0f;  // 2^24
+
 // elementwise product of two 8-element K/V-dtype pieces, rounded to the dtype
 template <int DT>
 __device__ __forceinline__ uint4 mul8(const uint4& a, const uint4& b) {
@@ -1294,11 +1351,20 @@ decode_attn_kivi_kernel(DecodeParams P) {
   // V side: codes (channel-major, 8 bytes per channel) at CB+4D, scale/zero (group-major)
   constexpr int VC = CB + 4 * D, VS = 2 * CB + 4 * D, VZ = 2 * CB + 6 * D;
 
-  __shared__ __attribute__((aligned(16))) char s_raw[NW][TBYTES];
-  __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][REP * 32];  // p of one block, [head][token]
-  __shared__ float s_al[NW][REP];
-  __shared__ float s_wo[NW * REP * D];
+  // LDS: per wave a raw tile, the p of one block ([head][token]) and its
+  // rescale factors, then the wave partials; the plain-row path (the
+  // unquantised recent rows in the same launch) reuses the same bytes.
+  constexpr int SZ_RAW = NW * TBYTES;
+  constexpr int SZ_PB = NW * REP * 32 * 2;
+  constexpr int SZ_ALW = (NW * REP * 4 + 15) / 16 * 16;
+  constexpr int SZ_KL = SZ_RAW + SZ_PB + SZ_ALW + NW * REP * D * 4;
+  constexpr int SZ_PL = PlainMfmaLds<D, REP, NW>::bytes;
+  __shared__ __attribute__((aligned(16))) char smem[SZ_KL > SZ_PL ? SZ_KL : SZ_PL];
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
+  char (*s_raw)[TBYTES] = reinterpret_cast<char (*)[TBYTES]>(smem);
+  uint16_t (*s_p)[REP * 32] = reinterpret_cast<uint16_t (*)[REP * 32]>(smem + SZ_RAW);
+  float (*s_al)[REP] = reinterpret_cast<float (*)[REP]>(smem + SZ_RAW + SZ_PB);
+  float* s_wo = reinterpret_cast<float*>(smem + SZ_RAW + SZ_PB + SZ_ALW);
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1322,10 +1388,19 @@ decode_attn_kivi_kernel(DecodeParams P) {
   const int nvalid_h = min(REP, P.rep - sub * REP);
 
   int t0 = item.z, t1 = min(item.w, dsc.T_c);
-  if (!(dsc.flags & HALO_CHUNK_KIVI2)) t1 = t0;  // not a KIVI chunk: nothing this kernel can read
   if ((dsc.flags & HALO_CHUNK_CAUSAL) && P.q_pos != nullptr) {
     const int64_t lim = P.q_pos[b] - dsc.chunk_start + 1;
     if (lim < (int64_t)t1) t1 = (int)max<int64_t>(lim, (int64_t)t0);
+  }
+  if (!(dsc.flags & HALO_CHUNK_KIVI2)) {
+    // plain K/V rows (the unquantised recent tokens) in the same launch
+    const char* kb = reinterpret_cast<const char*>(dsc.k) +
+                     ((dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h) * E::size;
+    const char* vb = reinterpret_cast<const char*>(dsc.v) +
+                     ((dsc.batch < 0 ? (int64_t)b * dsc.v_stride_b : 0) + (int64_t)h_kv * dsc.v_stride_h) * E::size;
+    plain_rows_mfma<DT, D, REP, NW>(P, smem, s_wm, s_wl, kb, vb, dsc.k_stride_t * E::size, dsc.v_stride_t * E::size,
+                                    t0, t1, b, hq0, nvalid_h, wslot);
+    return;
   }
   // block bytes of this (b, h_kv); strides are in bytes for KIVI chunks
   const char* base = reinterpret_cast<const char*>(dsc.k) +
@@ -1365,8 +1440,11 @@ decode_attn_kivi_kernel(DecodeParams P) {
     }
   }
   f32x4 acc[DB];
+  f32x4 accz[DT == HALO_F16 ? NG : 1];  // fp16: zero terms per V group
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int gg = 0; gg < (DT == HALO_F16 ? NG : 1); ++gg) accz[gg] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
   float l_lane = 0.f;        // this lane's share of head hl's denominator
   char* raw = s_raw[wave];
@@ -1407,7 +1485,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) {
             const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
-            const uint4 cd = kivi_codes8<DT>(c16);
+            const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
             sc[nb] = MfmaOp<DT>::run(cd, qs, sc[nb]);
             if constexpr (DT == HALO_BF16) sc[nb] = MfmaOp<DT>::run(cd, qs_lo, sc[nb]);
           }
@@ -1420,7 +1498,8 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const bool valid = nb * 16 + kg * 4 + c < nrows;
-            sv[nb][c] = valid ? (sc[nb][c] + sz[c]) * P.scale2 : -INFINITY;
+            const float s_code = DT == HALO_F16 ? sc[nb][c] * kSub16Scale : sc[nb][c];
+            sv[nb][c] = valid ? (s_code + sz[c]) * P.scale2 : -INFINITY;
             bm = fmaxf(bm, sv[nb][c]);
           }
         bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
@@ -1446,11 +1525,17 @@ decode_attn_kivi_kernel(DecodeParams P) {
         if (lane < REP) alw[lane] = alpha;
         wave_lds_fence();
         // ---- P.V: per group, codes against p*s and the zeros against p
+        if (__builtin_amdgcn_read_exec() & __ballot(hl < REP && alpha != 1.f)) {  // some head's max moved
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = alw[min(4 * kg + e, REP - 1)];
+          for (int e = 0; e < 4; ++e) {
+            const float a = alw[min(4 * kg + e, REP - 1)];
 #pragma unroll
-          for (int db = 0; db < DB; ++db) acc[db][e] *= a;
+            for (int db = 0; db < DB; ++db) acc[db][e] *= a;
+            if constexpr (DT == HALO_F16) {
+#pragma unroll
+              for (int gg = 0; gg < NG; ++gg) accz[gg][e] *= a;
+            }
+          }
         }
         const uint4 pa = hl < REP ? *reinterpret_cast<const uint4*>(pw + hl * 32 + kg * 8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
@@ -1464,11 +1549,16 @@ decode_attn_kivi_kernel(DecodeParams P) {
           for (int d2 = 0; d2 < 2; ++d2) {
             const int db = 2 * gg + d2;
             const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
-            const uint4 cd = kivi_codes8<DT>(c16);
+            const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
             acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
-            if constexpr (DT == HALO_BF16) acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
-            acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
+            if constexpr (DT == HALO_BF16) {
+              acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
+              acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
+            }
           }
+          // fp16: the code products carry 2^-24, so the zero term of the
+          // group (equal for all its columns) accumulates on its own
+          if constexpr (DT == HALO_F16) accz[gg] = MfmaOp<DT>::run(pa, zv8, accz[gg]);
         }
         wave_lds_fence();  // the next block rewrites p and the rescale factors
       }
@@ -1482,6 +1572,12 @@ decode_attn_kivi_kernel(DecodeParams P) {
   for (int r = 0; r < REP; ++r) {
     m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
     l_head[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), r));
+  }
+  if constexpr (DT == HALO_F16) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[db][e] = acc[db][e] * kSub16Scale + accz[db / 2][e];
   }
   write_partial_owners<D, REP, NW, DB>(P, wslot, wave, true, true, acc, m_run, l_head, s_wo, s_wm, s_wl);
 }

@@ -83,16 +83,16 @@ class DecodePlan:
     rows: int                    # attended K/V rows summed over (b, h_kv)
     keep: list = field(default_factory=list)  # tensors the descriptors point at
     work_host: Optional[np.ndarray] = None
-    kivi: bool = False           # every chunk is a run of 2-bit KIVI blocks
+    kivi: bool = False           # the table holds KIVI block runs (plain chunks may join them)
+    kivi_rows: int = 0           # rows of ``rows`` that are KIVI-quantised
 
     @property
     def kv_bytes(self) -> int:
         """Algorithmic K+V bytes one launch streams (every row read once)."""
-        if self.kivi:
-            from .kivi import GROUP, block_bytes
-            return self.rows // GROUP * block_bytes(self.D)
+        from .kivi import GROUP, block_bytes
         esz = torch.tensor([], dtype=self.dtype).element_size()
-        return self.rows * 2 * self.D * esz
+        return (self.kivi_rows // GROUP * block_bytes(self.D)
+                + (self.rows - self.kivi_rows) * 2 * self.D * esz)
 
 
 def choose_rep_t(rep: int) -> int:
@@ -261,9 +261,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
 
     descs, keep = pack_descs(chunks, B=B, H_kv=H_kv, D=D, dtype=dtype)
     kinds = {hasattr(c, "blocks") for c in chunks if not isinstance(c, SlotRef)}
-    if len(kinds) > 1:
-        raise AssertionError("a plan holds either plain or KIVI chunks; merge the two through accumulators")
-    kivi = kinds == {True}
+    kivi = True in kinds  # KIVI block runs, possibly with plain chunks (one KIVI launch)
     if kivi and split is not None and split % 32:
         raise AssertionError(f"split={split} must be a multiple of the 32-token KIVI block")
 
@@ -290,6 +288,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
     work = []
     offsets = [0]
     rows_attended = 0
+    kivi_rows = 0
     for b in range(B):
         live_idx = [i for i, c in enumerate(chunks) if live(c, b)]
         for h in range(H_kv):
@@ -305,6 +304,8 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                         work.append((i, g, t0, min(t0 + split, hi), len(work), 0, 0, 0))
                     if s == 0:
                         rows_attended += hi
+                        if hasattr(chunks[i], "blocks"):
+                            kivi_rows += hi
                 if len(work) == n0:
                     work.append((0, g, 0, 0, len(work), 0, 0, 0))
                 offsets.append(len(work))
@@ -318,7 +319,7 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
         descs=dev_descs, work=_to_device(work_np.reshape(-1), device),
         offsets=_to_device(np.asarray(offsets, dtype=np.int32), device),
         n_desc=len(chunks), n_work=len(work), n_groups=n_groups,
-        rows=rows_attended, keep=keep, work_host=work_np, kivi=kivi,
+        rows=rows_attended, keep=keep, work_host=work_np, kivi=kivi, kivi_rows=kivi_rows,
     )
 
 

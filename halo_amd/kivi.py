@@ -98,33 +98,25 @@ class KiviDecodeLayer:
 
     ``cold_blocks`` (B, H_kv, n, block_bytes) hold tokens [0, 32n) (from
     :func:`quantize`); ``recent`` are plain ``decode.ChunkRef`` chunks after
-    them.  One step is two launches on the current stream: the KIVI chunks
-    write fp32 accumulators (acc_mode 2), the recent chunks merge into them
-    and write (out, lse) (acc_mode 1) -- the quantised-buffer-plus-residual
-    split of KIVICache.update (baselines/kivi_cache.py:137-195) without
-    materialising the dequantised cache.
+    them.  One step is one attention launch plus its merge: the KIVI blocks
+    and the recent rows are work items of the same table -- the
+    quantised-buffer-plus-residual split of KIVICache.update
+    (baselines/kivi_cache.py:137-195) without materialising the dequantised
+    cache.
     """
 
     def __init__(self, *, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype, cold_blocks: torch.Tensor,
                  recent, device, chunk_tokens: int = 2048, split=None) -> None:
         from .decode import build_plan
-        from .triton_chunked import init_acc
         if chunk_tokens % GROUP:
             raise AssertionError(f"chunk_tokens={chunk_tokens} must be a multiple of {GROUP}")
         n = int(cold_blocks.shape[2])
         per = chunk_tokens // GROUP
         cold = [KiviChunkRef(cold_blocks[:, :, j:min(j + per, n)], j * GROUP, True) for j in range(0, n, per)]
         self.B, self.H, self.D = B, H, D
-        self.cold_plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=cold, device=device, split=split)
-        self.recent_plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=list(recent), device=device) \
-            if recent else None
-        self.m, self.l, self.o = init_acc(B=B, H=H, D_v=D, device=device)
+        self.plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=cold + list(recent or []),
+                               device=device, split=split)
 
     def step(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse=None, q_pos=None) -> None:
         from .decode import launch
-        if self.recent_plan is None:
-            launch(self.cold_plan, q, scale=scale, q_pos=q_pos, out=out, lse=lse)
-            return
-        launch(self.cold_plan, q, scale=scale, q_pos=q_pos, m=self.m, l=self.l, o=self.o, acc_mode=2)
-        launch(self.recent_plan, q, scale=scale, q_pos=q_pos, m=self.m, l=self.l, o=self.o, acc_mode=1,
-               out=out, lse=lse)
+        launch(self.plan, q, scale=scale, q_pos=q_pos, out=out, lse=lse)

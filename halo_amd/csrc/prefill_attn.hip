@@ -10,14 +10,17 @@
 //
 // Tiling: one workgroup = 4 waves = 128 query rows of one query head; each
 // wave owns 32 rows as two 16-row MFMA column blocks.  Key tiles of 64 rows
-// are staged in LDS by the whole workgroup: K row-major (read as MFMA A
-// operands), V transposed (V^T[d][key], read as A operands of O^T = V^T P^T).
+// are staged in LDS by the whole workgroup, double-buffered (the next tile's
+// loads are in flight while the current one is consumed): K row-major (read
+// as MFMA A operands), V row-major with swizzled pieces, read with
+// transposed LDS reads as the A operands of O^T = V^T P^T.
 //   scores  S^T[key][q] = sum_d K[key][d] Q[q][d]    v_mfma_f32_16x16x32
 //   output  O^T[d][q]  += sum_key V^T[d][key] P^T[key][q]
 // The P^T operand is built in registers from the S^T accumulators with a
 // permuted key order inside each 32-key step (keys 4g..4g+3 and 16+4g..
 // 16+4g+3 for lane group g); V^T is read with the same permutation, so no
-// cross-lane movement is needed.  Workgroups are mapped so that the query
+// cross-lane movement is needed.  Masks are applied only on tiles that cross
+// a chunk end or the causal diagonal.  Workgroups are mapped so that the query
 // heads sharing a KV head run on the same XCD (its L2 serves their K/V).
 
 #include "common.hpp"
@@ -37,7 +40,9 @@ struct PMfma<HALO_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
   __device__ static __forceinline__ uint32_t pack(float a, float b) {
-    return (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+    typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+    const b2 v = {(__bf16)a, (__bf16)b};  // round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 template <>
@@ -47,7 +52,9 @@ struct PMfma<HALO_F16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
   __device__ static __forceinline__ uint32_t pack(float a, float b) {
-    return (uint32_t)f32_to_f16_rne(a) | ((uint32_t)f32_to_f16_rne(b) << 16);
+    typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+    const h2 v = {(_Float16)a, (_Float16)b};  // round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
@@ -80,18 +87,39 @@ constexpr int kPfQW = 32;   // query rows per wave
 constexpr int kPfBQ = kPfNW * kPfQW;
 constexpr int kPfBK = 64;   // key rows per LDS tile
 
+// V tile in LDS: row r holds its 16-byte pieces at positions piece ^ swizzle(r)
+// (an even XOR: the piece pairs one transposed read covers stay adjacent; 4
+// consecutive rows land on distinct 32-byte bank ranges).
+template <int SL>
+__device__ __forceinline__ int pf_vswz(int r) {
+  return (2 * (r & 3) + 8 * ((r >> 3) & 1)) & (SL - 1);
+}
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
+// of the 8-byte reads of lanes 4e + i/4 (e = 0..3).
+typedef short pv4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 pf_tr16(const char* p) {
+  const pv4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) pv4i16_t*)(__attribute__((address_space(3))) char*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+// Slack (log2 units) by which a tile's max may exceed the running max before
+// the running max moves: probabilities stay below 2^8 and the accumulators are
+// rescaled only when the max really moves; out = o / l and lse = m + log2(l)
+// use the same m, so the result does not depend on when m moved.
+constexpr float kPfLazyMax = 8.0f;
+
 template <int DT, int D>
 __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
-  constexpr int KS = D / 32;            // d-steps of the score MFMA
-  constexpr int DB = D / 16;            // d-blocks of the output MFMA
-  constexpr int SL = D / 8;             // 16-byte pieces per row
-  constexpr int KROWB = D * 2 + 16;     // padded K row in LDS (bytes)
-  constexpr int VTROW = kPfBK * 2 + 16; // padded V^T row in LDS (bytes)
-  constexpr int KPT = kPfBK * SL / 256; // K pieces per thread per tile
-  constexpr int KQ = kPfBK / 4;         // key quads per tile
-  static_assert(KPT >= 1 && KQ * SL <= 256 * 1, "prefill tile shape");
-  __shared__ __attribute__((aligned(16))) char s_k[kPfBK * KROWB];
-  __shared__ __attribute__((aligned(16))) char s_vt[D * VTROW];
+  constexpr int KS = D / 32;              // d-steps of the score MFMA
+  constexpr int DB = D / 16;              // d-blocks of the output MFMA
+  constexpr int SL = D / 8;               // 16-byte pieces per row
+  constexpr int RB = D * 2;               // row bytes
+  constexpr int KROWB = RB + 16;          // padded K row in LDS (bytes)
+  constexpr int KTB = kPfBK * KROWB;      // K tile bytes in LDS
+  constexpr int STAGE = KTB + kPfBK * RB; // K tile + V tile
+  constexpr int KPT = kPfBK * SL / 256;   // K (and V) pieces per thread per tile
+  static_assert(KPT >= 1 && kPfBK * SL % 256 == 0, "prefill tile shape");
+  __shared__ __attribute__((aligned(16))) char s_buf[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -128,124 +156,169 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   const int64_t qpos0 = qs + row0 + ql;             // column block 0 query position
   const int64_t wg_qmax = qs + min(qt * kPfBQ + kPfBQ, P.T_q) - 1;
+  const int64_t wave_qmin = qs + row0;              // smallest query position of this wave
 
-  for (int ci = 0; ci < P.n_desc; ++ci) {
-    const halo_chunk_desc dsc = P.descs[ci];
-    if (dsc.batch >= 0 && dsc.batch != b) continue;
-    const bool causal = dsc.flags & HALO_CHUNK_CAUSAL;
-    int rows = dsc.T_c;
-    if (causal) rows = (int)max<int64_t>(0, min<int64_t>(rows, wg_qmax - dsc.chunk_start + 1));
-    if (rows <= 0) continue;
-    const char* kbase = reinterpret_cast<const char*>(dsc.k) +
-                        ((dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h) * 2;
-    const char* vbase = reinterpret_cast<const char*>(dsc.v) +
-                        ((dsc.batch < 0 ? (int64_t)b * dsc.v_stride_b : 0) + (int64_t)h_kv * dsc.v_stride_h) * 2;
-    const int64_t kst = dsc.k_stride_t * 2, vst = dsc.v_stride_t * 2;
-    for (int kt = 0; kt < rows; kt += kPfBK) {
-      const __amdgpu_buffer_rsrc_t rk = prsrc(kbase + (int64_t)kt * kst, (int64_t)(rows - kt) * kst);
-      const __amdgpu_buffer_rsrc_t rv = prsrc(vbase + (int64_t)kt * vst, (int64_t)(rows - kt) * vst);
-      uint4 kr[KPT], vr[4];
+  // ---- walk the (chunk, 64-row tile) sequence, one tile ahead
+  struct Tile {
+    const char* kb;
+    const char* vb;
+    int64_t kst, vst, cstart;
+    int rows, kt, causal;
+  };
+  // the first tile of the first chunk at or after `from` that has rows for
+  // this workgroup; returns false at the end of the table
+  auto open_chunk = [&](int from, int& ci, Tile& t) -> bool {
+    for (int c = from; c < P.n_desc; ++c) {
+      const halo_chunk_desc d = P.descs[c];
+      if (d.batch >= 0 && d.batch != b) continue;
+      const int causal = d.flags & HALO_CHUNK_CAUSAL;
+      int rows = d.T_c;
+      if (causal) rows = (int)max<int64_t>(0, min<int64_t>(rows, wg_qmax - d.chunk_start + 1));
+      if (rows <= 0) continue;
+      t.kb = reinterpret_cast<const char*>(d.k) +
+             ((d.batch < 0 ? (int64_t)b * d.k_stride_b : 0) + (int64_t)h_kv * d.k_stride_h) * 2;
+      t.vb = reinterpret_cast<const char*>(d.v) +
+             ((d.batch < 0 ? (int64_t)b * d.v_stride_b : 0) + (int64_t)h_kv * d.v_stride_h) * 2;
+      t.kst = d.k_stride_t * 2;
+      t.vst = d.v_stride_t * 2;
+      t.cstart = d.chunk_start;
+      t.rows = rows;
+      t.kt = 0;
+      t.causal = causal;
+      ci = c;
+      return true;
+    }
+    ci = P.n_desc;
+    return false;
+  };
+  auto load_tile = [&](const Tile& t, uint4 (&kr)[KPT], uint4 (&vr)[KPT]) {
+    const __amdgpu_buffer_rsrc_t rk = prsrc(t.kb + (int64_t)t.kt * t.kst, (int64_t)(t.rows - t.kt) * t.kst);
+    const __amdgpu_buffer_rsrc_t rv = prsrc(t.vb + (int64_t)t.kt * t.vst, (int64_t)(t.rows - t.kt) * t.vst);
 #pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const int id = tid + 256 * j;
-        kr[j] = pld16(rk, (int)((id / SL) * kst) + (id % SL) * 16);
-      }
-      const int vp = tid % SL, vq = tid / SL;   // V: d-piece, key quad
-      const bool vlive = vq < KQ;
+    for (int j = 0; j < KPT; ++j) {
+      const int id = tid + 256 * j;
+      kr[j] = pld16(rk, (int)((id / SL) * t.kst) + (id % SL) * 16);
+      vr[j] = pld16(rv, (int)((id / SL) * t.vst) + (id % SL) * 16);
+    }
+  };
+  auto store_tile = [&](char* st, const uint4 (&kr)[KPT], const uint4 (&vr)[KPT]) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) vr[j] = vlive ? pld16(rv, (int)((vq * 4 + j) * vst) + vp * 16) : make_uint4(0, 0, 0, 0);
-      __syncthreads();  // the previous tile's readers are done
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const int id = tid + 256 * j;
-        *reinterpret_cast<uint4*>(s_k + (id / SL) * KROWB + (id % SL) * 16) = kr[j];
-      }
-      if (vlive) {
-        // 4 keys x 8 channels -> 8 channels x 4 keys (two 16-bit keys per dword)
-        const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
-        const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-        const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
-        const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[j], w0[j], 0x05040100u),
-                                      __builtin_amdgcn_perm(w3[j], w2[j], 0x05040100u));
-          const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[j], w0[j], 0x07060302u),
-                                      __builtin_amdgcn_perm(w3[j], w2[j], 0x07060302u));
-          *reinterpret_cast<uint2*>(s_vt + (vp * 8 + 2 * j) * VTROW + vq * 8) = lo;
-          *reinterpret_cast<uint2*>(s_vt + (vp * 8 + 2 * j + 1) * VTROW + vq * 8) = hi;
-        }
-      }
-      __syncthreads();
+    for (int j = 0; j < KPT; ++j) {
+      const int id = tid + 256 * j;
+      const int r = id / SL, pc = id % SL;
+      *reinterpret_cast<uint4*>(st + r * KROWB + pc * 16) = kr[j];
+      *reinterpret_cast<uint4*>(st + KTB + r * RB + ((pc ^ pf_vswz<SL>(r)) << 4)) = vr[j];
+    }
+  };
 
-      // scores S^T for 4 key blocks x 2 query column blocks
-      pf32x4 st[4][2];
+  int ci;
+  Tile cur;
+  bool have = open_chunk(0, ci, cur);
+  if (have) {
+    uint4 kr[KPT], vr[KPT];
+    load_tile(cur, kr, vr);
+    store_tile(s_buf, kr, vr);
+  }
+  __syncthreads();
+  int stage = 0;
+  while (have) {
+    // the next tile: its loads are in flight while this one is consumed
+    Tile nxt = cur;
+    int ni = ci;
+    bool have_nxt = true;
+    nxt.kt += kPfBK;
+    if (nxt.kt >= nxt.rows) have_nxt = open_chunk(ci + 1, ni, nxt);
+    uint4 kr[KPT], vr[KPT];
+    if (have_nxt) load_tile(nxt, kr, vr);
+
+    const char* sk = s_buf + stage * STAGE;
+    const char* sv = sk + KTB;
+    // scores S^T for 4 key blocks x 2 query column blocks
+    pf32x4 st[4][2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        st[kb][0] = pf32x4{0.f, 0.f, 0.f, 0.f};
-        st[kb][1] = pf32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb][0] = pf32x4{0.f, 0.f, 0.f, 0.f};
+      st[kb][1] = pf32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const uint4 a = *reinterpret_cast<const uint4*>(s_k + (kb * 16 + ql) * KROWB + (s * 32 + g * 8) * 2);
-          st[kb][0] = PMfma<DT>::run(a, qb[0][s], st[kb][0]);
-          st[kb][1] = PMfma<DT>::run(a, qb[1][s], st[kb][1]);
-        }
+      for (int s = 0; s < KS; ++s) {
+        const uint4 a = *reinterpret_cast<const uint4*>(sk + (kb * 16 + ql) * KROWB + (s * 32 + g * 8) * 2);
+        st[kb][0] = PMfma<DT>::run(a, qb[0][s], st[kb][0]);
+        st[kb][1] = PMfma<DT>::run(a, qb[1][s], st[kb][1]);
       }
-      // online softmax per query column (lane's query ql of each block)
-      uint4 pb[2][2];
+    }
+    // masking only where the tile crosses the chunk end or the causal diagonal
+    const bool masked = cur.kt + kPfBK > cur.rows || (cur.causal && cur.cstart + cur.kt + kPfBK - 1 > wave_qmin);
+    uint4 pb[2][2];
+    bool moved = false;
+    float alpha[2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int64_t qp = qpos0 + c * 16;
-        float sv[4][4], bm = -INFINITY;
+    for (int c = 0; c < 2; ++c) {
+      const int64_t qp = qpos0 + c * 16;
+      float sv4[4][4];
+      float bm = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = kt + kb * 16 + g * 4 + e;
-            bool valid = key < rows;
-            if (causal) valid = valid && (dsc.chunk_start + key <= qp);
-            sv[kb][e] = valid ? st[kb][c][e] * P.scale2 : -INFINITY;
-            bm = fmaxf(bm, sv[kb][e]);
+        for (int e = 0; e < 4; ++e) {
+          float x = st[kb][c][e];
+          if (masked) {
+            const int key = cur.kt + kb * 16 + g * 4 + e;
+            const bool valid = key < cur.rows && (!cur.causal || cur.cstart + key <= qp);
+            x = valid ? x : -INFINITY;
           }
-        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float m_new = fmaxf(m_run[c], bm);
-        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run[c] - ms);
-        m_run[c] = m_new;
-        float p[4][4], psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            p[kb][e] = __builtin_amdgcn_exp2f(sv[kb][e] - ms);
-            psum += p[kb][e];
-          }
-        l_run[c] = l_run[c] * alpha + psum;
-        if (alpha != 1.f) {
-#pragma unroll
-          for (int db = 0; db < DB; ++db) o[c][db] *= alpha;
+          sv4[kb][e] = x;
+          bm = fmaxf(bm, x);
         }
-        // P^T operand of key step t: keys 4g..4g+3 of block 2t, then of block 2t+1
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float bms = bm * P.scale2;  // scores scale after the max (scale > 0)
+      const float m_old = m_run[c];
+      const float m_new = (bms > m_old + kPfLazyMax) ? bms : m_old;
+      alpha[c] = (m_new == m_old) ? 1.f : __builtin_amdgcn_exp2f(m_old - m_new);
+      moved |= m_new != m_old;
+      m_run[c] = m_new;
+      const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+      float p[4][4], psum = 0.f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          pb[c][t] = make_uint4(PMfma<DT>::pack(p[2 * t][0], p[2 * t][1]), PMfma<DT>::pack(p[2 * t][2], p[2 * t][3]),
-                                PMfma<DT>::pack(p[2 * t + 1][0], p[2 * t + 1][1]),
-                                PMfma<DT>::pack(p[2 * t + 1][2], p[2 * t + 1][3]));
-      }
-      // O^T += V^T P^T
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv4[kb][e], P.scale2, -ms));
+          psum += p[kb][e];
+        }
+      l_run[c] = l_run[c] * alpha[c] + psum;
+      // P^T operand of key step t: keys 4g..4g+3 of block 2t, then of block 2t+1
 #pragma unroll
       for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const char* vrow = s_vt + (db * 16 + ql) * VTROW;
-          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + (t * 32 + g * 4) * 2);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + (t * 32 + 16 + g * 4) * 2);
-          const uint4 a = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          o[0][db] = PMfma<DT>::run(a, pb[0][t], o[0][db]);
-          o[1][db] = PMfma<DT>::run(a, pb[1][t], o[1][db]);
-        }
+        pb[c][t] = make_uint4(PMfma<DT>::pack(p[2 * t][0], p[2 * t][1]), PMfma<DT>::pack(p[2 * t][2], p[2 * t][3]),
+                              PMfma<DT>::pack(p[2 * t + 1][0], p[2 * t + 1][1]),
+                              PMfma<DT>::pack(p[2 * t + 1][2], p[2 * t + 1][3]));
     }
+    if (__builtin_amdgcn_read_exec() & __ballot(moved)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[c][db] *= alpha[c];
+    }
+    // O^T += V^T P^T; V^T operands by transposed reads in the same key order
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int rlo = t * 32 + g * 4 + (ql >> 2), rhi = rlo + 16;
+        const int pc = 2 * db + ((ql & 3) >> 1), bo = (ql & 1) * 8;
+        const uint2 a0 = pf_tr16(sv + rlo * RB + ((pc ^ pf_vswz<SL>(rlo)) << 4) + bo);
+        const uint2 a1 = pf_tr16(sv + rhi * RB + ((pc ^ pf_vswz<SL>(rhi)) << 4) + bo);
+        const uint4 a = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        o[0][db] = PMfma<DT>::run(a, pb[0][t], o[0][db]);
+        o[1][db] = PMfma<DT>::run(a, pb[1][t], o[1][db]);
+      }
+    if (have_nxt) store_tile(s_buf + (stage ^ 1) * STAGE, kr, vr);
+    __syncthreads();  // the next tile is in LDS; this one is free for the tile after
+    stage ^= 1;
+    cur = nxt;
+    ci = ni;
+    have = have_nxt;
   }
 
   // normalise and store: lane holds O^T[d = 16db + 4g + e][query ql]

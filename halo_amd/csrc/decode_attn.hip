@@ -271,15 +271,18 @@ struct Selector {
   using E = Elem<DT>;
   static constexpr int EP = E::per16;
   static constexpr int PIECES = D / EP;                               // 16-byte pieces per row
+  static constexpr int G = D / 16;                                    // dot-product slices
+  static_assert(D % 16 == 0, "dot-product slices");
   static constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
   static constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
   static constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
   static constexpr int QB = 8;                                        // query heads summed per load batch
   static constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
-  // triples whose page-mean rows are loaded up front (the rest, only with
-  // rows wider than 256 bytes, are loaded where they are used)
-  static constexpr int TE = PIECES <= 16 ? kSelTPT : 1;
-  uint4 kb[TE][PIECES];       // page-mean rows of this thread's (page, row, head) triples
+  // triples whose page-mean rows are loaded up front (the rest are loaded
+  // where they are used: a second triple per thread only exists past 256
+  // triples, and rows of 512 bytes stay out of registers until then)
+  static constexpr int TE = PIECES < 16 ? kSelTPT : (PIECES == 16 ? 1 : 0);
+  uint4 kb[TE > 0 ? TE : 1][PIECES];  // page-mean rows of this thread's first TE triples
   int my_r[kSelTPT], my_h[kSelTPT];
   uint2 cw[CW];               // this thread's share of the candidate descriptors
   uint4 qv[QP][QB];           // first QB query heads of this thread's q-bar pieces (aligned q)
@@ -339,9 +342,11 @@ struct Selector {
   }
 
   // Same arithmetic as halo_chunk_score_topk: GQA-mean query rounded to the
-  // q dtype, ordered fp32 dot products with the page means (products and
-  // sums rounded separately), max over (row, KV head), rank by (score desc,
-  // index asc).  Returns the chunk index for `slot` (-1: slot past the
+  // q dtype, fp32 dot products with the page means in the scorer's fixed
+  // order (products and sums rounded separately: D cut into G = D/16 slices,
+  // slice s holding the 16-byte pieces s, s + G, ..., each slice summed in
+  // order, then a balanced pairwise tree over the slices), max over (row, KV
+  // head), rank by (score desc, index asc).  Returns the chunk index for `slot` (-1: slot past the
   // eligible count); the chosen descriptors are left in LDS at s_cat.
   __device__ __forceinline__ int finish(const DecodeParams& P, char* smem, int slot, bool writer) {
     const halo_select_cfg& S = P.sel;
@@ -433,15 +438,27 @@ struct Selector {
         const char* row = reinterpret_cast<const char*>(S.kmean) +
                           ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
                            (int64_t)(t / nrh) * S.km_stride_p) * E::size;
-        float acc = 0.f;
+        // the scorer's fixed order: piece c belongs to slice c % G (G = D/16)
+        // and comes at position c / G of it; G independent slice sums, then
+        // the pairwise tree over slices
+        float part[G];
 #pragma unroll
-        for (int c = 0; c < PIECES; ++c) {
-          float f[EP];
-          E::unpack(u < TE ? kb[u < TE ? u : 0][c] : *reinterpret_cast<const uint4*>(row + c * 16), f);
+        for (int sl = 0; sl < G; ++sl) {
+          float a = 0.f;
 #pragma unroll
-          for (int e = 0; e < EP; ++e) acc = acc + qg[c * EP + e] * f[e];
+          for (int c = sl; c < PIECES; c += G) {
+            float f[EP];
+            E::unpack(u < TE ? kb[u < TE ? u : 0][c] : *reinterpret_cast<const uint4*>(row + c * 16), f);
+#pragma unroll
+            for (int e = 0; e < EP; ++e) a = __fadd_rn(a, __fmul_rn(qg[c * EP + e], f[e]));
+          }
+          part[sl] = a;
         }
-        s_dot[t] = acc;
+#pragma unroll
+        for (int w = 1; w < G; w <<= 1)
+#pragma unroll
+          for (int sl = 0; sl + w < G; sl += 2 * w) part[sl] = __fadd_rn(part[sl], part[sl + w]);
+        s_dot[t] = part[0];
       }
     }
     __syncthreads();
@@ -1876,6 +1893,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
     HALO_CHECK_ARG(S.lead_items >= 0, "lead_items must be >= 0");
     HALO_CHECK_ARG(S.n_cold * rows * H_kv <= kSelTPT * 256, "n_cold * rows * H_kv must be <= 512");
     HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
+    HALO_CHECK_ARG(D % 16 == 0, "in-kernel selection needs head_dim % 16 == 0");
     HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(S.kmean) % 16 == 0 && (S.km_stride_b * esz) % 16 == 0 &&
                        (S.km_stride_h * esz) % 16 == 0 && (S.km_stride_p * esz) % 16 == 0,
                    "kmean rows must be 16-byte aligned");

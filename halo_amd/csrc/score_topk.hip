@@ -164,7 +164,8 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
   // (page, row, head) triple computes the whole dot product from 16-byte
   // loads that are all independent (one memory round trip per batch of
   // triples), products and sums rounded separately (no fused multiply-add),
-  // summed in channel order; the max over (row, h) is folded in order.
+  // summed in the scorer's slice order (below); the max over (row, h) is
+  // folded in order.
   const int nrh = nrows * P.H_kv;
   const int triples = n * nrh;
   constexpr int esz = DT == HALO_F32 ? 4 : 2;
@@ -179,28 +180,40 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
       const int64_t mb = (int64_t)(b0 + r) * P.msb + (int64_t)h * P.msh + (int64_t)s_chunk[i] * P.msp;
       const char* row = reinterpret_cast<const char*>(P.km) + mb * esz;
       const float* qg = s_qg + (r * P.H_kv + h) * P.D;
-      float acc = 0.f;
-#pragma unroll 16
-      for (int c = 0; c < P.D / ep; ++c) {
-        const uint4 v = *reinterpret_cast<const uint4*>(row + c * 16);
-        float f[8];
-        if constexpr (DT == HALO_F32) {
-          f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
-          f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
-        } else if constexpr (DT == HALO_BF16) {
-          f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-          f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
-        } else {
-          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      // D is cut into G = D/16 slices; slice c holds elements
+      // ep*(c + p*G) + e (p < 16/ep, e < ep), summed in (p, e) order; the G
+      // slice sums are added as a balanced pairwise tree in slice order.  This
+      // is the order of the fused selection in decode_attn.hip, whose slices
+      // sit in G lanes and meet in an xor butterfly.
+      const int G = P.D / 16;
+      float part[16];
+      for (int c = 0; c < G; ++c) {
+        float a = 0.f;
+        for (int p = 0; p < 16 / ep; ++p) {
+          const uint4 v = *reinterpret_cast<const uint4*>(row + (c + p * G) * 16);
+          float f[8];
+          if constexpr (DT == HALO_F32) {
+            f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+            f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+          } else if constexpr (DT == HALO_BF16) {
+            f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+            f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+          } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            f[2 * e] = f16_bits_to_f32((uint16_t)(w[e] & 0xffffu));
-            f[2 * e + 1] = f16_bits_to_f32((uint16_t)(w[e] >> 16));
+            for (int e = 0; e < 4; ++e) {
+              f[2 * e] = f16_bits_to_f32((uint16_t)(w[e] & 0xffffu));
+              f[2 * e + 1] = f16_bits_to_f32((uint16_t)(w[e] >> 16));
+            }
           }
-        }
 #pragma unroll
-        for (int e = 0; e < ep; ++e) acc = __fadd_rn(acc, __fmul_rn(qg[c * ep + e], f[e]));
+          for (int e = 0; e < ep; ++e) a = __fadd_rn(a, __fmul_rn(qg[ep * (c + p * G) + e], f[e]));
+        }
+        part[c] = a;
       }
+      for (int w = 1; w < G; w <<= 1)
+        for (int c = 0; c + w < G; c += 2 * w) part[c] = __fadd_rn(part[c], part[c + w]);
+      const float acc = part[0];
       s_dot[t] = acc;
     }
     __syncthreads();
@@ -344,7 +357,7 @@ extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t 
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0 && D > 0, "bad head sizes");
   HALO_CHECK_ARG(n_elig >= 0 && n_elig <= kMaxElig, "n_elig must be in [0, 1024]");
-  HALO_CHECK_ARG(D % (dtype == HALO_F32 ? 4 : 8) == 0, "head dim must fill whole 16-byte pieces");
+  HALO_CHECK_ARG(D % 16 == 0 && D <= 256, "head dim must be a multiple of 16, at most 256");
   HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(kmean) % 16 == 0 &&
                  (km_stride_p * (dtype == HALO_F32 ? 4 : 2)) % 16 == 0 &&
                  (km_stride_h * (dtype == HALO_F32 ? 4 : 2)) % 16 == 0 &&

@@ -48,7 +48,7 @@ class TieredDecodeLayer:
         self.hot, self.cold = list(hot), list(cold)
         n_cold = len(cold)
         self.fused = bool(fused) and n_cold <= _SEL_MAX_COLD and n_cold * B * H_kv <= _SEL_MAX_TRIPLES \
-            and B * H_kv * D <= _SEL_MAX_QBAR
+            and B * H_kv * D <= _SEL_MAX_QBAR and D % 16 == 0
         # Selection slots come first in the table (their workgroups are
         # dispatched first, which hides the selection work behind the hot
         # chunks).  Each slot is planned over the largest cold chunk, so its
@@ -145,9 +145,10 @@ class RaggedTieredDecodeLayer:
         B = len(rows)
         n_cold = [len(cold) for _, cold in rows]
         max_cold = max(n_cold)
-        if max_cold > _SEL_MAX_COLD or max_cold * H_kv > _SEL_MAX_TRIPLES or H_kv * D > _SEL_MAX_QBAR:
-            raise AssertionError(f"per-row selection over {max_cold} cold chunks x {H_kv} KV heads exceeds the "
-                                 f"in-kernel limits ({_SEL_MAX_COLD} chunks, {_SEL_MAX_TRIPLES} rows)")
+        if max_cold > _SEL_MAX_COLD or max_cold * H_kv > _SEL_MAX_TRIPLES or H_kv * D > _SEL_MAX_QBAR or D % 16:
+            raise AssertionError(f"per-row selection over {max_cold} cold chunks x {H_kv} KV heads (D={D}) exceeds "
+                                 f"the in-kernel limits ({_SEL_MAX_COLD} chunks, {_SEL_MAX_TRIPLES} rows, "
+                                 f"H_kv * D <= {_SEL_MAX_QBAR}, D % 16 == 0)")
         if top_k < 1:
             raise AssertionError("top_k must be >= 1")
         for b, (hot, cold) in enumerate(rows):

@@ -128,9 +128,11 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
  * descending, then index ascending); a slot past the number of eligible
  * chunks attends nothing.  idx_out[s*top_k + j] / score_out[s*n_cold + p]
  * receive the selection when non-NULL.  Limits: n_cold <= 64,
- * n_cold * rows * H_kv <= 512 and rows * H_kv * D <= 2048 per selection
- * (rows = 1 when per_row).  The work items of a slot must cover as many rows
- * as the largest catalog chunk (rows past a chunk's T_c are skipped).
+ * n_cold * rows * H_kv <= 512, rows * H_kv * D <= 2048 per selection and
+ * head_dim % 16 == 0 (rows = 1 when per_row).  The dot products use the
+ * scorer's fixed summation order (halo_chunk_score_topk).  The work
+ * items of a slot must cover as many rows as the largest catalog chunk (rows
+ * past a chunk's T_c are skipped).
  */
 typedef struct halo_select_cfg {
   const void* kmean; /* (B|1, H_kv, n_cold, D) page means, K dtype, rows 16-byte aligned */

@@ -66,6 +66,48 @@ def mean_key_scores(query: np.ndarray, k_mean: np.ndarray, dtype: str = "float32
     return attn.max(axis=(0, 1, 2)).astype(np.float32)
 
 
+def ordered_dot(q_g: np.ndarray, k_mean: np.ndarray, dtype: str = "float32") -> np.ndarray:
+    """sum_d q_g[..., d] * k_mean[..., p, d] in the build's fixed fp32 order:
+    q_g (..., D), k_mean (..., P, D) -> (..., P) float32.
+
+    The reference sums in torch's (unspecified) order
+    (baselines/scorer_ablations.py:233-236); the build fixes one: D is cut
+    into G = D/16 slices, slice c holding elements EP*(c + p*G) + e (EP =
+    elements per 16 bytes: 4 for fp32, 8 for 16-bit keys; p < 16/EP,
+    e < EP), each slice summed in (p, e) order with products and sums
+    rounded to fp32 separately, then the G slice sums added as a balanced
+    pairwise tree in slice order."""
+    D = q_g.shape[-1]
+    if D % 16:
+        raise ValueError(f"head dim {D} must be a multiple of 16")
+    EP = 4 if dtype == "float32" else 8
+    G, PPS = D // 16, 16 // EP
+    prod = (q_g.astype(np.float32)[..., None, :] * k_mean.astype(np.float32)).astype(np.float32)
+    sl = prod.reshape(prod.shape[:-1] + (PPS, G, EP))
+    sl = np.swapaxes(sl, -3, -2).reshape(prod.shape[:-1] + (G, 16))  # (..., P, G, 16) in (p, e) order
+    part = np.zeros(sl.shape[:-1], np.float32)
+    for j in range(16):
+        part = (part + sl[..., j]).astype(np.float32)
+    w = 1
+    while w < G:
+        for c in range(0, G - w, 2 * w):
+            part[..., c] = (part[..., c] + part[..., c + w]).astype(np.float32)
+        w *= 2
+    return part[..., 0]
+
+
+def ordered_scores(query: np.ndarray, k_mean: np.ndarray, dtype: str = "float32") -> np.ndarray:
+    """Chunk scores as the kernels compute them: the GQA-mean query
+    (rounded to the query dtype), ``ordered_dot`` with every page mean, max
+    over (b, h_kv, t_q) ignoring NaN; a score that is NaN everywhere is -inf.
+    Returns (P,) float32."""
+    H_kv = k_mean.shape[1]
+    q_g = gqa_mean_query(query, H_kv, dtype)  # (B, H_kv, T_q, D)
+    dots = ordered_dot(q_g, k_mean[:, :, None], dtype)  # (B, H_kv, T_q, P)
+    dots = np.where(np.isnan(dots), -np.inf, dots)
+    return dots.max(axis=(0, 1, 2)).astype(np.float32)
+
+
 def select_chunks(query: np.ndarray, k_mean: np.ndarray, eligible: np.ndarray, k: int,
                   dtype: str = "float32") -> np.ndarray:
     """The build's chunk selector: the alpha-only mean-key scorer

@@ -190,6 +190,64 @@ def test_select_chunks_brute_force():
         assert got.tolist() == brute
 
 
+def test_ordered_dot_slice_order():
+    """The scorer's fixed order: slices of 16 elements (element d of a
+    fp32 row belongs to slice (d // 4) % G, and within it comes at
+    position (d // (4 G), d % 4)), each summed in order, then a pairwise
+    tree over slices.  Values of 2^24 make every other order give a
+    different exact answer."""
+    big = np.float32(2.0 ** 24)
+    D = 64  # fp32: G = 4 slices
+    q = np.ones(D, np.float32)
+
+    def dot(pairs):
+        k = np.zeros((1, D), np.float32)
+        for d, v in pairs:
+            k[0, d] = v
+        return float(S.ordered_dot(q, k, "float32")[0])
+
+    # slices 0..3 hold 2^24, 1, 1, -2^24 (elements 0, 4, 8, 12): the tree
+    # adds (2^24 + 1) + (1 - 2^24) = 2^24 + (-(2^24 - 1)) = 1; a sequential
+    # sum over d would give ((2^24 + 1) + 1) - 2^24 = 0.
+    assert dot([(0, big), (4, 1.0), (8, 1.0), (12, -big)]) == 1.0
+    # the same four values inside slice 0 (elements 0, 16, 32, 48 = p 0..3)
+    # are summed in order: ((2^24 + 1) + 1) - 2^24 = 0.
+    assert dot([(0, big), (16, 1.0), (32, 1.0), (48, -big)]) == 0.0
+    # element order inside a piece: 2^24 + 1 + 1 at e = 0, 1, 2 of slice 1
+    # rounds twice (2^24); 1 + 1 + 2^24 at e = 0, 1, 2 is exact (2^24 + 2).
+    assert dot([(4, big), (5, 1.0), (6, 1.0)]) == float(big)
+    assert dot([(4, 1.0), (5, 1.0), (6, big)]) == float(big) + 2.0
+    # 16-bit keys: 8 elements per piece, so D = 128 has G = 8 slices;
+    # elements 8 and 64 are slice 1 (p 0) and slice 0 (p 1).
+    q2 = np.ones(128, np.float32)
+    k2 = np.zeros((1, 128), np.float32)
+    k2[0, 0], k2[0, 64], k2[0, 8], k2[0, 72] = big, 1.0, 1.0, -big
+    # slice 0: 2^24 + 1 -> 2^24; slice 1: 1 - 2^24 -> -(2^24 - 1); tree: 1
+    assert float(S.ordered_dot(q2, k2, "bfloat16")[0]) == 1.0
+
+
+def test_ordered_scores_match_float64_within_rounding():
+    rng = np.random.default_rng(3)
+    for D, dtype in ((64, "float32"), (128, "bfloat16"), (256, "float16")):
+        q = rng.standard_normal((1, 8, 1, D)).astype(np.float32)
+        km = rng.standard_normal((1, 2, 20, D)).astype(np.float32)
+        if dtype == "bfloat16":
+            q, km = round_bf16(q), round_bf16(km)
+        elif dtype == "float16":
+            q, km = q.astype(np.float16).astype(np.float32), km.astype(np.float16).astype(np.float32)
+        got = S.ordered_scores(q, km, dtype).astype(np.float64)
+        ref = S.mean_key_scores(q, km, dtype).astype(np.float64)
+        qg = S.gqa_mean_query(q, 2, dtype).astype(np.float64)
+        mag = np.einsum("bhtd,bhpd->bhtp", np.abs(qg), np.abs(km.astype(np.float64))).max(axis=(0, 1, 2))
+        bound = (16 + int(np.log2(D // 16)) + 2) * 2.0 ** -24 * mag
+        assert (np.abs(got - ref) <= bound).all()
+        # and the ranking agrees with the float64 one wherever the margin is clear
+        elig = np.arange(20)
+        srt = np.sort(ref)[::-1]
+        if srt[4] - srt[5] > 1e-3:
+            assert S.topk_indices(got, 5).tolist() == S.select_chunks(q, km, elig, 5, dtype).tolist()
+
+
 def test_page_means_and_gqa_query_mean():
     rng = np.random.default_rng(2)
     K = rng.standard_normal((1, 2, 70, 8)).astype(np.float32)

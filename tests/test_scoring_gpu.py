@@ -53,6 +53,8 @@ def test_scores_and_topk_match_oracle(dev, H, H_kv, dtype):
         idx, sc = score_topk(_gpu(q, dtype, dev), _gpu(km, dtype, dev), torch.from_numpy(elig).to(dev), 6)
         ref_sc = S.mean_key_scores(q, km, dtype)[elig]
         np.testing.assert_allclose(sc[0, :30].cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-5)
+        # the kernel's fixed summation order, bit for bit
+        np.testing.assert_array_equal(sc[0, :30].cpu().numpy(), S.ordered_scores(q, km, dtype)[elig])
         ref_sel = S.select_chunks(q, km, elig, 6, dtype)
         srt = np.sort(ref_sc.astype(np.float64))[::-1]
         if srt[5] - srt[6] > 1e-4:  # margin-checked
@@ -189,6 +191,8 @@ def test_fused_selection_per_row_ragged(dev, dtype):
     for b in range(B):
         ref_sc = S.mean_key_scores(x.q[b:b + 1], km_np[b:b + 1], dtype)[: n_el[b]]
         np.testing.assert_allclose(sc[b, : n_el[b]].cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-5)
+        np.testing.assert_array_equal(sc[b, : n_el[b]].cpu().numpy(),
+                                      S.ordered_scores(x.q[b:b + 1], km_np[b:b + 1], dtype)[: n_el[b]])
         assert (sc[b, n_el[b]:].cpu().numpy() == -7.0).all()
         srt = np.sort(ref_sc.astype(np.float64))[::-1]
         assert len(srt) <= top_k or srt[top_k - 1] - srt[top_k] > 1e-4, "fixture seed lost its margin"
@@ -271,6 +275,8 @@ def test_ragged_batched_decode(dev, dtype):
     for b, (k, v, n, n_hot) in enumerate(host):
         n_cold = n - n_hot
         ref_sc = S.mean_key_scores(q[b:b + 1, :, None], km[b:b + 1, :, :n_cold], dtype)
+        np.testing.assert_array_equal(layer.scores[b, :n_cold].cpu().numpy(),
+                                      S.ordered_scores(q[b:b + 1, :, None], km[b:b + 1, :, :n_cold], dtype))
         srt = np.sort(ref_sc.astype(np.float64))[::-1]
         assert len(srt) <= top_k or srt[top_k - 1] - srt[top_k] > 1e-4, "fixture seed lost its margin"
         want = S.select_chunks(q[b:b + 1, :, None], km[b:b + 1, :, :n_cold], np.arange(n_cold), top_k, dtype).tolist()

@@ -176,9 +176,18 @@ constexpr int kCachePolicyNT = 2;
 __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kCachePolicyNT));
 }
+// Buffer descriptor over [base, base + bytes).  base and bytes are
+// wave-uniform at every call site; reading them through readfirstlane puts
+// the descriptor in scalar registers, so each load is one instruction (a
+// descriptor the compiler cannot prove uniform turns every load into a
+// readfirstlane loop and its waits into vmcnt(0)).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int64_t bytes) {
   const int nrec = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, nrec, 0x00020000);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  char* ub = reinterpret_cast<char*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, __builtin_amdgcn_readfirstlane(nrec), 0x00020000);
 }
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
@@ -1043,6 +1052,12 @@ decode_attn_kernel(DecodeParams P) {
   } else {
     dsc = P.descs[item.x];
   }
+  // With in-kernel selection, the hot items hold back their K/V flood for
+  // ~1k cycles once their descriptor is in: the selection's page-mean loads,
+  // issued first by the slot items, then reach memory ahead of it instead of
+  // queueing behind tens of MiB of K/V (the selection sits on the critical
+  // path of the launch).
+  if (P.sel_on && !(item.x >= P.sel.slot0 && item.x < P.sel.slot0 + P.sel.top_k)) __builtin_amdgcn_s_sleep(16);
   const int hq0 = h_kv * P.rep + sub * REP;
   const int nvalid_h = min(REP, P.rep - sub * REP);
 

@@ -222,14 +222,15 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
   __syncthreads();
   int stage = 0;
   while (have) {
-    // the next tile: its loads are in flight while this one is consumed
+    // the next tile: its loads are issued after this tile's score MFMAs (a
+    // wait for them placed before the first MFMA would stall the wave) and
+    // are in flight during the softmax and P.V
     Tile nxt = cur;
     int ni = ci;
     bool have_nxt = true;
     nxt.kt += kPfBK;
     if (nxt.kt >= nxt.rows) have_nxt = open_chunk(ci + 1, ni, nxt);
     uint4 kr[KPT], vr[KPT];
-    if (have_nxt) load_tile(nxt, kr, vr);
 
     const char* sk = s_buf + stage * STAGE;
     const char* sv = sk + KTB;
@@ -246,6 +247,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
         st[kb][1] = PMfma<DT>::run(a, qb[1][s], st[kb][1]);
       }
     }
+    if (have_nxt) load_tile(nxt, kr, vr);
     // masking only where the tile crosses the chunk end or the causal diagonal
     const bool masked = cur.kt + kPfBK > cur.rows || (cur.causal && cur.cstart + cur.kt + kPfBK - 1 > wave_qmin);
     uint4 pb[2][2];

@@ -10,10 +10,11 @@
 //
 // Tiling: one workgroup = 4 waves = 128 query rows of one query head; each
 // wave owns 32 rows as two 16-row MFMA column blocks.  Key tiles of 64 rows
-// are staged in LDS by the whole workgroup, double-buffered (the next tile's
-// loads are in flight while the current one is consumed): K row-major (read
-// as MFMA A operands), V row-major with swizzled pieces, read with
-// transposed LDS reads as the A operands of O^T = V^T P^T.
+// are loaded straight into LDS (LDS-DMA) by the whole workgroup,
+// double-buffered (the next tile's loads are in flight while the current one
+// is consumed): K row-major with XOR-swizzled pieces (read as MFMA A
+// operands), V row-major with swizzled pieces, read with transposed LDS reads
+// as the A operands of O^T = V^T P^T.
 //   scores  S^T[key][q] = sum_d K[key][d] Q[q][d]    v_mfma_f32_16x16x32
 //   output  O^T[d][q]  += sum_key V^T[d][key] P^T[key][q]
 // The P^T operand is built in registers from the S^T accumulators with a
@@ -62,9 +63,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t prsrc(const char* base, int64_
   const int nrec = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, nrec, 0x00020000);
 }
-__device__ __forceinline__ uint4 pld16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 }  // namespace
 
@@ -94,6 +92,12 @@ template <int SL>
 __device__ __forceinline__ int pf_vswz(int r) {
   return (2 * (r & 3) + 8 * ((r >> 3) & 1)) & (SL - 1);
 }
+// K tile in LDS: row r holds its 16-byte pieces at positions piece ^ (r % SL),
+// so the 16 rows one MFMA operand read touches land on distinct bank ranges.
+template <int SL>
+__device__ __forceinline__ int pf_kswz(int r) {
+  return r & (SL - 1);
+}
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
 // of the 8-byte reads of lanes 4e + i/4 (e = 0..3).
 typedef short pv4i16_t __attribute__((ext_vector_type(4)));
@@ -114,9 +118,9 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
   constexpr int DB = D / 16;              // d-blocks of the output MFMA
   constexpr int SL = D / 8;               // 16-byte pieces per row
   constexpr int RB = D * 2;               // row bytes
-  constexpr int KROWB = RB + 16;          // padded K row in LDS (bytes)
-  constexpr int KTB = kPfBK * KROWB;      // K tile bytes in LDS
+  constexpr int KTB = kPfBK * RB;         // K tile bytes in LDS
   constexpr int STAGE = KTB + kPfBK * RB; // K tile + V tile
+  constexpr int RPI = 1024 / RB;          // rows per 1 KiB LDS-DMA instruction
   constexpr int KPT = kPfBK * SL / 256;   // K (and V) pieces per thread per tile
   static_assert(KPT >= 1 && kPfBK * SL % 256 == 0, "prefill tile shape");
   __shared__ __attribute__((aligned(16))) char s_buf[2 * STAGE];
@@ -191,34 +195,35 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
     ci = P.n_desc;
     return false;
   };
-  auto load_tile = [&](const Tile& t, uint4 (&kr)[KPT], uint4 (&vr)[KPT]) {
+  // Tile loads go straight from memory into LDS stage `st` (LDS-DMA: each
+  // 1 KiB instruction of a wave fills RPI consecutive rows, lane l the
+  // 16-byte position l % SL of row l / SL; the lane picks which global piece
+  // lands there, which lays out the swizzles).  Rows past the chunk read as
+  // zeros (buffer range check).  No registers hold the tile, so the loads of
+  // the next tile can be in flight during the whole current one.
+  auto issue_tile = [&](const Tile& t, char* st) {
     const __amdgpu_buffer_rsrc_t rk = prsrc(t.kb + (int64_t)t.kt * t.kst, (int64_t)(t.rows - t.kt) * t.kst);
     const __amdgpu_buffer_rsrc_t rv = prsrc(t.vb + (int64_t)t.kt * t.vst, (int64_t)(t.rows - t.kt) * t.vst);
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int id = tid + 256 * j;
-      kr[j] = pld16(rk, (int)((id / SL) * t.kst) + (id % SL) * 16);
-      vr[j] = pld16(rv, (int)((id / SL) * t.vst) + (id % SL) * 16);
-    }
-  };
-  auto store_tile = [&](char* st, const uint4 (&kr)[KPT], const uint4 (&vr)[KPT]) {
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int id = tid + 256 * j;
-      const int r = id / SL, pc = id % SL;
-      *reinterpret_cast<uint4*>(st + r * KROWB + pc * 16) = kr[j];
-      *reinterpret_cast<uint4*>(st + KTB + r * RB + ((pc ^ pf_vswz<SL>(r)) << 4)) = vr[j];
+      const int blk = wave * KPT + j;            // 1 KiB block of the tile
+      const int r = blk * RPI + lane / SL, pos = lane % SL;
+      // offsets computed before the calls: a __device__ helper call inside
+      // the builtin's arguments makes the host pass drop the kernel's stub
+      const int koff = (int)(r * t.kst) + ((pos ^ pf_kswz<SL>(r)) << 4);
+      const int voff = (int)(r * t.vst) + ((pos ^ pf_vswz<SL>(r)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(st + blk * 1024), 16,
+                                               koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(st + KTB + blk * 1024),
+                                               16, voff, 0, 0, 0);
     }
   };
 
   int ci;
   Tile cur;
   bool have = open_chunk(0, ci, cur);
-  if (have) {
-    uint4 kr[KPT], vr[KPT];
-    load_tile(cur, kr, vr);
-    store_tile(s_buf, kr, vr);
-  }
+  if (have) issue_tile(cur, s_buf);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's tile loads have landed in LDS
   __syncthreads();
   int stage = 0;
   while (have) {
@@ -230,8 +235,6 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
     bool have_nxt = true;
     nxt.kt += kPfBK;
     if (nxt.kt >= nxt.rows) have_nxt = open_chunk(ci + 1, ni, nxt);
-    uint4 kr[KPT], vr[KPT];
-
     const char* sk = s_buf + stage * STAGE;
     const char* sv = sk + KTB;
     // scores S^T for 4 key blocks x 2 query column blocks
@@ -242,12 +245,13 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
       st[kb][1] = pf32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const uint4 a = *reinterpret_cast<const uint4*>(sk + (kb * 16 + ql) * KROWB + (s * 32 + g * 8) * 2);
+        const int kr = kb * 16 + ql;
+        const uint4 a = *reinterpret_cast<const uint4*>(sk + kr * RB + (((s * 4 + g) ^ pf_kswz<SL>(kr)) << 4));
         st[kb][0] = PMfma<DT>::run(a, qb[0][s], st[kb][0]);
         st[kb][1] = PMfma<DT>::run(a, qb[1][s], st[kb][1]);
       }
     }
-    if (have_nxt) load_tile(nxt, kr, vr);
+    if (have_nxt) issue_tile(nxt, s_buf + (stage ^ 1) * STAGE);
     // masking only where the tile crosses the chunk end or the causal diagonal
     const bool masked = cur.kt + kPfBK > cur.rows || (cur.causal && cur.cstart + cur.kt + kPfBK - 1 > wave_qmin);
     uint4 pb[2][2];
@@ -315,7 +319,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
         o[0][db] = PMfma<DT>::run(a, pb[0][t], o[0][db]);
         o[1][db] = PMfma<DT>::run(a, pb[1][t], o[1][db]);
       }
-    if (have_nxt) store_tile(s_buf + (stage ^ 1) * STAGE, kr, vr);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
     __syncthreads();  // the next tile is in LDS; this one is free for the tile after
     stage ^= 1;
     cur = nxt;

@@ -30,7 +30,8 @@ namespace halo {
 constexpr int kWorkInts = 8;  // work record: desc, group, t0, t1, partial slot, 3 x pad
 
 struct MergeParams {
-  const int32_t* group_offsets;
+  const int32_t* group_offsets;  // NULL: group g owns slots [g * per_group, (g + 1) * per_group)
+  int per_group;
   int H, H_kv, rep, n_sub;
   float* m;
   float* l;
@@ -285,17 +286,37 @@ struct Selector {
   static constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
   static constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
   static constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
-  static constexpr int QB = 8;                                        // query heads summed per load batch
+  static constexpr int QB = EP == 8 ? 8 : 4;                          // query heads summed per load batch (LDS path)
   static constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
-  // triples whose page-mean rows are loaded up front (the rest are loaded
-  // where they are used: a second triple per thread only exists past 256
-  // triples, and rows of 512 bytes stay out of registers until then)
-  static constexpr int TE = PIECES < 16 ? kSelTPT : (PIECES == 16 ? 1 : 0);
-  uint4 kb[TE > 0 ? TE : 1][PIECES];  // page-mean rows of this thread's first TE triples
-  int my_r[kSelTPT], my_h[kSelTPT];
+  // Dot products are cut into units: unit u = (triple t = u / G, slice
+  // s = u % G), the 16 elements of pieces s, s + G, ... of one page-mean
+  // row.  The G lanes of a triple sit side by side in one wave, so a load
+  // instruction reads whole 128-byte runs of rows and the pairwise tree over
+  // slices is a butterfly inside the lane group.
+  static constexpr int PPS = 16 / EP;                                 // pieces per slice
+  static constexpr int KU = EP == 8 ? 6 : 3;                          // units per thread loaded up front
+  static_assert((G & (G - 1)) == 0 && G <= kWave, "slices per row");
+  uint4 kb[KU][PPS];          // page-mean pieces of this thread's first KU units
   uint2 cw[CW];               // this thread's share of the candidate descriptors
-  uint4 qv[QP][QB];           // first QB query heads of this thread's q-bar pieces (aligned q)
+  // q pieces loaded up front, 8 x 16 bytes: per lane (qlane) the PPS pieces
+  // of its own slice for the first QL query heads (qv[j * QL + h]), else the
+  // first QB heads of the thread's share of the LDS-staged q-bar pieces
+  // (qv[k * QB + j]); later heads are read where they are summed
+  static constexpr int QL = 8 / PPS;
+  static_assert(QP * QB == 8, "q pieces loaded up front");
+  uint4 qv[8];
   int n, kk, rows, b0, sel, nrh, triples;
+  // Every unit of a lane has the same (row, KV head, slice) when the lane
+  // groups of one unit batch (NT / G triples) cover whole multiples of nrh:
+  // the lane then forms its q-bar slice in registers (no LDS stage).
+  bool qlane;
+
+  __device__ __forceinline__ const char* km_row(const halo_select_cfg& S, int t, int H_kv) const {
+    const int i = t / nrh, rh = t % nrh;
+    return reinterpret_cast<const char*>(S.kmean) +
+           ((int64_t)(b0 + rh / H_kv) * S.km_stride_b + (int64_t)(rh % H_kv) * S.km_stride_h +
+            (int64_t)i * S.km_stride_p) * E::size;
+  }
 
   // Issue every global load of the selection (no waits): page-mean rows,
   // candidate descriptors, the first batch of query pieces.
@@ -310,22 +331,12 @@ struct Selector {
     nrh = rows * P.H_kv;
     triples = n * nrh;
 #pragma unroll
-    for (int u = 0; u < kSelTPT; ++u) {
-      const int t = tid + u * NT;
-      my_r[u] = 0;
-      my_h[u] = 0;
-      if (t < triples) {
-        const int i = t / nrh, rh = t % nrh;
-        my_r[u] = rh / P.H_kv;
-        my_h[u] = rh % P.H_kv;
-        if (u < TE) {
-          const char* row = reinterpret_cast<const char*>(S.kmean) +
-                            ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
-                             (int64_t)i * S.km_stride_p) * E::size;
+    for (int k = 0; k < KU; ++k) {
+      const int u = tid + k * NT;
+      const int t = min(u / G, triples - 1), sl = u % G;  // past the units: a valid row, loads unused
+      const char* row = km_row(S, t, P.H_kv);
 #pragma unroll
-          for (int c = 0; c < PIECES; ++c) kb[u < TE ? u : 0][c] = *reinterpret_cast<const uint4*>(row + c * 16);
-        }
-      }
+      for (int j = 0; j < PPS; ++j) kb[k][j] = *reinterpret_cast<const uint4*>(row + (sl + j * G) * 16);
     }
     const uint2* cat = reinterpret_cast<const uint2*>(S.catalog + (int64_t)sel * S.catalog_stride);
 #pragma unroll
@@ -333,7 +344,19 @@ struct Selector {
       const int w = tid + k * NT;
       if (w < n * DW2) cw[k] = cat[w];
     }
-    if (P.q_aligned) {
+    qlane = P.q_aligned && (NT / G) % nrh == 0;
+    if (qlane) {
+      const int rh = (tid / G) % nrh, sl = tid % G;
+      const char* qrow = reinterpret_cast<const char*>(P.q) +
+                         ((int64_t)(b0 + rh / P.H_kv) * P.q_stride_b + (int64_t)(rh % P.H_kv) * P.rep * P.q_stride_h) *
+                             E::size;
+#pragma unroll
+      for (int j = 0; j < PPS; ++j)
+#pragma unroll
+        for (int e = 0; e < QL; ++e)
+          if (e < P.rep) qv[j * QL + e] = *reinterpret_cast<const uint4*>(qrow + (int64_t)e * P.q_stride_h * E::size +
+                                                                          (sl + j * G) * 16);
+    } else if (P.q_aligned) {
       const int npieces = rows * P.H_kv * PIECES;
 #pragma unroll
       for (int k = 0; k < QP; ++k) {
@@ -344,7 +367,7 @@ struct Selector {
                              ((int64_t)(b0 + r) * P.q_stride_b + (int64_t)h * P.rep * P.q_stride_h) * E::size + c * 16;
 #pragma unroll
           for (int j = 0; j < QB; ++j)
-            if (j < P.rep) qv[k][j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)j * P.q_stride_h * E::size);
+            if (j < P.rep) qv[k * QB + j] = *reinterpret_cast<const uint4*>(qrow + (int64_t)j * P.q_stride_h * E::size);
         }
       }
     }
@@ -363,11 +386,50 @@ struct Selector {
     const int H_kv = P.H_kv, rep = P.rep;
     float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
     float* s_dot = s_qbar + kSelQbarLds;
+    float* s_sc = s_dot + kSelTPT * 256;  // per-candidate scores for the ranking (64, -inf past n)
     int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
     halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
     // GQA-mean query rows: fp32 sum over the rep heads in head order, times
     // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
-    if (P.q_aligned) {
+    auto qround = [&](float v) __attribute__((always_inline)) {
+      if (rep != 1) {
+        v = opaque(v * P.inv_rep);
+        v = DT == HALO_F32 ? v
+            : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
+                               : f16_bits_to_f32(f32_to_f16_rne(v)));
+      }
+      return v;
+    };
+    float qs[PPS * EP];  // qlane: this lane's q-bar slice (pieces sl, sl + G, ..)
+    if (qlane) {
+      const int rh = (tid / G) % nrh, sl = tid % G;
+      const char* qrow = reinterpret_cast<const char*>(P.q) +
+                         ((int64_t)(b0 + rh / H_kv) * P.q_stride_b + (int64_t)(rh % H_kv) * rep * P.q_stride_h) *
+                             E::size;
+#pragma unroll
+      for (int j = 0; j < PPS; ++j) {
+        float acc[EP];
+#pragma unroll
+        for (int e = 0; e < EP; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int h = 0; h < QL; ++h) {
+          if (h < rep) {
+            float f[EP];
+            E::unpack(qv[j * QL + h], f);
+#pragma unroll
+            for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
+          }
+        }
+        for (int h = QL; h < rep; ++h) {
+          float f[EP];
+          E::unpack(*reinterpret_cast<const uint4*>(qrow + (int64_t)h * P.q_stride_h * E::size + (sl + j * G) * 16), f);
+#pragma unroll
+          for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
+        }
+#pragma unroll
+        for (int e = 0; e < EP; ++e) qs[j * EP + e] = qround(acc[e]);
+      }
+    } else if (P.q_aligned) {
       const int npieces = rows * H_kv * PIECES;
 #pragma unroll
       for (int k = 0; k < QP; ++k) {
@@ -383,7 +445,7 @@ struct Selector {
         for (int j = 0; j < QB; ++j) {
           if (j < rep) {
             float f[EP];
-            E::unpack(qv[k][j], f);
+            E::unpack(qv[k * QB + j], f);
 #pragma unroll
             for (int e = 0; e < EP; ++e) acc[e] = acc[e] + f[e];
           }
@@ -405,16 +467,7 @@ struct Selector {
         }
         float* dst = s_qbar + (r * H_kv + h) * QS + c * EP;
 #pragma unroll
-        for (int e = 0; e < EP; ++e) {
-          float v = acc[e];
-          if (rep != 1) {
-            v = opaque(v * P.inv_rep);
-            v = DT == HALO_F32 ? v
-                : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
-                                   : f16_bits_to_f32(f32_to_f16_rne(v)));
-          }
-          dst[e] = v;
-        }
+        for (int e = 0; e < EP; ++e) dst[e] = qround(acc[e]);
       }
     } else {
       for (int e = tid; e < rows * H_kv * D; e += NT) {
@@ -422,14 +475,7 @@ struct Selector {
         const int64_t qb = (int64_t)(b0 + r) * P.q_stride_b;
         float acc = 0.f;
         for (int j = 0; j < rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * rep + j) * P.q_stride_h + d, DT);
-        float v = acc;
-        if (rep != 1) {
-          v = opaque(v * P.inv_rep);
-          v = DT == HALO_F32 ? v
-              : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16)
-                                 : f16_bits_to_f32(f32_to_f16_rne(v)));
-        }
-        s_qbar[(e / D) * QS + d] = v;
+        s_qbar[(e / D) * QS + d] = qround(acc);
       }
     }
 #pragma unroll
@@ -437,57 +483,123 @@ struct Selector {
       const int w = tid + k * NT;
       if (w < n * DW2) reinterpret_cast<uint2*>(s_cat)[w] = cw[k];
     }
-    __syncthreads();
+    // the q-bar stage (not used by qlane) is read across waves; the catalog is
+    // read after the ranking's barrier
+    if (!qlane) __syncthreads();
 
+    // Unit dot products: slice sl of triple t sums its pieces in order, each
+    // product and sum rounded on its own; then the pairwise tree over the G
+    // slices (part[sl] += part[sl + w], w = 1, 2, .., G/2) as a DPP
+    // butterfly in the triple's lane group: after each step every lane of a
+    // block holds the same sum (a + b == b + a), so the mirrors read it and
+    // the association is the scorer's; lane sl == 0 holds the triple's score.
+    // No LDS traffic beyond the one score per triple.
+    const int n_units = triples * G;
+    auto unit = [&](int u, const uint4 (&pc)[PPS]) __attribute__((always_inline)) {
+      const int t = u / G, sl = u % G;
+      float qf[PPS * EP];
+      if (qlane) {
 #pragma unroll
-    for (int u = 0; u < kSelTPT; ++u) {
-      const int t = tid + u * NT;
-      if (t < triples) {
-        const float* qg = s_qbar + (my_r[u] * H_kv + my_h[u]) * QS;
-        const char* row = reinterpret_cast<const char*>(S.kmean) +
-                          ((int64_t)(b0 + my_r[u]) * S.km_stride_b + (int64_t)my_h[u] * S.km_stride_h +
-                           (int64_t)(t / nrh) * S.km_stride_p) * E::size;
-        // the scorer's fixed order: piece c belongs to slice c % G (G = D/16)
-        // and comes at position c / G of it; G independent slice sums, then
-        // the pairwise tree over slices
-        float part[G];
+        for (int x = 0; x < PPS * EP; ++x) qf[x] = qs[x];
+      } else {
+        const float* qg = s_qbar + (t % nrh) * QS;
 #pragma unroll
-        for (int sl = 0; sl < G; ++sl) {
-          float a = 0.f;
+        for (int j = 0; j < PPS; ++j) {
+          const float4* qp = reinterpret_cast<const float4*>(qg + (sl + j * G) * EP);
 #pragma unroll
-          for (int c = sl; c < PIECES; c += G) {
-            float f[EP];
-            E::unpack(u < TE ? kb[u < TE ? u : 0][c] : *reinterpret_cast<const uint4*>(row + c * 16), f);
-#pragma unroll
-            for (int e = 0; e < EP; ++e) a = __fadd_rn(a, __fmul_rn(qg[c * EP + e], f[e]));
+          for (int e4 = 0; e4 < EP / 4; ++e4) {
+            const float4 v = qp[e4];
+            qf[j * EP + 4 * e4] = v.x;
+            qf[j * EP + 4 * e4 + 1] = v.y;
+            qf[j * EP + 4 * e4 + 2] = v.z;
+            qf[j * EP + 4 * e4 + 3] = v.w;
           }
-          part[sl] = a;
         }
+      }
+      float a = 0.f;
 #pragma unroll
-        for (int w = 1; w < G; w <<= 1)
+      for (int j = 0; j < PPS; ++j) {
+        float f[EP];
+        E::unpack(pc[j], f);
 #pragma unroll
-          for (int sl = 0; sl + w < G; sl += 2 * w) part[sl] = __fadd_rn(part[sl], part[sl + w]);
-        s_dot[t] = part[0];
+        for (int e = 0; e < EP; ++e) a = __fadd_rn(a, __fmul_rn(qf[j * EP + e], f[e]));
+      }
+      if constexpr (G >= 2) a = __fadd_rn(a, dpp_f<0xB1>(a));   // quad_perm [1,0,3,2]: slices 2m, 2m+1
+      if constexpr (G >= 4) a = __fadd_rn(a, dpp_f<0x4E>(a));   // quad_perm [2,3,0,1]: pairs of a quad
+      if constexpr (G >= 8) a = __fadd_rn(a, dpp_f<0x141>(a));  // row_half_mirror: quads of 8 lanes
+      if constexpr (G >= 16) a = __fadd_rn(a, dpp_f<0x140>(a)); // row_mirror: halves of 16 lanes
+      if (sl == 0) s_dot[t] = a;
+    };
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u0 = k * NT;
+      if (u0 < n_units && tid + u0 < n_units) unit(tid + u0, kb[k]);
+    }
+    for (int u0 = KU * NT; u0 < n_units; u0 += NT) {
+      const int u = tid + u0;
+      if (u < n_units) {
+        uint4 pc[PPS];
+        const char* row = km_row(S, u / G, H_kv);
+#pragma unroll
+        for (int j = 0; j < PPS; ++j) pc[j] = *reinterpret_cast<const uint4*>(row + (u % G + j * G) * 16);
+        unit(u, pc);
       }
     }
     __syncthreads();
     // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
-    // over (row, KV head), NaN -> -inf; rank by (score desc, index asc) with
-    // readlane broadcasts; the chosen chunks are listed in ascending index
-    // order with a ballot prefix count.
+    // over (row, KV head), NaN -> -inf; each lane counts the candidates
+    // ranked before it (score desc, index asc) from broadcast LDS reads of
+    // all 64 scores (lanes past n hold -inf, which never outranks); the
+    // chosen chunks are listed in ascending index order with a ballot
+    // prefix count.
     if (tid < kWave) {
       const int i = tid;
       float sc = -INFINITY;
       if (i < n) {
-        float best = -INFINITY;
-#pragma unroll 8
-        for (int rh = 0; rh < nrh; ++rh) best = fmaxf(best, s_dot[i * nrh + rh]);
+        const float* dr = s_dot + i * nrh;
+        float b4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        int rh = 0;
+        if ((nrh & 3) == 0) {  // rows 16-byte aligned: 4 scores per read, 4 reads in flight
+          for (; rh + 16 <= nrh; rh += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) v[x] = *reinterpret_cast<const float4*>(dr + rh + 4 * x);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+              b4[0] = fmaxf(b4[0], v[x].x);
+              b4[1] = fmaxf(b4[1], v[x].y);
+              b4[2] = fmaxf(b4[2], v[x].z);
+              b4[3] = fmaxf(b4[3], v[x].w);
+            }
+          }
+          for (; rh < nrh; rh += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(dr + rh);
+            b4[0] = fmaxf(b4[0], v.x);
+            b4[1] = fmaxf(b4[1], v.y);
+            b4[2] = fmaxf(b4[2], v.z);
+            b4[3] = fmaxf(b4[3], v.w);
+          }
+        }
+        for (; rh < nrh; ++rh) b4[0] = fmaxf(b4[0], dr[rh]);
+        const float best = fmaxf(fmaxf(b4[0], b4[1]), fmaxf(b4[2], b4[3]));
         sc = (best != best) ? -INFINITY : best;
       }
+      s_sc[i] = sc;
+      wave_lds_fence();
       int rank = 0;
-      for (int j = 0; j < n; ++j) {
-        const float sj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc), j));
-        rank += (sj > sc || (sj == sc && j < i)) ? 1 : 0;
+      for (int j0 = 0; j0 < n; j0 += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) v[x] = *reinterpret_cast<const float4*>(s_sc + j0 + 4 * x);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float sj[4] = {v[x].x, v[x].y, v[x].z, v[x].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = j0 + 4 * x + e;
+            rank += (sj[e] > sc || (sj[e] == sc && j < i)) ? 1 : 0;
+          }
+        }
       }
       const bool chosen = i < n && rank < kk;
       const uint64_t mask = __ballot(chosen);
@@ -1640,7 +1752,9 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
   const int hq0 = h_kv * P.rep + sub * REP;
   if (r >= min(REP, P.rep - sub * REP)) return;  // padding head
   const int hq = hq0 + r;
-  const int gbeg = P.group_offsets[g], gend = P.group_offsets[g + 1];
+  // uniform tables skip the offsets load (one dependent round trip)
+  const int gbeg = P.group_offsets ? P.group_offsets[g] : g * P.per_group;
+  const int gend = P.group_offsets ? P.group_offsets[g + 1] : gbeg + P.per_group;
   const int np = gend - gbeg;
   const bool has_acc = P.m != nullptr;
   const bool merge_in = has_acc && (P.acc_mode & 1);
@@ -1853,7 +1967,9 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
                 const int32_t* group_offsets, int n_groups, const int64_t* q_pos, float scale, float* m, float* l,
                 float* o, int64_t acc_stride_b, int acc_mode, void* out, int out_dtype, float* lse, void* workspace,
                 size_t workspace_bytes, const halo_select_cfg* sel, bool kivi, void* stream) {
-  HALO_CHECK_ARG(q && descs && work && group_offsets, "null pointer argument");
+  HALO_CHECK_ARG(q && descs && work, "null pointer argument");
+  HALO_CHECK_ARG(group_offsets || (n_groups > 0 && n_work % n_groups == 0),
+                 "group_offsets may be NULL only when n_work is a multiple of n_groups");
   HALO_CHECK_ARG(!kivi || dtype == HALO_F16 || dtype == HALO_BF16, "KIVI chunks need fp16 or bf16 q and scales");
   HALO_CHECK_ARG(!(kivi && sel), "in-kernel selection is not available for KIVI chunk tables");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0, "need H % H_kv == 0 and positive sizes");
@@ -1916,6 +2032,7 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
   }
   MergeParams mp;
   mp.group_offsets = group_offsets;
+  mp.per_group = n_groups > 0 ? n_work / n_groups : 0;
   mp.H = H;
   mp.H_kv = H_kv;
   mp.rep = rep;

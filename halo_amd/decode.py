@@ -82,6 +82,7 @@ class DecodePlan:
     n_groups: int
     rows: int                    # attended K/V rows summed over (b, h_kv)
     keep: list = field(default_factory=list)  # tensors the descriptors point at
+    uniform_groups: bool = False  # group g owns slots [g*per, (g+1)*per): the merge needs no offsets
     work_host: Optional[np.ndarray] = None
     kivi: bool = False           # the table holds KIVI block runs (plain chunks may join them)
     kivi_rows: int = 0           # rows of ``rows`` that are KIVI-quantised
@@ -314,12 +315,15 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
         work = [w for w in work if w[0] in early] + [w for w in work if w[0] not in early]
     work_np = np.asarray(work, dtype=np.int32).reshape(-1, WORK_INTS)
     dev_descs = _to_device(descs.view(np.uint8).copy(), device)
+    per = len(work) // n_groups
+    uniform = len(work) % n_groups == 0 and offsets == [g * per for g in range(n_groups + 1)]
     return DecodePlan(
         B=B, H=H, H_kv=H_kv, D=D, rep_t=rep_t, dtype=dtype,
         descs=dev_descs, work=_to_device(work_np.reshape(-1), device),
         offsets=_to_device(np.asarray(offsets, dtype=np.int32), device),
         n_desc=len(chunks), n_work=len(work), n_groups=n_groups,
         rows=rows_attended, keep=keep, work_host=work_np, kivi=kivi, kivi_rows=kivi_rows,
+        uniform_groups=uniform,
     )
 
 
@@ -387,7 +391,7 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t,
         plan.descs.data_ptr(), plan.n_desc,
         plan.work.data_ptr(), plan.n_work,
-        plan.offsets.data_ptr(), plan.n_groups,
+        None if plan.uniform_groups else plan.offsets.data_ptr(), plan.n_groups,
         nat.ptr(q_pos), float(scale),
         nat.ptr(m), nat.ptr(l), nat.ptr(o), plan.H, acc_mode,
         nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse),

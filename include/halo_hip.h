@@ -87,7 +87,10 @@ size_t halo_decode_workspace_size(int n_work, int rep_t, int D);
  *            descs[desc] for query-head group `group` = (b*H_kv + h_kv)*n_sub
  *            + sub (n_sub = ceil(rep/rep_t)) and writes partial `slot`;
  *            the slots of group g are group_offsets[g] .. group_offsets[g+1]-1
- *            (device int32 [n_groups+1]), a permutation of 0 .. n_work-1
+ *            (device int32 [n_groups+1]), a permutation of 0 .. n_work-1;
+ *            NULL when every group owns n_work / n_groups slots, group g
+ *            slots g*(n_work/n_groups) .. (g+1)*(n_work/n_groups)-1 (the merge
+ *            then reads no offsets)
  *   q_pos    device int64 [B] global query position, or NULL (no causal mask)
  *   scale    softmax scale applied to q.k in fp32
  *   m,l,o    fp32 online-softmax accumulators (B,H), (B,H), (B,H,D) with the

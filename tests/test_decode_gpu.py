@@ -242,3 +242,36 @@ def test_ragged_batch_rows(dev):
            q_pos=torch.tensor([T - 1 for T in lens], device=dev))
     for b in range(3):
         _check(out[b:b + 1], lse[b:b + 1], refs[b][0], refs[b][1], "float32")
+
+
+def test_uniform_group_offsets_optional(dev):
+    """A table whose groups own equal, consecutive slot ranges may omit
+    group_offsets (NULL): the merge then derives them; results are
+    bit-identical to passing the offsets, and the planner marks such tables."""
+    import dataclasses
+
+    from halo_amd.decode import ChunkRef, build_plan, launch
+    x = decode_inputs(7, B=2, H=8, H_kv=2, T=2048, D=128, dtype="bfloat16")
+    q, k, v = (_gpu(a, "bfloat16", dev) for a in (x.q, x.k, x.v))
+    refs = [ChunkRef(k[..., c:c + 512, :], v[..., c:c + 512, :], c, True) for c in range(0, 2048, 512)]
+    plan = build_plan(B=2, H=8, H_kv=2, D=128, dtype=torch.bfloat16, chunks=refs, device=dev, split=256)
+    assert plan.uniform_groups and plan.n_work % plan.n_groups == 0
+    outs = []
+    for p in (plan, dataclasses.replace(plan, uniform_groups=False)):
+        out = torch.empty((2, 8, 128), device=dev, dtype=torch.bfloat16)
+        lse = torch.empty((2, 8), device=dev)
+        launch(p, q[:, :, 0], scale=128 ** -0.5, out=out, lse=lse)
+        torch.cuda.synchronize()
+        outs.append((out, lse))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    ref, ref_lse = A.attention_f64(qn[:, :, 0], kn, vn, scale=128 ** -0.5)
+    _check(outs[0][0], outs[0][1], ref, ref_lse, "bfloat16")
+    # a table with unequal groups (row 1 attends 3 items per group, row 0
+    # attends 8) cannot omit the offsets: the entry point rejects it
+    ragged = build_plan(B=2, H=8, H_kv=2, D=128, dtype=torch.bfloat16, chunks=refs, device=dev, split=256,
+                        q_pos_host=[2047, 600])
+    assert not ragged.uniform_groups and ragged.n_work % ragged.n_groups != 0
+    out = torch.empty((2, 8, 128), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        launch(dataclasses.replace(ragged, uniform_groups=True), q[:, :, 0], scale=128 ** -0.5, out=out)

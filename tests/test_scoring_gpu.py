@@ -157,6 +157,30 @@ def test_fused_selection_matches_two_kernel_path(dev):
         assert torch.equal(a, b)
 
 
+def test_fused_selection_lead_items_miscount(dev):
+    """lead_items is a scheduling hint: understated (0) or overstated (every
+    record, so hot items also stage the selection's page means into LDS
+    before attending), the outputs, LSEs, indices and scores are identical
+    to the planner's count."""
+    scale = 1 / math.sqrt(C2["D"])
+    layer, q = _tiered_from_fixture(C2, dev, True)
+    cfg = layer.select_cfg
+    true_lead = cfg.lead_items
+    assert 0 < true_lead < layer.plan.n_work
+    res = []
+    for lead in (true_lead, 0, layer.plan.n_work):
+        cfg.lead_items = lead
+        out = torch.empty((1, C2["H"], C2["D"]), device=dev, dtype=torch.bfloat16)
+        lse = torch.empty((1, C2["H"]), device=dev)
+        layer.step(q[:, :, 0], scale=scale, out=out, lse=lse)
+        torch.cuda.synchronize()
+        res.append((layer.idx.clone(), layer.scores.clone(), out, lse))
+    cfg.lead_items = true_lead
+    for other in res[1:]:
+        for a, b in zip(res[0], other):
+            assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 def test_fused_selection_per_row_ragged(dev, dtype):
     """halo_decode_attn_tiered with one selection per batch row over a

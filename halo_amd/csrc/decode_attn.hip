@@ -997,8 +997,7 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, char* sme
             sv[nb][c] = valid ? sc[nb][c] * P.scale2 : -INFINITY;
             bm = fmaxf(bm, sv[nb][c]);
           }
-        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        bm = rows4_max(bm);
         const float m_new = fmaxf(m_lane, bm);
         const float ms = (m_new == -INFINITY) ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
@@ -1022,8 +1021,7 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, char* sme
         __syncthreads();  // hand the tile's p and rescale factors to the V-wave
       }
     }
-    float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
+    const float lsum = rows4_sum(l_lane);
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
       m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));
@@ -1646,8 +1644,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
             sv[nb][c] = valid ? (s_code + sz[c]) * P.scale2 : -INFINITY;
             bm = fmaxf(bm, sv[nb][c]);
           }
-        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        bm = rows4_max(bm);
         const float m_new = fmaxf(m_lane, bm);
         const float ms = (m_new == -INFINITY) ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
@@ -1710,8 +1707,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
     }
   }
   float m_run[REP], l_head[REP];
-  float lsum = l_lane + __shfl_xor(l_lane, 16, kWave);
-  lsum += __shfl_xor(lsum, 32, kWave);
+  const float lsum = rows4_sum(l_lane);
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
     m_run[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_lane), r));

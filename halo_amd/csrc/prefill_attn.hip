@@ -275,8 +275,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
           sv4[kb][e] = x;
           bm = fmaxf(bm, x);
         }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      bm = rows4_max(bm);
       const float bms = bm * P.scale2;  // scores scale after the max (scale > 0)
       const float m_old = m_run[c];
       const float m_new = (bms > m_old + kPfLazyMax) ? bms : m_old;
@@ -330,8 +329,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillParams P) {
   // normalise and store: lane holds O^T[d = 16db + 4g + e][query ql]
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    float lt = l_run[c] + __shfl_xor(l_run[c], 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    const float lt = rows4_sum(l_run[c]);
     const int r = row0 + c * 16 + ql;
     if (r >= P.T_q) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;

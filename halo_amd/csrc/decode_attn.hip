@@ -1497,14 +1497,14 @@ decode_attn_kivi_kernel(DecodeParams P) {
   // rescale factors, then the wave partials; the plain-row path (the
   // unquantised recent rows in the same launch) reuses the same bytes.
   constexpr int SZ_RAW = NW * TBYTES;
-  constexpr int SZ_PB = NW * REP * 32 * 2;
+  constexpr int SZ_PB = NW * REP * 64 * 2;
   constexpr int SZ_ALW = (NW * REP * 4 + 15) / 16 * 16;
   constexpr int SZ_KL = SZ_RAW + SZ_PB + SZ_ALW + NW * REP * D * 4;
   constexpr int SZ_PL = PlainMfmaLds<D, REP, NW>::bytes;
   __shared__ __attribute__((aligned(16))) char smem[SZ_KL > SZ_PL ? SZ_KL : SZ_PL];
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
   char (*s_raw)[TBYTES] = reinterpret_cast<char (*)[TBYTES]>(smem);
-  uint16_t (*s_p)[REP * 32] = reinterpret_cast<uint16_t (*)[REP * 32]>(smem + SZ_RAW);
+  uint16_t (*s_p)[REP * 64] = reinterpret_cast<uint16_t (*)[REP * 64]>(smem + SZ_RAW);
   float (*s_al)[REP] = reinterpret_cast<float (*)[REP]>(smem + SZ_RAW + SZ_PB);
   float* s_wo = reinterpret_cast<float*>(smem + SZ_RAW + SZ_PB + SZ_ALW);
 
@@ -1609,41 +1609,57 @@ decode_attn_kivi_kernel(DecodeParams P) {
       for (int i = 0; i < LPT; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[u][i];
       wave_lds_fence();
       const int tok0 = t0 + (it + u) * TB * 32;  // first token of the tile
-      for (int blk = 0; blk < TB; ++blk) {
-        const int nrows = min(32, t1 - (tok0 + blk * 32));  // <= 0: block past the range
-        if (nrows <= 0) break;
-        const char* bk = raw + blk * BB;
-        // ---- scores: 2 row blocks of 16 tokens, code MFMAs + one zero-term MFMA per k-step
-        f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        f32x4 sz = {0.f, 0.f, 0.f, 0.f};
+      // Blocks in pairs: the score MFMAs of both blocks are independent and
+      // issue together, one online-softmax step covers their 64 tokens
+      // (one max, one rescale), and the P.V MFMAs of both follow; a second
+      // block past the range is all masked (its tile bytes read as zeros)
+      // and adds nothing.
+      static_assert(TB % 2 == 0, "blocks are processed in pairs");
+      for (int bp = 0; bp < TB; bp += 2) {
+        const int nr0 = min(32, t1 - (tok0 + bp * 32));  // <= 0: pair past the range
+        if (nr0 <= 0) break;
+        const int nrw[2] = {nr0, min(32, t1 - (tok0 + (bp + 1) * 32))};
+        const char* bkp = raw + bp * BB;
+        // ---- scores: per block 2 row blocks of 16 tokens, code MFMAs + one zero-term MFMA per k-step
+        f32x4 sc[2][2], sz[2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+          sc[pb][0] = sc[pb][1] = sz[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slab
-          const uint4 sk = *reinterpret_cast<const uint4*>(bk + CB + 2 * c0);
-          const uint4 zk = *reinterpret_cast<const uint4*>(bk + CB + 2 * D + 2 * c0);
-          uint4 qs, qs_lo;
-          if constexpr (DT == HALO_BF16) mul8_bf16_split(qb[s], sk, qs, qs_lo);
-          else qs = mul8<DT>(qb[s], sk);
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb) {
-            const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
-            const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
-            sc[nb] = MfmaOp<DT>::run(cd, qs, sc[nb]);
-            if constexpr (DT == HALO_BF16) sc[nb] = MfmaOp<DT>::run(cd, qs_lo, sc[nb]);
+          for (int pb = 0; pb < 2; ++pb) {
+            const char* bk = bkp + pb * BB;
+            const uint4 sk = *reinterpret_cast<const uint4*>(bk + CB + 2 * c0);
+            const uint4 zk = *reinterpret_cast<const uint4*>(bk + CB + 2 * D + 2 * c0);
+            uint4 qs, qs_lo;
+            if constexpr (DT == HALO_BF16) mul8_bf16_split(qb[s], sk, qs, qs_lo);
+            else qs = mul8<DT>(qb[s], sk);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+              const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
+              const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
+              sc[pb][nb] = MfmaOp<DT>::run(cd, qs, sc[pb][nb]);
+              if constexpr (DT == HALO_BF16) sc[pb][nb] = MfmaOp<DT>::run(cd, qs_lo, sc[pb][nb]);
+            }
+            sz[pb] = MfmaOp<DT>::run(zk, qb[s], sz[pb]);
           }
-          sz = MfmaOp<DT>::run(zk, qb[s], sz);
         }
-        // ---- online softmax (lane: head hl, tokens 16nb + 4kg + c)
-        float sv[2][4], bm = -INFINITY;
+        // ---- online softmax over the pair (lane: head hl, tokens 32pb + 16nb + 4kg + c)
+        float sv[2][2][4], bm = -INFINITY;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const bool valid = nb * 16 + kg * 4 + c < nrows;
-            const float s_code = DT == HALO_F16 ? sc[nb][c] * kSub16Scale : sc[nb][c];
-            sv[nb][c] = valid ? (s_code + sz[c]) * P.scale2 : -INFINITY;
-            bm = fmaxf(bm, sv[nb][c]);
-          }
+          for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const bool valid = nb * 16 + kg * 4 + c < nrw[pb];
+              const float s_code = DT == HALO_F16 ? sc[pb][nb][c] * kSub16Scale : sc[pb][nb][c];
+              sv[pb][nb][c] = valid ? (s_code + sz[pb][c]) * P.scale2 : -INFINITY;
+              bm = fmaxf(bm, sv[pb][nb][c]);
+            }
         bm = rows4_max(bm);
         const float m_new = fmaxf(m_lane, bm);
         const float ms = (m_new == -INFINITY) ? 0.f : m_new;
@@ -1651,21 +1667,23 @@ decode_attn_kivi_kernel(DecodeParams P) {
         m_lane = m_new;
         float psum = 0.f;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          float p4[4];
+        for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            p4[c] = __builtin_amdgcn_exp2f(sv[nb][c] - ms);
-            psum += p4[c];
+          for (int nb = 0; nb < 2; ++nb) {
+            float p4[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              p4[c] = __builtin_amdgcn_exp2f(sv[pb][nb][c] - ms);
+              psum += p4[c];
+            }
+            if (hl < REP)
+              *reinterpret_cast<uint2*>(pw + hl * 64 + pb * 32 + nb * 16 + kg * 4) =
+                  make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
           }
-          if (hl < REP)
-            *reinterpret_cast<uint2*>(pw + hl * 32 + nb * 16 + kg * 4) =
-                make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
-        }
         l_lane = l_lane * alpha + psum;
         if (lane < REP) alw[lane] = alpha;
         wave_lds_fence();
-        // ---- P.V: per group, codes against p*s and the zeros against p
+        // ---- P.V: per block and group, codes against p*s and the zeros against p
         if (__builtin_amdgcn_read_exec() & __ballot(hl < REP && alpha != 1.f)) {  // some head's max moved
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -1678,30 +1696,35 @@ decode_attn_kivi_kernel(DecodeParams P) {
             }
           }
         }
-        const uint4 pa = hl < REP ? *reinterpret_cast<const uint4*>(pw + hl * 32 + kg * 8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int gg = 0; gg < NG; ++gg) {
-          const uint4 sv8 = *reinterpret_cast<const uint4*>(bk + VS + 2 * (gg * 32 + kg * 8));
-          const uint4 zv8 = *reinterpret_cast<const uint4*>(bk + VZ + 2 * (gg * 32 + kg * 8));
-          uint4 ps, ps_lo;
-          if constexpr (DT == HALO_BF16) mul8_bf16_split(pa, sv8, ps, ps_lo);
-          else ps = mul8<DT>(pa, sv8);
+        for (int pb = 0; pb < 2; ++pb) {
+          const char* bk = bkp + pb * BB;
+          const uint4 pa =
+              hl < REP ? *reinterpret_cast<const uint4*>(pw + hl * 64 + pb * 32 + kg * 8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-          for (int d2 = 0; d2 < 2; ++d2) {
-            const int db = 2 * gg + d2;
-            const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
-            const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
-            acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
-            if constexpr (DT == HALO_BF16) {
-              acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
-              acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
+          for (int gg = 0; gg < NG; ++gg) {
+            const uint4 sv8 = *reinterpret_cast<const uint4*>(bk + VS + 2 * (gg * 32 + kg * 8));
+            const uint4 zv8 = *reinterpret_cast<const uint4*>(bk + VZ + 2 * (gg * 32 + kg * 8));
+            uint4 ps, ps_lo;
+            if constexpr (DT == HALO_BF16) mul8_bf16_split(pa, sv8, ps, ps_lo);
+            else ps = mul8<DT>(pa, sv8);
+#pragma unroll
+            for (int d2 = 0; d2 < 2; ++d2) {
+              const int db = 2 * gg + d2;
+              const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
+              const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
+              acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
+              if constexpr (DT == HALO_BF16) {
+                acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
+                acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
+              }
             }
+            // fp16: the code products carry 2^-24, so the zero term of the
+            // group (equal for all its columns) accumulates on its own
+            if constexpr (DT == HALO_F16) accz[gg] = MfmaOp<DT>::run(pa, zv8, accz[gg]);
           }
-          // fp16: the code products carry 2^-24, so the zero term of the
-          // group (equal for all its columns) accumulates on its own
-          if constexpr (DT == HALO_F16) accz[gg] = MfmaOp<DT>::run(pa, zv8, accz[gg]);
         }
-        wave_lds_fence();  // the next block rewrites p and the rescale factors
+        wave_lds_fence();  // the next pair rewrites p and the rescale factors
       }
       wave_lds_fence();  // the next tile rewrites raw
     }
@@ -1731,9 +1754,8 @@ decode_attn_kivi_kernel(DecodeParams P) {
 // round trip; the TPC per-thread results are then combined in a fixed order
 // through LDS (deterministic run to run).
 // ---------------------------------------------------------------------------
-template <int D, int REP>
-__global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams P) {
-  constexpr int NT = 256;
+template <int D, int REP, int NT>
+__global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
   constexpr int C4 = D / 4;           // float4 columns of one head
   constexpr int TPC = NT / C4;        // threads sharing a column
   __shared__ float4 s_o[NT];
@@ -1924,7 +1946,13 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
                        st, p);
   }
   HALO_CHECK_HIP(hipGetLastError());
-  hipLaunchKernelGGL((decode_merge_kernel<D, REP>), dim3(n_groups, REP), dim3(256), 0, st, mp);
+  // Groups of more than 64 partials on average merge with 512 threads, so
+  // one batch of loads (8 partials per thread) covers a group.
+  if (n_work > 64 * n_groups) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512>), dim3(n_groups, REP), dim3(512), 0, st, mp);
+  } else {
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 256>), dim3(n_groups, REP), dim3(256), 0, st, mp);
+  }
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }

@@ -275,3 +275,27 @@ def test_uniform_group_offsets_optional(dev):
     out = torch.empty((2, 8, 128), device=dev, dtype=torch.bfloat16)
     with pytest.raises(AssertionError):
         launch(dataclasses.replace(ragged, uniform_groups=True), q[:, :, 0], scale=128 ** -0.5, out=out)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_many_partials_per_group(dev, dtype):
+    """Groups of more than 64 partials (here 128 and 130) take the merge's
+    512-thread form; results match the float64 closed form like the
+    256-thread form's."""
+    from halo_amd.decode import ChunkRef, build_plan, launch
+    x = decode_inputs(11, B=1, H=4, H_kv=1, T=16640, D=128, dtype=dtype)
+    q, k, v = (_gpu(a, dtype, dev) for a in (x.q, x.k, x.v))
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    ref, ref_lse = A.attention_f64(qn[:, :, 0], kn, vn, scale=128 ** -0.5)
+    for T, split in ((16384, 128), (16640, 128), (16384, 256)):
+        refs = [ChunkRef(k[..., c:min(c + 1024, T), :], v[..., c:min(c + 1024, T), :], c, True)
+                for c in range(0, T, 1024)]
+        plan = build_plan(B=1, H=4, H_kv=1, D=128, dtype=TDT[dtype], chunks=refs, device=dev, split=split)
+        assert (plan.n_work > 64 * plan.n_groups) == (split == 128)
+        out = torch.empty((1, 4, 128), device=dev, dtype=TDT[dtype])
+        lse = torch.empty((1, 4), device=dev)
+        launch(plan, q[:, :, 0], scale=128 ** -0.5, out=out, lse=lse)
+        torch.cuda.synchronize()
+        r, rl = (ref, ref_lse) if T == 16640 else A.attention_f64(qn[:, :, 0], kn[..., :T, :], vn[..., :T, :],
+                                                                 scale=128 ** -0.5)
+        _check(out, lse, r, rl, dtype)

@@ -495,7 +495,8 @@ def main() -> int:
             "chunk": chunk, "hot_chunks": n_hot, "top_k": top_k,
             "launch": ("hip graph; per layer: attention kernel with in-kernel top-k selection + merge kernel"
                        if layers[0].fused else "hip graph; per layer: scorer + attention + merge kernels"),
-            "split_rows": int(layers[0].plan.work_host[0, 3] - layers[0].plan.work_host[0, 2]),
+            "split_rows": int(layers[0].plan.work_host[-1, 3] - layers[0].plan.work_host[-1, 2]),
+            "selection_split_rows": int(layers[0].plan.work_host[0, 3] - layers[0].plan.work_host[0, 2]),
             "work_items": layers[0].plan.n_work,
         },
         "hbm_gbps_end_to_end": step_bytes / dt / 1e9,

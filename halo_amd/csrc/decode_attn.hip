@@ -1162,12 +1162,6 @@ decode_attn_kernel(DecodeParams P) {
   } else {
     dsc = P.descs[item.x];
   }
-  // With in-kernel selection, the hot items hold back their K/V flood for
-  // ~1k cycles once their descriptor is in: the selection's page-mean loads,
-  // issued first by the slot items, then reach memory ahead of it instead of
-  // queueing behind tens of MiB of K/V (the selection sits on the critical
-  // path of the launch).
-  if (P.sel_on && !(item.x >= P.sel.slot0 && item.x < P.sel.slot0 + P.sel.top_k)) __builtin_amdgcn_s_sleep(16);
   const int hq0 = h_kv * P.rep + sub * REP;
   const int nvalid_h = min(REP, P.rep - sub * REP);
 

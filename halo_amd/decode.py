@@ -238,7 +238,8 @@ def descs_to_device(descs: np.ndarray, device) -> torch.Tensor:
 def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                chunks: Sequence[ChunkRef], device, rep_t: Optional[int] = None,
                split: Optional[int] = None, q_pos_host: Optional[Sequence[int]] = None,
-               first: Optional[Sequence[int]] = None) -> DecodePlan:
+               first: Optional[Sequence[int]] = None, split_first: Optional[int] = None,
+               first_half_split: bool = False) -> DecodePlan:
     """Lay out descriptors and work items for a chunk list.
 
     ``q_pos_host`` (per batch row) lets the planner drop causal chunks that
@@ -251,7 +252,9 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
     order the merge reads them; the records themselves are in dispatch
     order, where the items of the chunks listed in ``first`` come before
     all others (the tiered layer puts its selection slots there, so their
-    longer dependency chain starts first).
+    longer dependency chain starts first); ``split_first`` (rows per item of
+    those chunks, default ``split``) cuts them finer, and
+    ``first_half_split`` sets it to half the split (at least 128 rows).
     """
     if H % H_kv:
         raise AssertionError(f"head count mismatch: q has {H}, kv has {H_kv}")
@@ -285,6 +288,8 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                 total_rows += rows * H_kv * n_sub
     if split is None:
         split = choose_split(total_rows, _num_cus(device), kivi=kivi)
+    if first_half_split and split_first is None:
+        split_first = max(128, split // 2)
 
     work = []
     offsets = [0]
@@ -301,8 +306,9 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
                     hi = T
                     if chunks[i].causal and q_pos_host is not None:
                         hi = min(T, int(q_pos_host[b]) - chunks[i].chunk_start + 1)
-                    for t0 in range(0, hi, split):
-                        work.append((i, g, t0, min(t0 + split, hi), len(work), 0, 0, 0))
+                    sp = split_first if (split_first and first is not None and i in first) else split
+                    for t0 in range(0, hi, sp):
+                        work.append((i, g, t0, min(t0 + sp, hi), len(work), 0, 0, 0))
                     if s == 0:
                         rows_attended += hi
                         if hasattr(chunks[i], "blocks"):

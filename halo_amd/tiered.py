@@ -51,15 +51,18 @@ class TieredDecodeLayer:
             and B * H_kv * D <= _SEL_MAX_QBAR and D % 16 == 0
         # Selection slots come first in the table (their workgroups are
         # dispatched first, which hides the selection work behind the hot
-        # chunks).  Each slot is planned over the largest cold chunk, so its
-        # work items cover whichever chunk is chosen; the unfused scorer
-        # overwrites the slot descriptors on the device every step.
+        # chunks) and are cut into items of half the split: their rows can
+        # only be read once the selection is known, so spreading them over
+        # twice the workgroups shortens that critical path.  Each slot is
+        # planned over the largest cold chunk, so its work items cover
+        # whichever chunk is chosen; the unfused scorer overwrites the slot
+        # descriptors on the device every step.
         widest = max(range(n_cold), key=lambda i: cold[i].T)
         slots = [cold[widest]] * top_k
         self.slot0 = 0
         self.plan: DecodePlan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype,
                                            chunks=slots + list(hot), device=device, split=split,
-                                           first=range(top_k))
+                                           first=range(top_k), first_half_split=True)
         cat, keep = pack_descs(cold, B=B, H_kv=H_kv, D=D, dtype=dtype)
         self.catalog = descs_to_device(cat, device)
         self.plan.keep += keep

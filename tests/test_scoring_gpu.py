@@ -313,3 +313,48 @@ def test_ragged_batched_decode(dev, dtype):
         tol = 1e-5 if dtype == "float32" else 2e-2
         assert np.abs(out[b:b + 1].float().cpu().numpy() - ro).max() <= tol
         assert np.abs(lse[b:b + 1].cpu().numpy() - rl).max() <= (1e-5 if dtype == "float32" else 1e-3)
+
+
+@pytest.mark.parametrize("case", ["lds_qbar", "many_units", "unaligned_q"])
+def test_fused_selection_paths(dev, case):
+    """The fused selector's other paths against the standalone scorer path,
+    bit for bit (indices, scores, outputs, LSE): 'lds_qbar' (3 batch rows x 2
+    KV heads: a lane's head varies across its dot-product units, so the GQA
+    query mean is staged in LDS), 'many_units' (64 candidates x 8 KV heads =
+    4096 units, past the six per lane held in registers), 'unaligned_q'
+    (query rows not 16-byte aligned: the element-wise q-bar)."""
+    from halo_amd.decode import ChunkRef
+    from halo_amd.tiered import TieredDecodeLayer
+    B, H, H_kv, c, n_hot, n_cold, top_k = {
+        "lds_qbar": (3, 8, 2, 128, 4, 12, 3),
+        "many_units": (1, 16, 8, 64, 4, 64, 5),
+        "unaligned_q": (1, 32, 8, 128, 4, 12, 4),
+    }[case]
+    D, T = 128, (n_hot + n_cold) * c
+    x = decode_inputs(61, B=B, H=H, H_kv=H_kv, T=T, D=D, dtype="bfloat16", n_planted=2, sigma=6.0)
+    q, k, v = (_gpu(a, "bfloat16", dev) for a in (x.q, x.k, x.v))
+    q = q[:, :, 0]
+    if case == "unaligned_q":
+        wide = torch.zeros((B, H, D + 1), device=dev, dtype=torch.bfloat16)
+        wide[..., 1:] = q
+        q = wide[..., 1:]
+        assert (q.stride(1) * 2) % 16 != 0
+    refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True)
+            for i in range(n_hot + n_cold)]
+    res = []
+    for fused in (True, False):
+        layer = TieredDecodeLayer(B=B, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:],
+                                  cold=refs[:n_cold], top_k=top_k, device=dev, fused=fused)
+        assert layer.fused == fused
+        out = torch.empty((B, H, D), device=dev, dtype=torch.bfloat16)
+        lse = torch.empty((B, H), device=dev)
+        layer.step(q, scale=D ** -0.5, out=out, lse=lse)
+        torch.cuda.synchronize()
+        res.append((layer.idx.clone(), layer.scores.clone(), out, lse))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    # the choice itself: top_k of the oracle's fixed-order scores
+    km = S.page_means(x.k[..., :n_cold * c, :], c, "bfloat16")
+    qn = q.float().cpu().numpy()[:, :, None, :]
+    sc = S.ordered_scores(qn, km, "bfloat16")
+    np.testing.assert_array_equal(res[0][1].cpu().numpy()[0, :n_cold], sc[:n_cold])

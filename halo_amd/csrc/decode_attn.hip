@@ -1854,8 +1854,9 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
   }
   if (P.out != nullptr) {
     float ov[4];
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;  // one division per thread, then products
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ov[e] = lsum > 0.f ? o4[e] / lsum : 0.f;
+    for (int e = 0; e < 4; ++e) ov[e] = o4[e] * inv;
     const int64_t oi = ((int64_t)b * P.H + hq) * D + d0;
     if (P.out_vec) {
       store_elem4(P.out, oi, P.out_dtype, ov);

@@ -97,6 +97,7 @@ _SIGNATURES = {
         _i32, _f32, _f32, _f32, _i32, _i32, _i32,  # normalize, alpha, beta, gamma, refresh, sink_pages, P_total
         _c_void_p,
     ]),
+    "halo_host_device_pointer": (_i32, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "halo_last_error": (ctypes.c_char_p, []),
     "halo_build_info": (ctypes.c_char_p, []),
 }
@@ -178,3 +179,11 @@ def stream_ptr(stream: Optional[torch.cuda.Stream] = None) -> int:
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else int(t.data_ptr())
+
+
+def host_device_pointer(ptr: int) -> int:
+    """Device-visible address of pinned host memory at ``ptr``
+    (``halo_host_device_pointer``)."""
+    out = _c_void_p()
+    check(lib().halo_host_device_pointer(ptr, ctypes.byref(out)), "halo_host_device_pointer")
+    return int(out.value)

@@ -111,6 +111,18 @@ def _check_kv(t: torch.Tensor, name: str) -> None:
         raise AssertionError(f"{name}: rows must be 16-byte aligned")
 
 
+def _kernel_address(t: torch.Tensor, name: str) -> int:
+    """Address a kernel reads ``t`` at: device memory as is; a chunk kept in
+    pinned host memory (the cold tier) through its device-visible mapping,
+    so the kernel streams it over the host link in place."""
+    if t.device.type != "cpu":
+        return t.data_ptr()
+    if not t.is_pinned():
+        raise AssertionError(f"{name}: a host-resident chunk must be in pinned memory (pin_memory())")
+    base = t.untyped_storage().data_ptr()
+    return nat.host_device_pointer(base) + (t.data_ptr() - base)
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     esz = t.element_size()
     if t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(-2) * esz) % 16:
@@ -185,7 +197,7 @@ def pack_descs(chunks: Sequence[ChunkRef], *, B: int, H_kv: int, D: int, dtype: 
         _check_kv(v, f"chunk {i} v")
         keep += [k, v]
         d = descs[i]
-        d["k"], d["v"] = k.data_ptr(), v.data_ptr()
+        d["k"], d["v"] = _kernel_address(k, f"chunk {i} k"), _kernel_address(v, f"chunk {i} v")
         if c.batch < 0:
             d["ksb"], d["ksh"], d["kst"] = k.stride(0), k.stride(1), k.stride(2)
             d["vsb"], d["vsh"], d["vst"] = v.stride(0), v.stride(1), v.stride(2)

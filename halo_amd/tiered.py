@@ -68,6 +68,8 @@ class TieredDecodeLayer:
         self.plan.keep += keep
         self.eligible = torch.arange(len(cold), device=device, dtype=torch.int32)
         if cold_kmean is None:
+            if any(c.k.device.type == "cpu" for c in cold):
+                raise AssertionError("cold chunks in pinned host memory need cold_kmean (their page means on the GPU)")
             cold_kmean = self.build_means(cold)
         self.kmean = cold_kmean
         self.idx = torch.empty((1, top_k), device=device, dtype=torch.int32)

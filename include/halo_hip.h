@@ -343,6 +343,18 @@ int halo_decode_attn_kivi(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- build metadata ---------------------------------------------------- */
+/*
+ * Device-visible address of pinned host memory (allocated by hipHostMalloc,
+ * e.g. a pinned torch tensor), written to *dev.  A chunk descriptor holding
+ * that address makes the decode kernels read the chunk in place from host
+ * DRAM over the host link: the refetch of selected cold chunks then happens
+ * inside the attention launch with no host round trip.  Replaces the
+ * DRAM -> GPU block moves of the pinned cold tier (halo/memory_tier.py:
+ * 150-157, 197-205; halo/triton_chunked.py:325-350).  HALO_E_INVALID when
+ * `host` is not pinned host memory.
+ */
+int halo_host_device_pointer(const void* host, void** dev);
+
 const char* halo_last_error(void);
 const char* halo_build_info(void);
 

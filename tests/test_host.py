@@ -155,3 +155,15 @@ def test_wrap_with_halo_attaches_components():
     assert all(getattr(a, "_halo_cache", None) is m._halo_cache for a in m.layers)
     with pytest.raises(ValueError):
         wrap_with_halo(Model(), HALOConfig(chunked=True, eviction=True))
+
+
+def test_host_resident_chunk_must_be_pinned():
+    """A chunk in host memory is read in place only when pinned; an ordinary
+    host tensor is rejected before any device call."""
+    import pytest
+    import torch
+
+    from halo_amd.decode import ChunkRef, pack_descs
+    k = torch.zeros((1, 2, 64, 128), dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="pinned"):
+        pack_descs([ChunkRef(k, k.clone(), 0, True)], B=1, H_kv=2, D=128, dtype=torch.bfloat16)

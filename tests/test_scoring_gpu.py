@@ -358,3 +358,35 @@ def test_fused_selection_paths(dev, case):
     qn = q.float().cpu().numpy()[:, :, None, :]
     sc = S.ordered_scores(qn, km, "bfloat16")
     np.testing.assert_array_equal(res[0][1].cpu().numpy()[0, :n_cold], sc[:n_cold])
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "two_kernel"])
+def test_cold_chunks_read_in_place_from_pinned_host(dev, fused):
+    """Cold chunks kept in pinned host memory (descriptors hold their
+    device-visible addresses) are read by the kernels in place: indices,
+    scores, outputs and LSE equal the same layer with the chunks in HBM."""
+    from halo_amd.decode import ChunkRef
+    from halo_amd.tiered import TieredDecodeLayer
+    H, H_kv, D, c, n_hot, n_cold, top_k = 32, 8, 128, 256, 4, 12, 4
+    x = decode_inputs(71, B=1, H=H, H_kv=H_kv, T=(n_hot + n_cold) * c, D=D, dtype="bfloat16", n_planted=4,
+                      sigma=8.0)
+    q, k, v = (_gpu(a, "bfloat16", dev) for a in (x.q, x.k, x.v))
+    refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True)
+            for i in range(n_hot + n_cold)]
+    dev_layer = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:],
+                                  cold=refs[:n_cold], top_k=top_k, device=dev, fused=fused)
+    host_cold = [ChunkRef(r.k.cpu().pin_memory(), r.v.cpu().pin_memory(), r.chunk_start, r.causal)
+                 for r in refs[:n_cold]]
+    assert all(r.k.is_pinned() and r.k.device.type == "cpu" for r in host_cold)
+    host_layer = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:],
+                                   cold=host_cold, top_k=top_k, device=dev, cold_kmean=dev_layer.kmean,
+                                   fused=fused)
+    res = []
+    for layer in (dev_layer, host_layer):
+        out = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+        lse = torch.empty((1, H), device=dev)
+        layer.step(q[:, :, 0], scale=D ** -0.5, out=out, lse=lse)
+        torch.cuda.synchronize()
+        res.append((layer.idx.clone(), layer.scores.clone(), out, lse))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)

@@ -1791,20 +1791,31 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
       ml[k] = *reinterpret_cast<const float2*>(wml + (int64_t)pp * REP * 2);
       op[k] = wo4[(int64_t)pp * REP * C4];
     }
+    // the batch's max first, then independent weights (one rescale of the
+    // running values per batch instead of a dependent chain per partial)
+    float mb = mt;
+#pragma unroll
+    for (int k = 0; k < MB; ++k)
+      if (p0 + k * TPC < np) mb = fmaxf(mb, ml[k].x);
+    const float ms = (mb == -INFINITY) ? 0.f : mb;
+    const float a = __builtin_amdgcn_exp2f(mt - ms);
+    lt *= a;
+    ot.x *= a;
+    ot.y *= a;
+    ot.z *= a;
+    ot.w *= a;
 #pragma unroll
     for (int k = 0; k < MB; ++k) {
       if (p0 + k * TPC < np) {
-        const float mn = fmaxf(mt, ml[k].x);
-        const float ms = (mn == -INFINITY) ? 0.f : mn;
-        const float a = __builtin_amdgcn_exp2f(mt - ms), c = __builtin_amdgcn_exp2f(ml[k].x - ms);
-        lt = lt * a + ml[k].y * c;
-        ot.x = ot.x * a + op[k].x * c;
-        ot.y = ot.y * a + op[k].y * c;
-        ot.z = ot.z * a + op[k].z * c;
-        ot.w = ot.w * a + op[k].w * c;
-        mt = mn;
+        const float c = __builtin_amdgcn_exp2f(ml[k].x - ms);
+        lt += ml[k].y * c;
+        ot.x += op[k].x * c;
+        ot.y += op[k].y * c;
+        ot.z += op[k].z * c;
+        ot.w += op[k].w * c;
       }
     }
+    mt = mb;
   }
   // The incoming accumulator is read by every thread before the barrier:
   // the column-0 thread overwrites m/l after it.

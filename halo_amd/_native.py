@@ -97,6 +97,8 @@ _SIGNATURES = {
         _i32, _f32, _f32, _f32, _i32, _i32, _i32,  # normalize, alpha, beta, gamma, refresh, sink_pages, P_total
         _c_void_p,
     ]),
+    "halo_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64,
+                                _c_void_p, _i32, _c_void_p]),
     "halo_host_device_pointer": (_i32, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "halo_last_error": (ctypes.c_char_p, []),
     "halo_build_info": (ctypes.c_char_p, []),

@@ -138,7 +138,9 @@ class ChunkScorer:
         n_full = T // p
         prev = int(self._num_full_pages.get(layer_idx, 0))
         self.observe_calls += 1
-        if n_full <= prev:
+        if n_full < prev:  # the rows were replaced (a peel): recompute every page
+            prev = 0
+        elif n_full == prev:
             return
         km = self._k_mean.get(layer_idx)
         if km is None or km.shape[-2] < n_full or km.dtype != K_full.dtype:
@@ -150,6 +152,11 @@ class ChunkScorer:
         chunk_means(K_full, p, row0=prev * p, n_pages=n_full - prev, out=km, page_offset=prev)
         self._k_mean[layer_idx] = km
         self._num_full_pages[layer_idx] = n_full
+
+    def forget(self, layer_idx: int) -> None:
+        """Drop the page means of ``layer_idx`` (its GPU rows were replaced)."""
+        self._k_mean.pop(layer_idx, None)
+        self._num_full_pages.pop(layer_idx, None)
 
     def page_means(self, layer_idx: int) -> Optional[torch.Tensor]:
         km = self._k_mean.get(layer_idx)

@@ -1,0 +1,84 @@
+// Batched block moves between the tiers of the cold-KV store (gfx950).
+//
+// A tier buffer holds fixed-size blocks (one block = one layer's K or V rows
+// of `block_size` tokens for every KV head).  A move of many blocks is one
+// launch that reads the block list on the device, so the caller's schedule
+// (which blocks, from which tier) never goes through the host.  Either side
+// may be pinned host memory addressed through its device-visible mapping:
+// the DRAM tier is then read or written in place over the host link.
+//
+// Reference semantics: TieredStorage.move_block (halo/memory_tier.py:150-157)
+// moves one block per call through torch copies; HALORefetcher._issue and
+// HALODemoter.flush (halo/refetcher.py:102-114, halo/demoter.py:49-77) call it
+// once per block from a Python loop.
+#include "common.hpp"
+
+namespace halo {
+namespace {
+
+constexpr int kCopyThreads = 256;
+constexpr int64_t kCopyPiece = 64 * 1024;  // bytes per workgroup
+constexpr int kCopyUnroll = 4;             // 16-byte loads in flight per thread
+
+struct CopyPair {
+  char* dst;
+  const char* src;
+};
+
+__global__ void __launch_bounds__(kCopyThreads)
+    copy_blocks_kernel(CopyPair p0, CopyPair p1, int64_t block_bytes, const int32_t* blocks, int n_blocks,
+                       int64_t max_blocks, const int8_t* tier_of, int src_tier, int pieces) {
+  const int item = blockIdx.x / pieces;
+  const int piece = blockIdx.x % pieces;
+  if (item >= n_blocks) return;
+  const int32_t b = blocks[item];
+  if (b < 0 || (int64_t)b >= max_blocks) return;
+  if (tier_of != nullptr && (int)tier_of[b] != src_tier) return;
+  const CopyPair pr = blockIdx.y == 0 ? p0 : p1;
+  const int64_t lo = (int64_t)piece * kCopyPiece;
+  const int64_t hi = min(lo + kCopyPiece, block_bytes);
+  const uint4* s = reinterpret_cast<const uint4*>(pr.src + (int64_t)b * block_bytes + lo);
+  uint4* d = reinterpret_cast<uint4*>(pr.dst + (int64_t)b * block_bytes + lo);
+  const int n16 = (int)((hi - lo) / 16);
+  for (int base = 0; base < n16; base += kCopyThreads * kCopyUnroll) {
+    uint4 r[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int j = base + u * kCopyThreads + (int)threadIdx.x;
+      if (j < n16) r[u] = s[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int j = base + u * kCopyThreads + (int)threadIdx.x;
+      if (j < n16) d[j] = r[u];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace halo
+
+using namespace halo;
+
+extern "C" int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, const void* src_v,
+                                int64_t block_bytes, const int32_t* blocks, int n_blocks, int64_t max_blocks,
+                                const int8_t* tier_of, int src_tier, void* stream) {
+  HALO_CHECK_ARG(n_blocks >= 0, "n_blocks < 0");
+  if (n_blocks == 0) return HALO_OK;
+  HALO_CHECK_ARG(dst_k && src_k && blocks, "null pointer argument");
+  HALO_CHECK_ARG((dst_v == nullptr) == (src_v == nullptr), "dst_v and src_v must both be set or both NULL");
+  HALO_CHECK_ARG(block_bytes > 0 && block_bytes % 16 == 0, "block_bytes must be a positive multiple of 16");
+  HALO_CHECK_ARG(max_blocks > 0, "max_blocks must be positive");
+  auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  HALO_CHECK_ARG(aligned(dst_k) && aligned(src_k) && aligned(dst_v) && aligned(src_v),
+                 "tier buffers must be 16-byte aligned");
+  const int64_t pieces = (block_bytes + kCopyPiece - 1) / kCopyPiece;
+  HALO_CHECK_ARG(pieces * n_blocks < (int64_t)1 << 31, "too many blocks for one launch");
+  const dim3 grid((unsigned)(pieces * n_blocks), dst_v ? 2u : 1u);
+  const CopyPair p0{static_cast<char*>(dst_k), static_cast<const char*>(src_k)};
+  const CopyPair p1{static_cast<char*>(dst_v ? dst_v : dst_k), static_cast<const char*>(src_v ? src_v : src_k)};
+  hipLaunchKernelGGL(copy_blocks_kernel, grid, dim3(kCopyThreads), 0, static_cast<hipStream_t>(stream), p0, p1,
+                     block_bytes, blocks, n_blocks, max_blocks, tier_of, src_tier, (int)pieces);
+  HALO_CHECK_HIP(hipGetLastError());
+  return HALO_OK;
+}

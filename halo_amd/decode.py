@@ -86,6 +86,7 @@ class DecodePlan:
     work_host: Optional[np.ndarray] = None
     kivi: bool = False           # the table holds KIVI block runs (plain chunks may join them)
     kivi_rows: int = 0           # rows of ``rows`` that are KIVI-quantised
+    ws: Optional[torch.Tensor] = None  # this plan's partial buffer (halo_decode_workspace_size bytes)
 
     @property
     def kv_bytes(self) -> int:
@@ -346,19 +347,26 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
 
 
 # ---------------------------------------------------------------------------
-# Workspace: one partial buffer per (device, stream); launches on one stream
-# are ordered, so reusing it across calls is safe.
+# Workspace: every plan owns its partial buffer, sized when the plan is built
+# and alive as long as the plan.  A HIP graph that captured a launch of the
+# plan therefore keeps replaying into memory that nobody else can be handed
+# (a buffer shared per stream and regrown for a larger plan would be returned
+# to the caching allocator while a captured graph still writes through it).
+# Launches of one plan are ordered when they share a stream; launching the
+# same plan on two streams at once needs a ``workspace=`` of its own for one.
 # ---------------------------------------------------------------------------
-_WS: dict = {}
+def workspace_bytes(n_work: int, rep_t: int, D: int) -> int:
+    """Bytes of partials a launch with ``n_work`` items writes
+    (``halo_decode_workspace_size``: n_work x rep_t x (D + 2) fp32)."""
+    return int(n_work) * int(rep_t) * (int(D) + 2) * 4
 
 
-def workspace(device, stream_ptr: int, nbytes: int) -> torch.Tensor:
-    key = (torch.device(device).index, stream_ptr)
-    ws = _WS.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _WS[key] = ws
-    return ws
+def plan_workspace(plan: "DecodePlan", device) -> torch.Tensor:
+    """The plan's own workspace, allocated on first use."""
+    if plan.ws is None:
+        nbytes = workspace_bytes(plan.n_work, plan.rep_t, plan.D)
+        plan.ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+    return plan.ws
 
 
 def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
@@ -366,11 +374,14 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
            m: Optional[torch.Tensor] = None, l: Optional[torch.Tensor] = None,
            o: Optional[torch.Tensor] = None, acc_mode: int = 0,
            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-           stream: Optional[torch.cuda.Stream] = None, select=None) -> None:
+           stream: Optional[torch.cuda.Stream] = None, select=None,
+           workspace: Optional[torch.Tensor] = None) -> None:
     """Enqueue one ``halo_decode_attn`` on ``stream`` (default: current).
 
     ``select`` (a ``_native.SelectCfg``) enqueues ``halo_decode_attn_tiered``
-    instead: the table's selection slots choose their chunks in-kernel."""
+    instead: the table's selection slots choose their chunks in-kernel.
+    ``workspace`` (a uint8 device tensor) replaces the plan's own partial
+    buffer, for a second concurrent launch of the same plan."""
     L = nat.lib()
     if q.dim() != 3 or tuple(q.shape) != (plan.B, plan.H, plan.D):
         raise AssertionError(f"expected q (B, H, D) = {(plan.B, plan.H, plan.D)}, got {tuple(q.shape)}")
@@ -403,7 +414,9 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
             raise AssertionError("all tensors must be on the query's device")
     sp = nat.stream_ptr(stream)
     nbytes = int(L.halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
-    ws = workspace(q.device, sp, nbytes)
+    ws = plan_workspace(plan, q.device) if workspace is None else workspace
+    if ws.dtype != torch.uint8 or ws.device != q.device or ws.numel() < nbytes:
+        raise AssertionError(f"workspace must be a uint8 tensor of >= {nbytes} bytes on {q.device}")
     args = (
         q.data_ptr(), q.stride(0), q.stride(1), nat.dtype_code(plan.dtype),
         plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t,

@@ -93,6 +93,29 @@ def finalize(
     return (out, lse) if return_lse else out
 
 
+def lse_merge(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor, lse_b: torch.Tensor):
+    """Combine two partial attention results over disjoint key sets
+    (``halo_lse_merge``; HALOCacheChunked._lse_merge,
+    halo/kv_cache_chunked.py:194-239): lse = logaddexp(lse_a, lse_b), out =
+    exp(lse_a - lse) out_a + exp(lse_b - lse) out_b, where a side whose lse
+    is -inf contributes nothing.  out_* (..., D) and lse_* (...) any float
+    dtype; returns fp32 (out, lse)."""
+    L = nat.lib()
+    if out_a.shape != out_b.shape or lse_a.shape != lse_b.shape or tuple(out_a.shape[:-1]) != tuple(lse_a.shape):
+        raise AssertionError(f"shapes: out {tuple(out_a.shape)}/{tuple(out_b.shape)}, "
+                             f"lse {tuple(lse_a.shape)}/{tuple(lse_b.shape)}")
+    D = out_a.shape[-1]
+    oa, ob = out_a.float().contiguous(), out_b.float().contiguous()
+    la, lb = lse_a.float().contiguous(), lse_b.float().contiguous()
+    out = torch.empty_like(oa)
+    lse = torch.empty_like(la)
+    n = la.numel()
+    if n:
+        nat.check(L.halo_lse_merge(oa.data_ptr(), la.data_ptr(), ob.data_ptr(), lb.data_ptr(), n, D,
+                                   out.data_ptr(), lse.data_ptr(), nat.stream_ptr()), "halo_lse_merge")
+    return out, lse
+
+
 def _al(t: torch.Tensor) -> torch.Tensor:
     esz = t.element_size()
     if t.stride(-1) != 1 or t.data_ptr() % 16 or (t.stride(-2) * esz) % 16:
@@ -261,6 +284,7 @@ __all__ = [
     "init_acc",
     "update_chunk",
     "finalize",
+    "lse_merge",
     "triton_chunked_attention",
     "triton_chunked_attention_streamed",
     "triton_chunked_attention_single_launch",

@@ -342,6 +342,25 @@ int halo_decode_attn_kivi(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           void* out, int out_dtype, float* lse,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- tier block moves -------------------------------------------------- */
+
+/*
+ * Copy whole blocks between two tier buffers of the cold-KV store: for each
+ * i < n_blocks with b = blocks[i] in [0, max_blocks) (and, when tier_of is
+ * non-NULL, tier_of[b] == src_tier), bytes [b*block_bytes, (b+1)*block_bytes)
+ * of src_k go to dst_k, and likewise src_v -> dst_v when both are non-NULL.
+ * Other entries are skipped, so a device-computed candidate list needs no
+ * host-side filtering.  Pointers are device-visible addresses (pinned host
+ * memory through halo_host_device_pointer is read or written in place);
+ * 16-byte aligned, block_bytes % 16 == 0.  One launch on `stream`.
+ * Replaces the per-block TieredStorage.move_block calls of HALORefetcher._issue
+ * and HALODemoter.flush (halo/memory_tier.py:150-157, halo/refetcher.py:
+ * 102-114, halo/demoter.py:49-77).
+ */
+int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, const void* src_v,
+                     int64_t block_bytes, const int32_t* blocks, int n_blocks, int64_t max_blocks,
+                     const int8_t* tier_of, int src_tier, void* stream);
+
 /* ---- build metadata ---------------------------------------------------- */
 /*
  * Device-visible address of pinned host memory (allocated by hipHostMalloc,

@@ -107,8 +107,11 @@ def test_demote_flush_and_tensor_indices(small_config, storage_factory):
 
 def test_chunked_cache_peels_and_counts():
     """Warm-up keeps everything; the first 1-token step past 2*chunk_size
-    peels all but recent_window rows into chunk_size host chunks; later steps
-    peel once the recent rows exceed recent_window + chunk_size."""
+    peels all but recent_window rows into chunk_size host chunks (with their
+    global positions and per-chunk key sums); later steps peel once the
+    recent rows exceed recent_window + chunk_size."""
+    import numpy as np
+
     from halo_amd import HALOCacheChunked, HALOConfig
     cfg = HALOConfig(chunk_size=16, recent_window=4, block_size=4)
     cache = HALOCacheChunked(config=cfg, chunk_size=16, recent_window=4)
@@ -120,15 +123,62 @@ def test_chunked_cache_peels_and_counts():
     assert cache._mode == "chunked" and K.shape[-2] == 4
     assert cache.get_seq_length(0) == 41
     cold = cache._cold[0]
-    assert cold.rows == 37 and [c.shape[-2] for c, _, _ in cold.chunks()] == [16, 16, 5]
-    got = torch.cat([c for c, _, _ in cold.chunks()], dim=-2)
+    assert cold.rows == 37 and [c.n for c in cold.chunks] == [16, 16, 5]
+    got = torch.cat([c.k[..., :c.n, :] for c in cold.chunks], dim=-2)
     assert torch.equal(got, k[..., :37, :])
+    assert np.array_equal(np.concatenate([c.pos[:c.n] for c in cold.chunks]), np.arange(37))
+    assert np.array_equal(cache._gpu_pos[0], np.arange(37, 41))
+    means = cache.cold_chunk_means(0)
+    want = torch.stack([k[..., 0:16, :].mean(-2), k[..., 16:32, :].mean(-2), k[..., 32:37, :].mean(-2)], dim=2)
+    torch.testing.assert_close(means, want, rtol=1e-6, atol=1e-6)
     for _ in range(16):
         cache.update(torch.randn(1, 2, 1, 8), torch.randn(1, 2, 1, 8), 0)
-    assert cache.get_seq_length(0) == 57 and cache._k[0].shape[-2] <= 4 + 16
+    assert cache.get_seq_length(0) == 57 and cache.layers[0].keys.shape[-2] <= 4 + 16
     assert cache.demoted_blocks_total > 0
     cache.reset()
     assert cache.get_seq_length(0) == 0 and cache._mode == "warmup"
+
+
+def test_chunked_cache_is_a_transformers_cache():
+    """The Path-D cache speaks transformers' Cache protocol (the reference
+    derives it from DynamicCache, halo/kv_cache.py:69)."""
+    pytest.importorskip("transformers")
+    from transformers.cache_utils import Cache
+
+    from halo_amd import HALOCacheChunked
+    cache = HALOCacheChunked(chunk_size=16, recent_window=4)
+    assert isinstance(cache, Cache)
+    cache.update(torch.randn(1, 2, 10, 8), torch.randn(1, 2, 10, 8), 0)
+    assert cache.get_seq_length() == 10 and cache.get_mask_sizes(1, 0) == (11, 0)
+
+
+def test_warmup_attention_matches_unwrapped_model():
+    """Before any peel the halo_chunked interface is one-shot attention with
+    the model's mask: a wrapped tiny Qwen2 (fp32, CPU) gives the unwrapped
+    model's logits, with and without left padding (reference
+    tests/test_chunked_wrap_integration.py:72-101)."""
+    pytest.importorskip("transformers")
+    from transformers import AutoModelForCausalLM
+    from transformers.models.qwen2 import Qwen2Config
+
+    from halo_amd import HALOConfig, wrap_with_halo
+    cfg = Qwen2Config(vocab_size=256, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512,
+                      tie_word_embeddings=False, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    model = AutoModelForCausalLM.from_config(cfg).eval()
+    ids = torch.randint(5, 250, (2, 48), generator=torch.Generator().manual_seed(1))
+    mask = torch.ones_like(ids)
+    mask[1, :7] = 0
+    with torch.no_grad():
+        ref = model(ids, attention_mask=mask, use_cache=False).logits
+    wrap_with_halo(model, HALOConfig(chunked=True, chunk_size=32, recent_window=8))
+    assert model.config._attn_implementation == "halo_chunked"
+    cache = model._halo_cache
+    with torch.no_grad():
+        got = model(ids, attention_mask=mask, past_key_values=cache, use_cache=True).logits
+    assert cache._mode == "warmup" and cache.get_seq_length() == 48
+    torch.testing.assert_close(got, ref, rtol=0, atol=1e-5)
 
 
 def test_wrap_with_halo_attaches_components():

@@ -91,16 +91,16 @@ def test_chunked_cache_decode_and_prefill(dev, dtype):
         cache.update(kg[:, :, t:t + 1], vg[:, :, t:t + 1], 0)
     assert cache._mode == "chunked" and cache.get_seq_length(0) == T0 + 3
     q = round_to(rng.standard_normal((B, H, 1, D)).astype(np.float32), nm)
-    out = cache.compute_attention(torch.from_numpy(q).to(dev).to(dtype), 0)
+    out = cache.compute_attention(torch.from_numpy(q).to(dev).to(dtype), layer_idx=0)
     torch.cuda.synchronize()
     ro, _ = A.attention_f64(q[:, :, 0], ks, vs, scale=1 / math.sqrt(D))
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert np.abs(out[:, :, 0].float().cpu().numpy() - ro).max() <= tol
+    st = cache.last_stats
+    assert st.cold_positions + st.hot_positions == T0 + 3 and st.used_lse_merge
     tel = cache.telemetry()
-    assert tel["cold_positions"] + tel["hot_positions"] == T0 + 3 and tel["used_lse_merge"]
-    if dtype == torch.bfloat16:
-        qp = round_to(rng.standard_normal((B, H, 20, D)).astype(np.float32), nm)
-        outp = cache.compute_attention(torch.from_numpy(qp).to(dev).to(dtype), 0)
-        torch.cuda.synchronize()
-        rp, _ = A.prefill_f64(qp, ks, vs, scale=1 / math.sqrt(D), q_start=T0 + 3 - 20)
-        assert np.abs(outp.float().cpu().numpy() - rp).max() <= 2e-2
+    assert tel["mode"] == "chunked" and tel["cold_positions_per_layer_max"] == st.cold_positions
+    qp = round_to(rng.standard_normal((B, H, 20, D)).astype(np.float32), nm)
+    outp = cache.compute_attention(torch.from_numpy(qp).to(dev).to(dtype), layer_idx=0)
+    rp, _ = A.prefill_f64(qp, ks, vs, scale=1 / math.sqrt(D), q_start=T0 + 3 - 20)
+    assert np.abs(outp.float().cpu().numpy() - rp).max() <= tol

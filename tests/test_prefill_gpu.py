@@ -66,9 +66,17 @@ def test_prefill_chunk_order_and_partition_invariance(dev):
     assert (la - lb).abs().max().item() <= 1e-3
 
 
-def test_prefill_rejects_fp32(dev):
+def test_prefill_fp32_runs_on_the_decode_path(dev):
+    """fp32 queries are accepted (the reference computes any T_q in fp32,
+    halo/kv_cache_chunked.py:241-276) and match the float64 closed form."""
     from halo_amd.decode import ChunkRef
     from halo_amd.prefill import prefill_attention
-    k = torch.zeros((1, 2, 64, 64), device=dev)
-    with pytest.raises(AssertionError):
-        prefill_attention(torch.zeros((1, 2, 16, 64), device=dev), [ChunkRef(k, k, 0, True)])
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((1, 4, 16, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 80, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 80, 64)).astype(np.float32)
+    kd, vd = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    out = prefill_attention(torch.from_numpy(q).to(dev), [ChunkRef(kd[:, :, :64], vd[:, :, :64], 0, True),
+                                                          ChunkRef(kd[:, :, 64:], vd[:, :, 64:], 64, True)])
+    want, _ = A.prefill_f64(q, k, v, scale=1 / math.sqrt(64), q_start=80 - 16)
+    assert np.abs(out.cpu().numpy() - want).max() <= 1e-5

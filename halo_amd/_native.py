@@ -72,6 +72,8 @@ _SIGNATURES = {
     "halo_decode_attn": (_i32, _DECODE_ARGS + [_c_void_p]),                      # + stream
     "halo_decode_attn_tiered": (_i32, _DECODE_ARGS + [ctypes.POINTER(SelectCfg), _c_void_p]),  # + sel, stream
     "halo_decode_attn_kivi": (_i32, _DECODE_ARGS + [_c_void_p]),                 # + stream
+    "halo_decode_static_scratch_bytes": (_size_t, []),
+    "halo_decode_attn_noalloc": (_i32, _DECODE_ARGS[:-2] + [ctypes.POINTER(SelectCfg), _c_void_p]),  # sel, stream
     "halo_finalize": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32,
                              _c_void_p, _i32, _c_void_p, _c_void_p]),
     "halo_lse_merge": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "../../include/halo_hip.h"

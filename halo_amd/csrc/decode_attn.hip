@@ -2088,6 +2088,76 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split-K partials live in a file-scope device
+// array instead of a caller workspace.  Each GPU holds its own copy of the
+// array for the life of the process; its device address is looked up once
+// per device (with that device current) and kept, and only that address is
+// handed to kernels -- the array's name is a host-side stand-in.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream).
+int scratch_address(hipStream_t stream, void** out) {
+  int cur = 0;
+  HALO_CHECK_HIP(hipGetDevice(&cur));
+  int dev = cur;
+  if (stream != nullptr) HALO_CHECK_HIP(hipStreamGetDevice(stream, &dev));
+  HALO_CHECK_ARG(dev >= 0 && dev < kScratchDevices, "device index out of range for the static scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) HALO_CHECK_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) HALO_CHECK_HIP(hipSetDevice(cur));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return HALO_E_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HALO_OK;
+}
+}  // namespace
+
+extern "C" size_t halo_decode_static_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int halo_decode_attn_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                        int B, int H, int H_kv, int D, int rep_t,
+                                        const halo_chunk_desc* descs, int n_desc,
+                                        const int32_t* work, int n_work,
+                                        const int32_t* group_offsets, int n_groups,
+                                        const int64_t* q_pos, float scale,
+                                        float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                                        void* out, int out_dtype, float* lse,
+                                        const halo_select_cfg* sel, void* stream) {
+  HALO_CHECK_ARG(n_work > 0 && rep_t > 0 && D > 0, "empty chunk table");
+  const size_t need = halo_decode_workspace_size(n_work, rep_t, D);
+  if (need > kScratchBytes) {
+    set_error("halo_decode_attn_noalloc: " + std::to_string(need) + " bytes of partials for " +
+              std::to_string(n_work) + " work items exceed the static scratch of " + std::to_string(kScratchBytes) +
+              " bytes; use halo_decode_attn / halo_decode_attn_tiered with a workspace");
+    return HALO_E_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(reinterpret_cast<hipStream_t>(stream), &ws);
+  if (rc != HALO_OK) return rc;
+  return decode_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, rep_t, descs, n_desc, work, n_work,
+                     group_offsets, n_groups, q_pos, scale, m, l, o, acc_stride_b, acc_mode, out, out_dtype, lse,
+                     ws, kScratchBytes, sel, false, stream);
+}
+
 extern "C" int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
                                 int B, int H, int H_kv, int D, int rep_t,
                                 const halo_chunk_desc* descs, int n_desc,

@@ -375,13 +375,16 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
            o: Optional[torch.Tensor] = None, acc_mode: int = 0,
            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
            stream: Optional[torch.cuda.Stream] = None, select=None,
-           workspace: Optional[torch.Tensor] = None) -> None:
+           workspace: Optional[torch.Tensor] = None, noalloc: bool = False) -> None:
     """Enqueue one ``halo_decode_attn`` on ``stream`` (default: current).
 
     ``select`` (a ``_native.SelectCfg``) enqueues ``halo_decode_attn_tiered``
     instead: the table's selection slots choose their chunks in-kernel.
     ``workspace`` (a uint8 device tensor) replaces the plan's own partial
-    buffer, for a second concurrent launch of the same plan."""
+    buffer, for a second concurrent launch of the same plan.  ``noalloc``
+    enqueues ``halo_decode_attn_noalloc`` instead: the partials go to the
+    library's static device scratch (no workspace at all; launches that
+    overlap on one GPU must not use it)."""
     L = nat.lib()
     if q.dim() != 3 or tuple(q.shape) != (plan.B, plan.H, plan.D):
         raise AssertionError(f"expected q (B, H, D) = {(plan.B, plan.H, plan.D)}, got {tuple(q.shape)}")
@@ -413,6 +416,17 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         if t is not None and t.device != q.device:
             raise AssertionError("all tensors must be on the query's device")
     sp = nat.stream_ptr(stream)
+    if noalloc:
+        if plan.kivi:
+            raise AssertionError("the allocation-free entry point covers plain and tiered tables, not KIVI")
+        head = (q.data_ptr(), q.stride(0), q.stride(1), nat.dtype_code(plan.dtype),
+                plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t, plan.descs.data_ptr(), plan.n_desc,
+                plan.work.data_ptr(), plan.n_work, None if plan.uniform_groups else plan.offsets.data_ptr(),
+                plan.n_groups, nat.ptr(q_pos), float(scale), nat.ptr(m), nat.ptr(l), nat.ptr(o), plan.H, acc_mode,
+                nat.ptr(out), nat.dtype_code(out.dtype) if out is not None else 0, nat.ptr(lse))
+        nat.check(L.halo_decode_attn_noalloc(*head, ctypes.byref(select) if select is not None else None, sp),
+                  "halo_decode_attn_noalloc")
+        return
     nbytes = int(L.halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
     ws = plan_workspace(plan, q.device) if workspace is None else workspace
     if ws.dtype != torch.uint8 or ws.device != q.device or ws.numel() < nbytes:

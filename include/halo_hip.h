@@ -172,6 +172,32 @@ int halo_decode_attn_tiered(const void* q, int64_t q_stride_b, int64_t q_stride_
                             const halo_select_cfg* sel, void* stream);
 
 /*
+ * Allocation-free variant of halo_decode_attn_tiered (sel != NULL) and
+ * halo_decode_attn (sel == NULL): same arguments and results, but the split-K
+ * partials go to a static device array inside the library instead of a
+ * caller workspace, so the caller passes only inputs and outputs.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Each GPU holds one copy of the array,
+ * halo_decode_static_scratch_bytes() bytes (8 MiB), until the process ends;
+ * a table whose partials (halo_decode_workspace_size) exceed it is refused
+ * with HALO_E_WORKSPACE before anything is launched.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams) race.
+ * Nothing in the array needs clearing between calls (every work item writes
+ * its own partial before the merge reads it).
+ */
+size_t halo_decode_static_scratch_bytes(void);
+int halo_decode_attn_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                             int B, int H, int H_kv, int D, int rep_t,
+                             const halo_chunk_desc* descs, int n_desc,
+                             const int32_t* work, int n_work,
+                             const int32_t* group_offsets, int n_groups,
+                             const int64_t* q_pos, float scale,
+                             float* m, float* l, float* o, int64_t acc_stride_b, int acc_mode,
+                             void* out, int out_dtype, float* lse,
+                             const halo_select_cfg* sel, void* stream);
+
+/*
  * finalize: out = o / (l > 0 ? l : 1) cast to out_dtype, optional
  * lse = m + log(l).  Replaces halo/triton_chunked.py:195-207 (which does not
  * return the LSE).  m,l: (B,H) fp32 contiguous, o: (B,H,D) fp32 contiguous.

@@ -1,18 +1,25 @@
 """Decode-attention throughput of the tiered-KV path on one MI355X.
 
-Workload (default): Llama-3-8B-shaped GQA decode, bf16, batch 1, 32 query
+Workload (headline): Llama-3-8B-shaped GQA decode, bf16, batch 1, 32 query
 heads / 8 KV heads, head dim 128, 32768 cached tokens in 32 chunks of 1024,
-hot_ratio 0.25 (the last 8 chunks), 24 cold chunks of which the scorer
-selects the top 4 per layer per step by mean-key dot product; keys carry 4
-planted high-variance channels (sigma 8).  32 layers with distinct buffers
-(4 GiB of K/V in HBM, far above the 256 MB last-level cache).  One step =
-for every layer: the split-K attention kernel over the hot chunks and 4
-selection slots (whose workgroups first score the 24 cold chunks' mean keys
-and pick the top 4 in-kernel), then the split-K merge kernel; the 64
-launches are replayed from one HIP graph.  Inputs are resident in HBM when the timed region starts (the
-cold chunks' HBM copies stand for their refetched state); the rate with the
-top-4 refetched over PCIe every step is measured separately and reported as
-``pcie_inclusive``.
+hot_ratio 0.25 (the last 8 chunks, in HBM), 24 cold chunks per layer in
+pinned host memory, of which the scorer selects the top 4 per layer per step
+by mean-key dot product inside the attention launch; keys carry 4 planted
+high-variance channels (sigma 8); 32 layers with distinct buffers.  Each
+layer's query follows a seeded drifting trajectory (AR(1) in fp32:
+q_t = rho q_{t-1} + sqrt(1 - rho^2) e_t, rho 0.98), so the selection moves
+from step to step.  A selected chunk is read from an HBM staging slot when
+the staging cache holds it (12 slots per layer, refilled by hipMemcpyAsync on
+a side stream from the returned scores) and in place over the host link
+otherwise.  One step = the next query written to HBM, the commits of landed
+fills, the 64 launches of the 32 layers replayed from one HIP graph, and the
+score read-back with the cache's policy -- all inside the timed region;
+tokens/s = 1 / step time, with the hit rate and the host-link bytes.
+
+Beside it: the same layers with every cold chunk resident in HBM
+(kernel-level roofline of the attention launch), the same workload with no
+staging cache (every selected chunk read over the link), and the other
+configurations (chunked prefill, ragged batch, KIVI cold tier).
 
 Prints one JSON line.  ``--gpus N`` with N > 1 exits: this build measures
 one GPU.
@@ -125,132 +132,99 @@ def cpu_baseline(torch, kvs, qs, layers, *, chunk, n_hot, top_k, L, budget_s):
     }
 
 
-def pcie_inclusive(torch, layers, qs, *, steps, scale):
-    """Every selected cold chunk refetched host->device every step: cold
-    chunks live in pinned host memory, the scorer's choice is read back, the
-    4 chunks are copied with hipMemcpyAsync on the copy stream into HBM
-    staging slots while the hot chunks are attended, then merged."""
-    from halo_amd.decode import ChunkRef, build_plan, launch
-    from halo_amd.memory_tier import copy_stream
-    from halo_amd.triton_chunked import init_acc
-
-    dev = qs[0].device
-    L = len(layers)
-    H, D = layers[0].H, layers[0].D
-    cs = copy_stream(dev)
-    compute = torch.cuda.current_stream()
-    host = []
-    for lay in layers:
-        hk = [c.k.cpu().pin_memory() for c in lay.cold]
-        hv = [c.v.cpu().pin_memory() for c in lay.cold]
-        host.append((hk, hv))
-    shape = tuple(layers[0].cold[0].k.shape)
-    slots = [(torch.empty(shape, device=dev, dtype=torch.bfloat16), torch.empty(shape, device=dev, dtype=torch.bfloat16))
-             for _ in range(layers[0].top_k)]
-    hot_plans = [build_plan(B=1, H=H, H_kv=lay.H_kv, D=D, dtype=torch.bfloat16, chunks=lay.hot, device=dev)
-                 for lay in layers]
-    slot_plans = [build_plan(B=1, H=H, H_kv=layers[0].H_kv, D=D, dtype=torch.bfloat16,
-                             chunks=[ChunkRef(sk, sv, 0, False) for (sk, sv) in slots], device=dev)]
-    out = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
-    ev_copy = torch.cuda.Event()
-    nbytes = 0
-
-    def step():
-        nonlocal nbytes
-        for li, lay in enumerate(layers):
-            q = qs[li]
-            lay.select(q)
-            ids = lay.idx[0].cpu().tolist()
-            cs.wait_stream(compute)
-            with torch.cuda.stream(cs):
-                for s, c in enumerate(ids):
-                    slots[s][0].copy_(host[li][0][c], non_blocking=True)
-                    slots[s][1].copy_(host[li][1][c], non_blocking=True)
-                    nbytes += 2 * host[li][0][c].numel() * 2
-                ev_copy.record(cs)
-            m, l_, o = init_acc(B=1, H=H, D_v=D, device=dev)
-            launch(hot_plans[li], q, scale=scale, m=m, l=l_, o=o, acc_mode=2)
-            compute.wait_event(ev_copy)
-            launch(slot_plans[0], q, scale=scale, m=m, l=l_, o=o, acc_mode=1, out=out)
-
-    step()
-    torch.cuda.synchronize()
-    nbytes = 0
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    # pinned H2D peak on this box: one 64 MiB copy stream-ordered, repeated
-    big_h = torch.empty(64 << 20, dtype=torch.uint8).pin_memory()
-    big_d = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-    for _ in range(2):
-        big_d.copy_(big_h, non_blocking=True)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for _ in range(10):
-        big_d.copy_(big_h, non_blocking=True)
-    torch.cuda.synchronize()
-    h2d_peak = 10 * (64 << 20) / (time.perf_counter() - t1) / 1e9
-    res = {
-        "tokens_per_s": 1.0 / dt,
-        "ms_per_step": dt * 1e3,
-        "refetch_bytes_per_step": nbytes // steps,
-        "link_gbps": nbytes / steps / dt / 1e9,
-        "h2d_pinned_peak_gbps": h2d_peak,
-        "policy": "every layer's top-4 refetched from pinned host memory every step (no staging-cache hits)",
-        "refetch": "host reads the selection, hipMemcpyAsync of the 4 chunks on a copy stream, hot chunks attended meanwhile",
-    }
-    res["in_kernel"] = zero_copy_refetch(torch, layers, qs, host, steps=steps, scale=scale)
-    return res
-
-
-def zero_copy_refetch(torch, layers, qs, host, *, steps, scale):
-    """The same worst-case policy with the refetch inside the attention
-    launch: the cold catalog points at the pinned host chunks (their
-    device-visible addresses), so the selection workgroups stream the chosen
-    chunks over the host link while the hot workgroups read HBM; no host
-    round trip, one HIP graph for the 32-layer step."""
+def host_tier(torch, layers):
+    """The cold chunks of every layer as contiguous pinned host tensors (the
+    cold tier), copied from their HBM originals."""
     from halo_amd.decode import ChunkRef
-    from halo_amd.tiered import TieredDecodeLayer
+    tiers = []
+    for lay in layers:
+        cold = []
+        for c in lay.cold:
+            hk = torch.empty(tuple(c.k.shape), dtype=c.k.dtype, pin_memory=True)
+            hv = torch.empty(tuple(c.v.shape), dtype=c.v.dtype, pin_memory=True)
+            hk.copy_(c.k)
+            hv.copy_(c.v)
+            cold.append(ChunkRef(hk, hv, c.chunk_start, c.causal))
+        tiers.append(cold)
+    return tiers
 
-    dev = qs[0].device
-    L = len(layers)
-    zl = []
-    for li, lay in enumerate(layers):
-        cold = [ChunkRef(host[li][0][j], host[li][1][j], c.chunk_start, c.causal) for j, c in enumerate(lay.cold)]
-        zl.append(TieredDecodeLayer(B=1, H=lay.H, H_kv=lay.H_kv, D=lay.D, dtype=lay.dtype, hot=lay.hot, cold=cold,
-                                    top_k=lay.top_k, device=dev, cold_kmean=lay.kmean))
-    outs = [torch.empty((1, lay.H, lay.D), device=dev, dtype=lay.dtype) for lay in layers]
 
-    def step():
-        for li in range(L):
-            zl[li].step(qs[li], scale=scale, out=outs[li])
+def query_trajectory(torch, dev, *, steps, L, H, D, rho, seed):
+    """Per-layer AR(1) query drift in fp32, rounded to bf16:
+    q_0 ~ N(0, 1), q_t = rho q_{t-1} + sqrt(1 - rho^2) e_t.  (steps, L, 1, H, D)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    q = torch.randn((L, 1, H, D), generator=gen, device=dev)
+    out = torch.empty((steps, L, 1, H, D), device=dev, dtype=torch.bfloat16)
+    c = math.sqrt(max(0.0, 1.0 - rho * rho))
+    for t in range(steps):
+        q = rho * q + c * torch.randn((L, 1, H, D), generator=gen, device=dev)
+        out[t] = q.to(torch.bfloat16)
+    return out
 
+
+def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, warm_fills=None, segments=4):
+    """Timed decode steps over the staged layers.  A step writes the next
+    queries, then runs the layers as ``segments`` consecutive HIP graphs;
+    before each segment the fills that landed for its layers are committed,
+    after it its scores go back to the host, and while the next segment runs
+    the host plans the previous segment's fills (so they have one step to
+    land).  Returns the reading."""
+    dev = qtraj.device
+    L = len(staged)
+    H, D = staged[0].H, staged[0].D
+    qbuf = torch.empty((L, 1, H, D), device=dev, dtype=torch.bfloat16)
+    outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    bounds = [(g * L // segments, (g + 1) * L // segments) for g in range(segments)]
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
+    n_traj = qtraj.shape[0]
+    graphs = []
     with torch.cuda.stream(s):
-        step()
+        qbuf.copy_(qtraj[0])
+        for li in range(L):
+            staged[li].step(qbuf[li], scale=scale, out=outs[li])
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            step()
-        g.replay()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(steps):
-            g.replay()
-        e1.record(s)
-    torch.cuda.synchronize()
-    dt = e0.elapsed_time(e1) / 1e3 / steps
-    per_chunk = 2 * host[0][0][0].numel() * host[0][0][0].element_size()
-    nbytes = L * layers[0].top_k * per_chunk
+        for lo, hi in bounds:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for li in range(lo, hi):
+                    staged[li].step(qbuf[li], scale=scale, out=outs[li])
+            graphs.append(g)
+        torch.cuda.synchronize()
+        t0 = 0.0
+        budget = staging.max_inflight
+        if warm_fills is not None:
+            staging.max_inflight = warm_fills   # the warm-up may fill the empty cache faster
+        for t in range(warmup + steps):
+            if t == warmup:
+                staging.drain()
+                torch.cuda.synchronize()
+                staging.max_inflight = budget
+                staging.reset_counters()
+                t0 = time.perf_counter()
+            for (lo, hi), g in zip(bounds, graphs):
+                staging.before_step(lo, hi)
+                if lo == 0:
+                    qbuf.copy_(qtraj[t % n_traj], non_blocking=True)
+                g.replay()
+                staging.after_step(lo, hi)
+                staging.service()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        staging.drain()      # count the last steps' selections too
+    del graphs
+    sel = staging.hits + staging.misses
+    link = (staging.fill_bytes + staging.miss_bytes) / steps
+    log(f"{label}: {dt * 1e3:.3f} ms/step, hit rate {staging.hit_rate():.4f} over {sel} selections, "
+        f"{staging.fills / steps:.2f} fills/step, link {link / 2**20:.1f} MiB/step")
     return {
-        "tokens_per_s": 1.0 / dt,
-        "ms_per_step": dt * 1e3,
-        "refetch_bytes_per_step": nbytes,
-        "link_gbps": nbytes / dt / 1e9,
-        "refetch": "selected cold chunks read in place from pinned host memory by the attention kernel (no host sync)",
+        "tokens_per_s": 1.0 / dt, "ms_per_step": dt * 1e3, "hit_rate": staging.hit_rate(),
+        "selections": sel, "hits": staging.hits, "misses": staging.misses,
+        "fills_per_step": staging.fills / steps,
+        "prefetch_bytes_per_step": staging.fill_bytes / steps,
+        "in_place_miss_bytes_per_step": staging.miss_bytes / steps,
+        "link_bytes_per_step": link, "link_gbps": link / dt / 1e9, "segments": segments,
     }
 
 
@@ -418,17 +392,22 @@ def bench_ragged_c4(torch, dev, *, steps: int):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200, help="timed decode steps of the headline")
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--rho", type=float, default=0.98, help="per-step correlation of the query trajectory")
+    ap.add_argument("--slots", type=int, default=12, help="HBM staging slots per layer (of the 24 cold chunks)")
+    ap.add_argument("--keep", type=int, default=6, help="best-scoring chunks per layer the cache stages")
+    ap.add_argument("--max-inflight", type=int, default=16, help="host-to-device chunk copies in flight at once")
+    ap.add_argument("--segments", type=int, default=4, help="graphs per step (layer segments) of the headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-pcie", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the drift / no-staging comparison legs")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the prefill (MFMA) and KIVI cold-tier measurements")
+                    help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
     ap.add_argument("--unfused", action="store_true",
-                    help="select with the standalone scorer kernel instead of in the attention kernel")
+                    help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not run (how the path shards across "
@@ -438,48 +417,44 @@ def main() -> int:
     import torch
 
     from halo_amd import _native
+    from halo_amd.staging import ColdStaging
+    from halo_amd.tiered import TieredDecodeLayer
 
     _native.lib()
     dev = torch.device("cuda:0")
     L, H, H_kv, D, T, chunk, n_hot, top_k = args.layers, 32, 8, 128, 32768, 1024, 8, 4
+    n_cold = T // chunk - n_hot
     scale = 1.0 / math.sqrt(D)
     log(f"building {L} layers of K/V ({L * 2 * H_kv * T * D * 2 / 2**30:.1f} GiB)")
     layers, qs, kvs = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
                                   n_planted=4, sigma=8.0, dev=dev, seed=1, split=args.split,
                                   fused=not args.unfused)
+    # algorithmic bytes of one layer's attention launch: K+V rows of hot +
+    # selected chunks, q, out and lse, plus the cold chunks' mean keys it scores
+    rows = layers[0].attended_rows
+    score_bytes = n_cold * H_kv * D * 2
+    attn_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4 + score_bytes
+    step_bytes = L * attn_bytes
+
+    # ---------------------------------------------------------------- headline
+    log("cold tier: copying 24 chunks per layer to pinned host memory")
+    tiers = host_tier(torch, layers)
+    staged = [TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=lay.hot, cold=tiers[li],
+                                top_k=top_k, device=dev, cold_kmean=lay.kmean, split=args.split)
+              for li, lay in enumerate(layers)]
+    staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight)
+    n_traj = args.warmup + args.steps
+    qtraj = query_trajectory(torch, dev, steps=n_traj, L=L, H=H, D=D, rho=args.rho, seed=11)
+    head = refetch_run(torch, staged, staging, qtraj, warmup=args.warmup, steps=args.steps, scale=scale,
+                       label=f"staged, rho {args.rho}", warm_fills=10 ** 6, segments=args.segments)
+    dt = head["ms_per_step"] * 1e-3
+
+    # ------------------------------------------------- kernel-level (all HBM)
     outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
     lses = [torch.empty((1, H), device=dev, dtype=torch.float32) for _ in range(L)]
-
-    def step():
-        for li in range(L):
-            layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li])
-
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            step()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    log("graph captured; warmup")
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        g.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
-    log(f"timed {args.steps} steps: {dt * 1e3:.3f} ms/step")
 
-    # Per-kernel durations with HIP events on the launch stream.  Host-side
-    # launch latency would inflate per-launch event pairs, so the attention
-    # launches (split-K kernel + merge kernel) and the scorer launches are each
-    # captured in a graph of their own and timed over whole replays on the
-    # capture stream.
     def capture(fn):
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.stream(s):
@@ -489,11 +464,6 @@ def main() -> int:
                 fn()
         torch.cuda.synchronize()
         return gr
-
-    # one layer's launch pair: attention with in-kernel selection + merge
-    g_attn = capture(lambda: [layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li]) for li in range(L)])
-    # the standalone scorer kernel (plug-in API path), for reference
-    g_score = capture(lambda: [layers[li].select(qs[li]) for li in range(L)])
 
     def time_graph(gr, reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -506,18 +476,15 @@ def main() -> int:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / (reps * L)
 
-    reps = max(5, min(args.steps, 50))
-    attn_avg = time_graph(g_attn, reps)
+    g_attn = capture(lambda: [layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li]) for li in range(L)])
+    g_score = capture(lambda: [layers[li].select(qs[li]) for li in range(L)])
+    reps = 50
+    attn_avg = time_graph(g_attn, reps)          # ms per layer: attention kernel + merge kernel
     score_avg = time_graph(g_score, reps)
-    rows = layers[0].attended_rows
-    # algorithmic bytes of one layer's launch: K+V rows of hot + selected
-    # chunks, q, out and lse, plus the cold chunks' mean keys it scores
-    score_bytes = (T // chunk - n_hot) * H_kv * D * 2
-    attn_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4 + (score_bytes if layers[0].fused else 0)
     achieved = attn_bytes / (attn_avg * 1e-3) / 1e9
-    step_bytes = L * (attn_bytes if layers[0].fused else attn_bytes + score_bytes + H * D * 2)
-    log(f"attention launch avg {attn_avg * 1e3:.2f} us ({achieved:.0f} GB/s), "
-        f"standalone scorer {score_avg * 1e3:.2f} us")
+    log(f"kernel-level (all HBM): attention launch avg {attn_avg * 1e3:.2f} us ({achieved:.0f} GB/s), "
+        f"{1.0 / (attn_avg * 1e-3 * L):.0f} tokens/s; standalone scorer {score_avg * 1e3:.2f} us")
+    del g_attn, g_score
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "decode_attn_c2_traffic.json")
@@ -539,23 +506,28 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (N(0,1) q/k/v, 4 planted key channels sigma 8, random init)",
+        "data": "synthetic (N(0,1) k/v, 4 planted key channels sigma 8, AR(1) query drift rho "
+                f"{args.rho}, random init)",
         "config": {
-            "workload": "Llama-3-8B-shaped GQA decode, 32 layers looped, batch 1, 32/8 heads, d128, "
-                        "32768 ctx in 32x1024 chunks, 8 hot + top-4 of 24 cold by mean-key score",
+            "workload": "Llama-3-8B-shaped GQA decode, 32 layers looped, batch 1, 32/8 heads, d128, 32768 ctx in "
+                        "32x1024 chunks, 8 hot chunks in HBM + top-4 of 24 cold chunks in pinned host memory "
+                        "selected per layer per step by mean-key score, refetched through an HBM staging cache",
             "layers": L, "batch": 1, "q_heads": H, "kv_heads": H_kv, "head_dim": D, "ctx": T,
-            "chunk": chunk, "hot_chunks": n_hot, "top_k": top_k,
-            "launch": ("hip graph; per layer: attention kernel with in-kernel top-k selection + merge kernel"
-                       if layers[0].fused else "hip graph; per layer: scorer + attention + merge kernels"),
-            "split_rows": int(layers[0].plan.work_host[-1, 3] - layers[0].plan.work_host[-1, 2]),
-            "selection_split_rows": int(layers[0].plan.work_host[0, 3] - layers[0].plan.work_host[0, 2]),
-            "work_items": layers[0].plan.n_work,
+            "chunk": chunk, "hot_chunks": n_hot, "cold_chunks": n_cold, "top_k": top_k,
+            "query_drift_rho": args.rho, "staging_slots_per_layer": args.slots, "staging_keep": staging.keep,
+            "staging_bytes": staging.slot_bytes, "max_fills_in_flight": args.max_inflight,
+            "segments": args.segments,
+            "launch": "per step: query copy, fill commits, hip graph of 32 x (attention kernel with in-kernel "
+                      "top-k selection + merge kernel), score read-back, staging policy",
         },
         "hbm_gbps_end_to_end": step_bytes / dt / 1e9,
+        "hbm_frac_end_to_end": step_bytes / dt / 1e9 / HBM_PEAK_GBPS,
         "hbm_bytes_per_step": step_bytes,
+        "refetch": head,
         "roofline": {
             "bound": "hbm",
-            "kernel": "halo_decode_attn_tiered (decode_attn_kernel<bf16,128,4,4> + decode_merge_kernel<128,4>)",
+            "kernel": "halo_decode_attn_tiered (decode_attn_kernel<bf16,128,4,4> + decode_merge_kernel<128,4>), "
+                      "one C2 layer with every selected chunk in HBM (kernel level)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -563,23 +535,43 @@ def main() -> int:
             "traffic": traffic,
             "bytes_per_launch": attn_bytes,
             "avg_launch_us": attn_avg * 1e3,
+            "kernel_level_tokens_per_s": 1.0 / (attn_avg * 1e-3 * L),
             "standalone_scorer_avg_us": score_avg * 1e3,
         },
     }
+    if not args.no_sweep:
+        sweep = {}
+        for rho in (0.95, 0.99):
+            staging.clear()
+            qt = query_trajectory(torch, dev, steps=20 + 100, L=L, H=H, D=D, rho=rho, seed=12)
+            sweep[f"rho_{rho}"] = refetch_run(torch, staged, staging, qt, warmup=20, steps=100, scale=scale,
+                                              label=f"staged, rho {rho}", warm_fills=10 ** 6,
+                                              segments=args.segments)
+        # a larger cache (16 slots per layer) on the headline trajectory
+        big = ColdStaging(staged, n_slots=16, keep=args.keep, max_inflight=args.max_inflight)
+        sweep["slots_16"] = refetch_run(torch, staged, big, qtraj, warmup=args.warmup, steps=100, scale=scale,
+                                        label=f"staged, 16 slots, rho {args.rho}", warm_fills=10 ** 6,
+                                        segments=args.segments)
+        del big
+        staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight)
+        staging.clear()
+        budget = staging.max_inflight
+        staging.max_inflight = 0                # nothing staged: every selected chunk read over the host link
+        sweep["no_staging"] = refetch_run(torch, staged, staging, qtraj, warmup=3, steps=20, scale=scale,
+                                          label="no staging (in-place reads)", segments=args.segments)
+        staging.max_inflight = budget
+        result["refetch_sweep"] = sweep
     if not args.no_extra:
         extra = {}
         log("prefill leg")
-        extra["prefill_c3"] = bench_prefill_c3(torch, dev, reps=max(3, min(args.steps, 10)))
+        extra["prefill_c3"] = bench_prefill_c3(torch, dev, reps=10)
         log("ragged leg")
-        extra["ragged_c4"] = bench_ragged_c4(torch, dev, steps=max(3, min(args.steps, 20)))
+        extra["ragged_c4"] = bench_ragged_c4(torch, dev, steps=20)
         log("kivi leg")
-        del g, g_attn, g_score
+        del staging, staged
         torch.cuda.empty_cache()
-        extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=max(3, min(args.steps, 20)))
+        extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=20)
         result["extra"] = extra
-    if not args.no_pcie:
-        log("pcie-inclusive leg")
-        result["pcie_inclusive"] = pcie_inclusive(torch, layers, qs, steps=max(3, min(args.steps, 10)), scale=scale)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, kvs, qs, layers, chunk=chunk, n_hot=n_hot, top_k=top_k, L=L,

@@ -50,8 +50,15 @@ class SelectCfg(ctypes.Structure):
         ("n_cold", _i32), ("top_k", _i32), ("slot0", _i32), ("per_row", _i32),
         ("idx_out", _c_void_p),
         ("score_out", _c_void_p),
-        ("lead_items", _i32), ("reserved", _i32),
+        ("lead_items", _i32), ("n_slots", _i32),
+        ("slot_catalog", _c_void_p), ("residency", _c_void_p), ("res_out", _c_void_p),
     ]
+
+
+class Fill(ctypes.Structure):
+    """halo_fill (include/halo_hip.h)."""
+    _fields_ = [("dst_k", _c_void_p), ("src_k", _c_void_p), ("dst_v", _c_void_p), ("src_v", _c_void_p),
+                ("bytes", _i64)]
 
 
 _DECODE_ARGS = [
@@ -101,6 +108,8 @@ _SIGNATURES = {
     ]),
     "halo_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64,
                                 _c_void_p, _i32, _c_void_p]),
+    "halo_stage_fills": (_i32, [ctypes.POINTER(Fill), _i32, _c_void_p]),
+    "halo_store_i32": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "halo_host_device_pointer": (_i32, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "halo_last_error": (ctypes.c_char_p, []),
     "halo_build_info": (ctypes.c_char_p, []),

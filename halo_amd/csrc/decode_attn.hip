@@ -250,7 +250,13 @@ constexpr int kSelTPT = 2;  // (page, row, head) triples per thread: at most 2 x
 static_assert(sizeof(halo_chunk_desc) % 8 == 0, "descriptors are copied as 8-byte words");
 constexpr int kSelMaxQbar = 2048;
 constexpr int kSelQbarLds = kSelMaxQbar + 4 * 64;  // padded rows: at most 2048 / 64 rows of +4 floats
-constexpr int kSelBytes = kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4 + kSelMaxCold * (int)sizeof(halo_chunk_desc);
+constexpr int kSelMaxSlots = 64;  // HBM staging slots per selection
+// LDS of the selection: q-bar rows, dot products, scores, picks, then the
+// candidate descriptors, the staging-slot descriptors right after them (so
+// entry kSelMaxCold + r of the combined table is slot r) and the residency.
+constexpr int kSelCatOff = kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4;
+constexpr int kSelBytes = kSelCatOff + (kSelMaxCold + kSelMaxSlots) * (int)sizeof(halo_chunk_desc) + kSelMaxCold * 4;
+static_assert(sizeof(halo_select_cfg) == 120, "halo_select_cfg layout");
 
 __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
   halo_chunk_desc u;
@@ -298,6 +304,9 @@ struct Selector {
   static_assert((G & (G - 1)) == 0 && G <= kWave, "slices per row");
   uint4 kb[KU][PPS];          // page-mean pieces of this thread's first KU units
   uint2 cw[CW];               // this thread's share of the candidate descriptors
+  uint2 sw[CW];               // ... and of the staging-slot descriptors
+  int rres;                   // residency of candidate tid (tid < n), -1 without staging
+  int staged_slot;            // after finish(): staging slot of this slot's chunk, -1 when read in place
   // q pieces loaded up front, 8 x 16 bytes: per lane (qlane) the PPS pieces
   // of its own slice for the first QL query heads (qv[j * QL + h]), else the
   // first QB heads of the thread's share of the LDS-staged q-bar pieces
@@ -344,6 +353,16 @@ struct Selector {
       const int w = tid + k * NT;
       if (w < n * DW2) cw[k] = cat[w];
     }
+    rres = -1;
+    if (S.residency != nullptr) {
+      if (tid < n) rres = S.residency[(int64_t)sel * S.catalog_stride + tid];
+      const uint2* scat = reinterpret_cast<const uint2*>(S.slot_catalog + (int64_t)sel * S.n_slots);
+#pragma unroll
+      for (int k = 0; k < CW; ++k) {
+        const int w = tid + k * NT;
+        if (w < S.n_slots * DW2) sw[k] = scat[w];
+      }
+    }
     qlane = P.q_aligned && (NT / G) % nrh == 0;
     if (qlane) {
       const int rh = (tid / G) % nrh, sl = tid % G;
@@ -378,8 +397,10 @@ struct Selector {
   // order (products and sums rounded separately: D cut into G = D/16 slices,
   // slice s holding the 16-byte pieces s, s + G, ..., each slice summed in
   // order, then a balanced pairwise tree over the slices), max over (row, KV
-  // head), rank by (score desc, index asc).  Returns the chunk index for `slot` (-1: slot past the
-  // eligible count); the chosen descriptors are left in LDS at s_cat.
+  // head), rank by (score desc, index asc).  Returns the chunk index p for
+  // `slot` (-1: slot past the eligible count); the chunk's catalog entry is
+  // left in LDS at kSelCatOff and staged_slot names the staging slot that
+  // holds it (-1: none; its descriptor is entry kSelMaxCold + staged_slot).
   __device__ __forceinline__ int finish(const DecodeParams& P, char* smem, int slot, bool writer) {
     const halo_select_cfg& S = P.sel;
     const int tid = threadIdx.x;
@@ -389,6 +410,8 @@ struct Selector {
     float* s_sc = s_dot + kSelTPT * 256;  // per-candidate scores for the ranking (64, -inf past n)
     int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
     halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
+    halo_chunk_desc* s_slot = s_cat + kSelMaxCold;
+    int* s_res = reinterpret_cast<int*>(s_slot + kSelMaxSlots);
     // GQA-mean query rows: fp32 sum over the rep heads in head order, times
     // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
     auto qround = [&](float v) __attribute__((always_inline)) {
@@ -482,6 +505,15 @@ struct Selector {
     for (int k = 0; k < CW; ++k) {
       const int w = tid + k * NT;
       if (w < n * DW2) reinterpret_cast<uint2*>(s_cat)[w] = cw[k];
+    }
+    if (S.residency != nullptr) {
+#pragma unroll
+      for (int k = 0; k < CW; ++k) {
+        const int w = tid + k * NT;
+        if (w < S.n_slots * DW2) reinterpret_cast<uint2*>(s_slot)[w] = sw[k];
+      }
+      // an entry outside [0, n_slots) reads as "not staged"
+      if (tid < n) s_res[tid] = (rres >= 0 && rres < S.n_slots) ? rres : -1;
     }
     // the q-bar stage (not used by qlane) is read across waves; the catalog is
     // read after the ranking's barrier
@@ -608,10 +640,17 @@ struct Selector {
       if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
     }
     __syncthreads();
+    const bool staged = S.residency != nullptr;
     if (writer && S.idx_out) {
       for (int j = tid; j < S.top_k; j += NT) S.idx_out[(int64_t)sel * S.top_k + j] = j < kk ? s_pick[j] : -1;
     }
-    return __builtin_amdgcn_readfirstlane(slot < kk ? s_pick[slot] : -1);
+    if (writer && S.res_out) {
+      for (int j = tid; j < S.top_k; j += NT)
+        S.res_out[(int64_t)sel * S.top_k + j] = (j < kk && staged) ? s_res[s_pick[j]] : -1;
+    }
+    const int pick = slot < kk ? s_pick[slot] : -1;
+    staged_slot = __builtin_amdgcn_readfirstlane((pick >= 0 && staged) ? s_res[pick] : -1);
+    return __builtin_amdgcn_readfirstlane(pick);
   }
 };
 
@@ -1153,7 +1192,22 @@ decode_attn_kernel(DecodeParams P) {
     if (!early_sel) selr.issue(P, b);
     const int pick = selr.finish(P, smem, item.x - P.sel.slot0, writer);
     if (pick >= 0) {
-      dsc = uniform_desc(reinterpret_cast<const halo_chunk_desc*>(smem + kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4)[pick]);
+      // the chunk's own catalog entry (rows, start, flags); a staged chunk is
+      // read through its slot's addresses and strides
+      const halo_chunk_desc* tbl = reinterpret_cast<const halo_chunk_desc*>(smem + kSelCatOff);
+      halo_chunk_desc d = tbl[pick];
+      if (selr.staged_slot >= 0) {
+        const halo_chunk_desc& sd = tbl[kSelMaxCold + selr.staged_slot];
+        d.k = sd.k;
+        d.v = sd.v;
+        d.k_stride_b = sd.k_stride_b;
+        d.k_stride_h = sd.k_stride_h;
+        d.k_stride_t = sd.k_stride_t;
+        d.v_stride_b = sd.v_stride_b;
+        d.v_stride_h = sd.v_stride_h;
+        d.v_stride_t = sd.v_stride_t;
+      }
+      dsc = uniform_desc(d);
     } else {
       dsc = P.descs[item.x];
       dsc.T_c = 0;
@@ -2052,6 +2106,8 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
                    "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
     HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");
     HALO_CHECK_ARG(S.lead_items >= 0, "lead_items must be >= 0");
+    HALO_CHECK_ARG(S.residency == nullptr || (S.slot_catalog != nullptr && S.n_slots >= 1 && S.n_slots <= kSelMaxSlots),
+                   "staging needs slot_catalog and 1 <= n_slots <= 64");
     HALO_CHECK_ARG(S.n_cold * rows * H_kv <= kSelTPT * 256, "n_cold * rows * H_kv must be <= 512");
     HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
     HALO_CHECK_ARG(D % 16 == 0, "in-kernel selection needs head_dim % 16 == 0");

@@ -82,3 +82,54 @@ extern "C" int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, con
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Staging-cache helpers: a batch of host-to-device chunk copies in one call,
+// and a batch of int32 stores whose (index, value) pairs travel in the kernel
+// arguments (no host buffer has to outlive the call).
+// ---------------------------------------------------------------------------
+namespace halo {
+namespace {
+constexpr int kStorePairs = 32;
+struct StorePairs {
+  int64_t idx[kStorePairs];
+  int32_t val[kStorePairs];
+  int n;
+};
+
+__global__ void store_i32_kernel(int32_t* base, int64_t n_elems, StorePairs p) {
+  const int i = threadIdx.x;
+  if (i < p.n && p.idx[i] >= 0 && p.idx[i] < n_elems) base[p.idx[i]] = p.val[i];
+}
+}  // namespace
+}  // namespace halo
+
+extern "C" int halo_stage_fills(const halo_fill* fills, int n, void* stream) {
+  HALO_CHECK_ARG(n >= 0 && (n == 0 || fills != nullptr), "bad fill list");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int i = 0; i < n; ++i) {
+    const halo_fill& f = fills[i];
+    HALO_CHECK_ARG(f.bytes >= 0 && (f.bytes == 0 || (f.dst_k && f.src_k)), "fill: null pointer");
+    if (f.bytes == 0) continue;
+    HALO_CHECK_HIP(hipMemcpyAsync(f.dst_k, f.src_k, (size_t)f.bytes, hipMemcpyHostToDevice, st));
+    if (f.dst_v != nullptr) HALO_CHECK_HIP(hipMemcpyAsync(f.dst_v, f.src_v, (size_t)f.bytes, hipMemcpyHostToDevice, st));
+  }
+  return HALO_OK;
+}
+
+extern "C" int halo_store_i32(int32_t* base, int64_t n_elems, const int64_t* idx, const int32_t* vals, int n,
+                              void* stream) {
+  HALO_CHECK_ARG(n >= 0 && (n == 0 || (base && idx && vals)), "null pointer argument");
+  for (int i0 = 0; i0 < n; i0 += kStorePairs) {
+    StorePairs p;
+    p.n = n - i0 < kStorePairs ? n - i0 : kStorePairs;
+    for (int j = 0; j < kStorePairs; ++j) {
+      p.idx[j] = j < p.n ? idx[i0 + j] : -1;
+      p.val[j] = j < p.n ? vals[i0 + j] : 0;
+    }
+    hipLaunchKernelGGL(store_i32_kernel, dim3(1), dim3(kStorePairs), 0, static_cast<hipStream_t>(stream), base,
+                       n_elems, p);
+    HALO_CHECK_HIP(hipGetLastError());
+  }
+  return HALO_OK;
+}

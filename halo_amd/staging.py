@@ -1,0 +1,317 @@
+"""HBM staging cache for cold chunks kept in pinned host memory.
+
+A stack of tiered decode layers (``TieredDecodeLayer`` whose cold chunks
+live in pinned host DRAM) selects its top-k cold chunks inside the attention
+launch every step.  Without staging, every selected chunk is read in place
+over the host link.  This cache keeps up to ``n_slots`` cold chunks per layer
+in HBM slots and points the in-kernel selection at them through a per-chunk
+residency entry (``halo_select_cfg.residency``): a chosen chunk whose entry
+names a slot is read from HBM (a hit), otherwise in place from host memory
+(a miss, still exact: the rows are the same).
+
+Policy (reference: HALORefetcher.predict_hot / schedule,
+halo/refetcher.py:38-114 -- predict the next hot set as the top
+(hot + lookahead) by the last score and fetch what is missing on a side
+stream): the layers' chunk scores, written by the selection itself, come
+back to the host through a small pinned ring; the ``keep`` best-scoring
+chunks of each layer are the predicted set, and those not staged are copied
+host-to-device into free slots with ``hipMemcpyAsync`` on the copy stream,
+best ranks first across layers, at most ``max_inflight`` copies in flight.
+
+Ordering (no kernel observes a change while it runs):
+  * a fill copies the chunk's rows into a slot that no residency entry
+    names, on the copy stream, and records an event (slot descriptors never
+    change: the kernel takes a staged chunk's rows, start and flags from its
+    own catalog entry and only the addresses from the slot);
+  * a fill whose event has completed is committed before the next launches
+    of its layer: one batched store of residency entries on the compute
+    stream; every launch after it reads the slot, every launch before it read
+    host memory.  A fill still in flight is committed later (the compute
+    stream never waits for the link);
+  * an eviction stores -1 on the compute stream after the launches already
+    queued; the slot becomes free for a new fill only once an event
+    recorded after that store has completed, i.e. once every launch that
+    could have read the old entry has finished.
+A step may run as consecutive segments of layers (one graph each): a
+segment's scores are planned while the later segments execute, so the
+scores of step t can decide that segment's residency from step t + 1 on.
+Hit and miss counts come from ``res_out``: the entry the kernel actually
+used for each chosen chunk.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .decode import ChunkRef, descs_to_device, pack_descs
+from .memory_tier import copy_stream
+
+_FREE, _FILLING, _READY, _RELEASING = 0, 1, 2, 3
+
+
+class ColdStaging:
+    """HBM staging slots + residency for the cold chunks of ``layers``.
+
+    ``layers``: ``TieredDecodeLayer`` objects with the fused in-kernel
+    selection over cold chunks held as contiguous pinned host tensors, the
+    same number of cold chunks each.  ``n_slots`` HBM slots per layer (each
+    the size of the layer's widest cold chunk); ``keep`` best-scoring chunks
+    per layer are staged (default n_slots - 2, so fills in flight and slots
+    waiting for release have room); ``max_inflight`` bounds the copies in
+    flight on the link."""
+
+    def __init__(self, layers: Sequence, *, n_slots: int = 12, keep: Optional[int] = None,
+                 max_inflight: int = 8, ring: int = 16) -> None:
+        if not layers:
+            raise AssertionError("no layers")
+        self.layers = list(layers)
+        lay0 = self.layers[0]
+        self.device = lay0.plan.descs.device
+        self.n_cold = len(lay0.cold)
+        self.top_k = lay0.top_k
+        if not 1 <= n_slots <= 64:
+            raise AssertionError("n_slots must be in [1, 64]")
+        self.n_slots = int(n_slots)
+        self.keep = int(keep if keep is not None else max(self.top_k, n_slots - 2))
+        if not self.top_k <= self.keep <= self.n_slots:
+            raise AssertionError(f"keep={self.keep} must be in [top_k={self.top_k}, n_slots={self.n_slots}]")
+        self.max_inflight = int(max_inflight)
+        L, n, k = len(self.layers), self.n_cold, self.top_k
+        for li, lay in enumerate(self.layers):
+            if not lay.fused or lay.select_cfg is None:
+                raise AssertionError(f"layer {li}: staging needs the fused in-kernel selection")
+            if len(lay.cold) != n or lay.top_k != k:
+                raise AssertionError("every layer must have the same number of cold chunks and top_k")
+            for c in lay.cold:
+                if c.k.device.type != "cpu" or not c.k.is_pinned() or not c.k.is_contiguous() \
+                        or not c.v.is_contiguous():
+                    raise AssertionError(f"layer {li}: cold chunks must be contiguous pinned host tensors")
+        dev = self.device
+        self.residency = torch.full((L, n), -1, dtype=torch.int32, device=dev)
+        # one feedback row per layer: scores (fp32) | picks (int32) | residency used (int32)
+        self._W = n + 2 * k
+        self.feedback = torch.zeros((L, self._W), dtype=torch.float32, device=dev)
+        self.scores = self.feedback[:, :n]
+        self.idx = self.feedback[:, n:n + k].view(torch.int32)
+        self.res_out = self.feedback[:, n + k:].view(torch.int32)
+        self.idx.fill_(-1)
+        self.res_out.fill_(-1)
+        self._ring = [torch.empty((L, self._W), dtype=torch.float32, pin_memory=True) for _ in range(max(2, ring))]
+        self._ring_ev = [torch.cuda.Event() for _ in self._ring]
+        self._ring_rows = [(0, L)] * len(self._ring)
+        self._queued = 0           # segments whose feedback was queued for the host
+        self._seen = 0             # segments the host has processed
+        # host mirror of the cache
+        self.slot_of = np.full((L, n), -1, dtype=np.int64)        # FILLING / READY slot of a chunk
+        self.state = np.full((L, self.n_slots), _FREE, dtype=np.int8)
+        self.holds = np.full((L, self.n_slots), -1, dtype=np.int64)
+        self._pending: list = []   # (layer, chunk, slot, event): fills not committed yet
+        self._releasing: list = []
+        self._release_ev: Optional[torch.cuda.Event] = None
+        self.chunk_bytes = np.zeros((L, n), dtype=np.int64)
+        self._slot_k, self._slot_v, self._slot_cat = [], [], []
+        # addresses for the batched copies: slot (layer, s) K/V, cold chunk (layer, c) K/V, bytes per tensor
+        self._dst = np.zeros((L, self.n_slots, 2), dtype=np.uint64)
+        self._src = np.zeros((L, n, 2), dtype=np.uint64)
+        self._nbytes = np.zeros((L, n), dtype=np.int64)
+        for li, lay in enumerate(self.layers):
+            shape = max((tuple(c.k.shape) for c in lay.cold), key=lambda s: s[-2])
+            sk = torch.empty((self.n_slots,) + shape, dtype=lay.dtype, device=dev)
+            sv = torch.empty_like(sk)
+            # slot descriptors never change: they give the addresses and strides
+            # a staged chunk is read through; its rows, start and flags come
+            # from the chunk's own catalog entry
+            sdesc, _ = pack_descs([ChunkRef(sk[s], sv[s], 0, False) for s in range(self.n_slots)],
+                                  B=lay.B, H_kv=lay.H_kv, D=lay.D, dtype=lay.dtype)
+            self._slot_k.append(sk)
+            self._slot_v.append(sv)
+            self._slot_cat.append(descs_to_device(sdesc, dev))
+            for j in range(self.n_slots):
+                self._dst[li, j] = (sk[j].data_ptr(), sv[j].data_ptr())
+            for j, c in enumerate(lay.cold):
+                if tuple(c.k.shape) != tuple(sk.shape[1:]):
+                    raise AssertionError(f"layer {li} cold chunk {j}: shape {tuple(c.k.shape)} differs from the "
+                                         f"layer's other cold chunks {tuple(sk.shape[1:])}")
+                self._src[li, j] = (c.k.data_ptr(), c.v.data_ptr())
+                self._nbytes[li, j] = c.k.numel() * c.k.element_size()
+            self.chunk_bytes[li] = 2 * self._nbytes[li]
+            cfg = lay.select_cfg
+            cfg.n_slots = self.n_slots
+            cfg.slot_catalog = self._slot_cat[li].data_ptr()
+            cfg.residency = self.residency[li].data_ptr()
+            cfg.res_out = self.res_out[li].data_ptr()
+            cfg.score_out = self.scores[li].data_ptr()
+            cfg.idx_out = self.idx[li].data_ptr()
+        self.reset_counters()
+
+    # ----------------------------------------------------------------- per step
+    # ``lo``/``hi`` name a segment of layers [lo, hi) run as one graph; the
+    # defaults cover every layer.
+    def before_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
+        """Commit the landed fills of layers [lo, hi) with one batched store
+        of their residency entries on the compute stream.  Call before
+        enqueueing those layers' launches."""
+        hi = len(self.layers) if hi is None else hi
+        done, rest = [], []
+        for p in self._pending:
+            (done if lo <= p[0] < hi and p[3].query() else rest).append(p)
+        self._pending = rest
+        if done:
+            self._store([li * self.n_cold + c for li, c, _, _ in done], [s for _, _, s, _ in done])
+            for li, c, s, _ in done:
+                self.state[li, s] = _READY
+
+    def after_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
+        """Queue the feedback rows of layers [lo, hi) (scores, picks,
+        residency used) for the host: one copy after those layers' launches."""
+        hi = len(self.layers) if hi is None else hi
+        if self._queued - self._seen >= len(self._ring):
+            raise RuntimeError("feedback ring overrun: call service() after every after_step()")
+        r = self._queued % len(self._ring)
+        self._ring[r][lo:hi].copy_(self.feedback[lo:hi], non_blocking=True)
+        self._ring_ev[r].record(torch.cuda.current_stream(self.device))
+        self._ring_rows[r] = (lo, hi)
+        self._queued += 1
+
+    def drain(self) -> None:
+        """Process every queued segment's feedback now (waits for it)."""
+        self.service(lag=0)
+
+    def service(self, *, lag: int = 1) -> None:
+        """Process returned feedback -- waiting for every queued segment but
+        the ``lag`` newest, and taking those too when they are done -- count
+        hits and misses, free released slots, and plan evictions and fills
+        for the processed segments' layers."""
+        target = self._queued - lag
+        rows, scores = [], []
+        while self._seen < self._queued:
+            r = self._seen % len(self._ring)
+            if self._seen < target:
+                self._ring_ev[r].synchronize()
+            elif not self._ring_ev[r].query():
+                break
+            lo, hi = self._ring_rows[r]
+            fb = self._ring[r].numpy()[lo:hi]
+            self._account(fb, lo)
+            rows.append(np.arange(lo, hi))
+            scores.append(fb[:, :self.n_cold].copy())
+            self._seen += 1
+        if self._release_ev is not None and self._release_ev.query():
+            for li, s in self._releasing:
+                self.state[li, s] = _FREE
+                self.holds[li, s] = -1
+            self._releasing = []
+            self._release_ev = None
+        if rows:
+            self._plan(np.concatenate(rows), np.concatenate(scores))
+
+    # ----------------------------------------------------------------- internals
+    def _store(self, flat_idx: list, values: list) -> None:
+        """residency.view(-1)[flat_idx] = values on the compute stream (the
+        pairs travel in the kernel arguments)."""
+        idx = np.ascontiguousarray(flat_idx, dtype=np.int64)
+        val = np.ascontiguousarray(values, dtype=np.int32)
+        nat.check(nat.lib().halo_store_i32(self.residency.data_ptr(), self.residency.numel(), idx.ctypes.data,
+                                           val.ctypes.data, len(idx), nat.stream_ptr()), "halo_store_i32")
+
+    def _account(self, fb: np.ndarray, lo: int) -> None:
+        n, k = self.n_cold, self.top_k
+        idx = np.ascontiguousarray(fb[:, n:n + k]).view(np.int32)
+        res = np.ascontiguousarray(fb[:, n + k:]).view(np.int32)
+        valid = idx >= 0
+        miss = valid & (res < 0)
+        self.hits += int((valid & (res >= 0)).sum())
+        self.misses += int(miss.sum())
+        if miss.any():
+            r, j = np.nonzero(miss)
+            self.miss_bytes += int(self.chunk_bytes[lo + r, idx[r, j]].sum())
+
+    def _plan(self, layers: np.ndarray, scores: np.ndarray) -> None:
+        sc = np.where(np.isnan(scores), -np.inf, scores)
+        order = np.argsort(-sc, axis=1, kind="stable")      # score desc, index asc
+        rank = np.empty_like(order)
+        np.put_along_axis(rank, order, np.arange(sc.shape[1])[None, :], axis=1)
+        missing = (rank < self.keep) & (self.slot_of[layers] < 0)
+        if not missing.any():
+            return
+        r, c = np.nonzero(missing)
+        pri = np.lexsort((layers[r], rank[r, c]))           # best ranks first, then layer order
+        budget = self.max_inflight - len(self._pending)
+        evicted, fills = [], []
+        for i in pri:
+            if budget <= 0:
+                break
+            li, ch, rk = int(layers[r[i]]), int(c[i]), rank[r[i]]
+            free = np.flatnonzero(self.state[li] == _FREE)
+            if free.size == 0:
+                ready = np.flatnonzero(self.state[li] == _READY)
+                if ready.size:
+                    worst = ready[np.argmax(rk[self.holds[li, ready]])]
+                    if rk[self.holds[li, worst]] >= self.keep:
+                        evicted.append((li, int(self.holds[li, worst]), int(worst)))
+                        self.slot_of[li, self.holds[li, worst]] = -1
+                        self.state[li, worst] = _RELEASING
+                continue
+            fills.append(self._reserve(li, ch, int(free[0])))
+            budget -= 1
+        if fills:
+            self._issue(fills)
+        if evicted:
+            self._store([li * self.n_cold + ch for li, ch, _ in evicted], [-1] * len(evicted))
+            self._releasing += [(li, s) for li, _, s in evicted]
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._release_ev = ev
+
+    def _reserve(self, li: int, c: int, s: int) -> tuple:
+        self.state[li, s] = _FILLING
+        self.holds[li, s] = c
+        self.slot_of[li, c] = s
+        self.fills += 1
+        self.fill_bytes += int(self.chunk_bytes[li, c])
+        return li, c, s
+
+    def _issue(self, fills: list) -> None:
+        """One batch of hipMemcpyAsync copies on the copy stream, one event
+        after them for every fill of the batch."""
+        arr = (nat.Fill * len(fills))()
+        for i, (li, c, s) in enumerate(fills):
+            arr[i].dst_k, arr[i].dst_v = int(self._dst[li, s, 0]), int(self._dst[li, s, 1])
+            arr[i].src_k, arr[i].src_v = int(self._src[li, c, 0]), int(self._src[li, c, 1])
+            arr[i].bytes = int(self._nbytes[li, c])
+        cs = copy_stream(self.device)
+        nat.check(nat.lib().halo_stage_fills(arr, len(fills), nat.stream_ptr(cs)), "halo_stage_fills")
+        ev = torch.cuda.Event()
+        ev.record(cs)
+        self._pending += [(li, c, s, ev) for li, c, s in fills]
+
+    # ----------------------------------------------------------------- control
+    def clear(self) -> None:
+        """Empty every slot (synchronises the device first)."""
+        torch.cuda.synchronize(self.device)
+        self._pending, self._releasing, self._release_ev = [], [], None
+        self._seen = self._queued
+        self.residency.fill_(-1)
+        self.slot_of.fill(-1)
+        self.state.fill(_FREE)
+        self.holds.fill(-1)
+        torch.cuda.synchronize(self.device)
+        self.reset_counters()
+
+    def resident(self, layer: int) -> list:
+        """Chunks of ``layer`` whose residency entry has been committed."""
+        return sorted(int(self.holds[layer, s]) for s in np.flatnonzero(self.state[layer] == _READY))
+
+    def reset_counters(self) -> None:
+        self.hits = self.misses = self.fills = self.fill_bytes = self.miss_bytes = 0
+
+    def hit_rate(self) -> float:
+        n = self.hits + self.misses
+        return self.hits / n if n else 0.0
+
+    @property
+    def slot_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self._slot_k + self._slot_v)

@@ -150,7 +150,22 @@ typedef struct halo_select_cfg {
    * items (0 = not stated).  Those workgroups start the selection's loads
    * before reading their record; a wrong count costs loads, not results. */
   int32_t lead_items;
-  int32_t reserved;
+  /* HBM staging of the cold chunks (all NULL / 0: every chosen chunk is
+   * read through its catalog descriptor).  residency[s*catalog_stride + p]
+   * is the staging slot that holds cold chunk p (-1: none); the kernel then
+   * reads the chunk's rows through the addresses and strides of
+   * slot_catalog[s*n_slots + slot] (its rows, start, flags and batch still
+   * come from the chunk's catalog entry, so slot descriptors never change).  Writers
+   * store a slot index only after the slot's rows have landed, and -1 only
+   * when the slot will not be overwritten before the launches that may have
+   * read the old index have finished, so a launch reads either descriptor
+   * and the same rows.  res_out[s*top_k + j] receives the residency entry
+   * used for the j-th chosen chunk (>= 0: served from HBM staging).
+   * n_slots <= 64. */
+  int32_t n_slots;
+  const halo_chunk_desc* slot_catalog;
+  const int32_t* residency;
+  int32_t* res_out;
 } halo_select_cfg;
 
 /*
@@ -386,6 +401,36 @@ int halo_decode_attn_kivi(const void* q, int64_t q_stride_b, int64_t q_stride_h,
 int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, const void* src_v,
                      int64_t block_bytes, const int32_t* blocks, int n_blocks, int64_t max_blocks,
                      const int8_t* tier_of, int src_tier, void* stream);
+
+/* ---- HBM staging of cold chunks ---------------------------------------- */
+
+/* One host-to-device chunk copy of the staging cache: bytes from src_k to
+ * dst_k and, when dst_v is non-NULL, from src_v to dst_v. */
+typedef struct halo_fill {
+  void* dst_k;
+  const void* src_k;
+  void* dst_v;
+  const void* src_v;
+  int64_t bytes;
+} halo_fill;
+
+/*
+ * Enqueue n fills as hipMemcpyAsync host-to-device copies on `stream`
+ * (sources pinned host memory), in list order.  Replaces the per-block
+ * move_block calls of HALORefetcher._issue (halo/refetcher.py:102-114) for
+ * the staging cache of halo_select_cfg.residency.
+ */
+int halo_stage_fills(const halo_fill* fills, int n, void* stream);
+
+/*
+ * base[idx[i]] = vals[i] for i < n (entries with idx outside [0, n_elems)
+ * are skipped), as kernels on `stream` whose pairs travel in the kernel
+ * arguments: the host arrays are read during the call only.  The staging
+ * cache commits and releases residency entries with it.  No counterpart in
+ * the reference (whose tier directory is a host dict,
+ * halo/memory_tier.py:133).
+ */
+int halo_store_i32(int32_t* base, int64_t n_elems, const int64_t* idx, const int32_t* vals, int n, void* stream);
 
 /* ---- build metadata ---------------------------------------------------- */
 /*

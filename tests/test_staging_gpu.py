@@ -1,0 +1,136 @@
+"""The HBM staging cache for cold chunks in pinned host memory
+(``ColdStaging``): with the cold tier on the host and a drifting query,
+every step's output, LSE and selection equal those of the same layer with
+every cold chunk in HBM, bit for bit, whether a chosen chunk is served from
+a staging slot or read in place over the host link; fills and evictions
+commit only between steps; a constant query ends with every selection a
+hit.  Eager steps and HIP-graph replays are both covered."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(dev, *, L=2, n_chunks=16, chunk=256, n_hot=4, top_k=3, slots=6, keep=None, seed=0):
+    from halo_amd.decode import ChunkRef
+    from halo_amd.staging import ColdStaging
+    from halo_amd.tiered import TieredDecodeLayer
+    H, H_kv, D = 16, 4, 128
+    g = torch.Generator(device=dev).manual_seed(seed)
+    hbm, staged = [], []
+    for _ in range(L):
+        k = torch.randn((1, H_kv, n_chunks * chunk, D), generator=g, device=dev)
+        k[..., :3] *= 6
+        k = k.to(torch.bfloat16)
+        v = torch.randn((1, H_kv, n_chunks * chunk, D), generator=g, device=dev).to(torch.bfloat16)
+        refs = [ChunkRef(k[..., i * chunk:(i + 1) * chunk, :], v[..., i * chunk:(i + 1) * chunk, :], i * chunk, True)
+                for i in range(n_chunks)]
+        n_cold = n_chunks - n_hot
+        a = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:], cold=refs[:n_cold],
+                              top_k=top_k, device=dev)
+        host = []
+        for c in refs[:n_cold]:
+            hk = torch.empty(tuple(c.k.shape), dtype=c.k.dtype, pin_memory=True)
+            hv = torch.empty(tuple(c.v.shape), dtype=c.v.dtype, pin_memory=True)
+            hk.copy_(c.k)
+            hv.copy_(c.v)
+            host.append(ChunkRef(hk, hv, c.chunk_start, True))
+        b = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:], cold=host,
+                              top_k=top_k, device=dev, cold_kmean=a.kmean)
+        hbm.append(a)
+        staged.append(b)
+    st = ColdStaging(staged, n_slots=slots, keep=keep, max_inflight=4)
+    return hbm, staged, st, (H, D)
+
+
+def _queries(dev, steps, L, H, D, rho, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn((L, 1, H, D), generator=g, device=dev)
+    out = []
+    for _ in range(steps):
+        q = rho * q + math.sqrt(1 - rho * rho) * torch.randn((L, 1, H, D), generator=g, device=dev)
+        out.append(q.to(torch.bfloat16))
+    return out
+
+
+def test_staged_steps_match_all_hbm_bit_for_bit(dev):
+    hbm, staged, st, (H, D) = _setup(dev)
+    L = len(hbm)
+    scale = 1 / math.sqrt(D)
+    served = set()
+    for t, q in enumerate(_queries(dev, 30, L, H, D, 0.8, 1)):
+        st.before_step()
+        outs = []
+        for li in range(L):
+            o1 = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+            l1 = torch.empty((1, H), device=dev)
+            o2, l2 = torch.empty_like(o1), torch.empty_like(l1)
+            hbm[li].step(q[li], scale=scale, out=o1, lse=l1)
+            staged[li].step(q[li], scale=scale, out=o2, lse=l2)
+            outs.append((o1, l1, o2, l2))
+        st.after_step()
+        torch.cuda.synchronize()
+        for li, (o1, l1, o2, l2) in enumerate(outs):
+            assert torch.equal(o1, o2) and torch.equal(l1, l2), (t, li)
+            assert torch.equal(hbm[li].idx[0], st.idx[li]), (t, li)
+            res = st.res_out[li].cpu().numpy()
+            served |= {int(c) for c, r in zip(st.idx[li].cpu().numpy(), res) if r >= 0}
+        st.service()
+    assert st.hits > 0 and st.misses > 0 and served
+    assert st.fills > 0
+
+
+def test_constant_query_ends_all_hits_in_a_graph(dev):
+    hbm, staged, st, (H, D) = _setup(dev, seed=3)
+    L = len(hbm)
+    scale = 1 / math.sqrt(D)
+    q = _queries(dev, 1, L, H, D, 0.0, 4)[0]
+    qbuf = q.clone()
+    outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    ref = [torch.empty_like(o) for o in outs]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for li in range(L):
+            staged[li].step(qbuf[li], scale=scale, out=outs[li])
+            hbm[li].step(q[li], scale=scale, out=ref[li])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for li in range(L):
+                staged[li].step(qbuf[li], scale=scale, out=outs[li])
+        for _ in range(8):
+            st.before_step()
+            g.replay()
+            st.after_step()
+            st.service()
+        torch.cuda.synchronize()
+        for li in range(L):
+            assert torch.equal(outs[li], ref[li])
+            top = set(int(c) for c in st.idx[li].cpu().tolist())
+            assert top <= set(st.resident(li))
+        st.drain()
+        st.reset_counters()
+        for _ in range(3):
+            st.before_step()
+            g.replay()
+            st.after_step()
+            st.service()
+        st.drain()
+    assert st.misses == 0 and st.hits == 3 * L * 3
+    for li in range(L):
+        assert torch.equal(outs[li], ref[li])
+
+
+def test_staging_validates_its_inputs(dev):
+    from halo_amd.staging import ColdStaging
+    hbm, staged, st, _ = _setup(dev, L=1, slots=4)
+    with pytest.raises(AssertionError):
+        ColdStaging(hbm, n_slots=4)              # cold chunks in HBM, not pinned host memory
+    with pytest.raises(AssertionError):
+        ColdStaging(staged, n_slots=4, keep=2)   # keep below top_k

@@ -406,6 +406,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
+    ap.add_argument("--only", choices=["c3", "c4", "c5"], default=None,
+                    help="run one secondary leg alone (chunked prefill, ragged batch, KIVI) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
     args = ap.parse_args()
@@ -422,6 +424,12 @@ def main() -> int:
 
     _native.lib()
     dev = torch.device("cuda:0")
+    if args.only is not None:
+        leg = {"c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
+               "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
+               "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps))}[args.only]
+        print(json.dumps({"leg": args.only, **leg()}), flush=True)
+        return 0
     L, H, H_kv, D, T, chunk, n_hot, top_k = args.layers, 32, 8, 128, 32768, 1024, 8, 4
     n_cold = T // chunk - n_hot
     scale = 1.0 / math.sqrt(D)

@@ -216,11 +216,13 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     del graphs
     sel = staging.hits + staging.misses
     link = (staging.fill_bytes + staging.miss_bytes) / steps
-    log(f"{label}: {dt * 1e3:.3f} ms/step, hit rate {staging.hit_rate():.4f} over {sel} selections, "
+    log(f"{label}: {dt * 1e3:.3f} ms/step, hit rate {staging.hit_rate():.4f} over {sel} selections "
+        f"({staging.misses_predicted} of {staging.misses} misses predicted), "
         f"{staging.fills / steps:.2f} fills/step, link {link / 2**20:.1f} MiB/step")
     return {
         "tokens_per_s": 1.0 / dt, "ms_per_step": dt * 1e3, "hit_rate": staging.hit_rate(),
         "selections": sel, "hits": staging.hits, "misses": staging.misses,
+        "misses_predicted": staging.misses_predicted,
         "fills_per_step": staging.fills / steps,
         "prefetch_bytes_per_step": staging.fill_bytes / steps,
         "in_place_miss_bytes_per_step": staging.miss_bytes / steps,

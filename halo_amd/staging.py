@@ -26,8 +26,9 @@ Ordering (no kernel observes a change while it runs):
   * a fill whose event has completed is committed before the next launches
     of its layer: one batched store of residency entries on the compute
     stream; every launch after it reads the slot, every launch before it read
-    host memory.  A fill still in flight is committed later (the compute
-    stream never waits for the link);
+    host memory.  A fill still in flight is committed later, except an urgent
+    one (a chunk among its layer's current top-k, which the next launch would
+    otherwise read over the link): the compute stream waits for its copy;
   * an eviction stores -1 on the compute stream after the launches already
     queued; the slot becomes free for a new fill only once an event
     recorded after that store has completed, i.e. once every launch that
@@ -40,6 +41,7 @@ used for each chosen chunk.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence
 
 import numpy as np
@@ -59,12 +61,13 @@ class ColdStaging:
     selection over cold chunks held as contiguous pinned host tensors, the
     same number of cold chunks each.  ``n_slots`` HBM slots per layer (each
     the size of the layer's widest cold chunk); ``keep`` best-scoring chunks
-    per layer are staged (default n_slots - 2, so fills in flight and slots
-    waiting for release have room); ``max_inflight`` bounds the copies in
+    per layer are staged (default n_slots - 2); ``spare`` slots per layer are
+    kept free or releasing (staged chunks outside the kept set are released
+    worst rank first to keep them); ``max_inflight`` bounds the copies in
     flight on the link."""
 
     def __init__(self, layers: Sequence, *, n_slots: int = 12, keep: Optional[int] = None,
-                 max_inflight: int = 8, ring: int = 16) -> None:
+                 max_inflight: int = 8, spare: int = 0, ring: int = 16) -> None:
         if not layers:
             raise AssertionError("no layers")
         self.layers = list(layers)
@@ -79,6 +82,7 @@ class ColdStaging:
         if not self.top_k <= self.keep <= self.n_slots:
             raise AssertionError(f"keep={self.keep} must be in [top_k={self.top_k}, n_slots={self.n_slots}]")
         self.max_inflight = int(max_inflight)
+        self.spare = int(spare)
         L, n, k = len(self.layers), self.n_cold, self.top_k
         for li, lay in enumerate(self.layers):
             if not lay.fused or lay.select_cfg is None:
@@ -108,7 +112,8 @@ class ColdStaging:
         self.slot_of = np.full((L, n), -1, dtype=np.int64)        # FILLING / READY slot of a chunk
         self.state = np.full((L, self.n_slots), _FREE, dtype=np.int8)
         self.holds = np.full((L, self.n_slots), -1, dtype=np.int64)
-        self._pending: list = []   # (layer, chunk, slot, event): fills not committed yet
+        self._pending: list = []   # (layer, chunk, slot, event, urgent): fills not committed yet
+        self._last_rank = np.full((L, n), n, dtype=np.int64)     # rank at the last planning pass
         self._releasing: list = []
         self._release_ev: Optional[torch.cuda.Event] = None
         self.chunk_bytes = np.zeros((L, n), dtype=np.int64)
@@ -151,17 +156,27 @@ class ColdStaging:
     # ``lo``/``hi`` name a segment of layers [lo, hi) run as one graph; the
     # defaults cover every layer.
     def before_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
-        """Commit the landed fills of layers [lo, hi) with one batched store
-        of their residency entries on the compute stream.  Call before
-        enqueueing those layers' launches."""
+        """Commit the fills of layers [lo, hi) that have landed, and the
+        urgent ones (chunks among the layer's current top-k, which the next
+        launch would otherwise read over the link) after a device-side wait
+        for their copy, with one batched store of residency entries on the
+        compute stream.  Call before enqueueing those layers' launches."""
         hi = len(self.layers) if hi is None else hi
-        done, rest = [], []
+        compute = torch.cuda.current_stream(self.device)
+        done, rest, waited = [], [], set()
         for p in self._pending:
-            (done if lo <= p[0] < hi and p[3].query() else rest).append(p)
+            li, c, s, ev, urgent = p
+            if lo <= li < hi and (urgent or ev.query()):
+                if urgent and id(ev) not in waited:
+                    compute.wait_event(ev)
+                    waited.add(id(ev))
+                done.append(p)
+            else:
+                rest.append(p)
         self._pending = rest
         if done:
-            self._store([li * self.n_cold + c for li, c, _, _ in done], [s for _, _, s, _ in done])
-            for li, c, s, _ in done:
+            self._store([li * self.n_cold + c for li, c, _, _, _ in done], [s for _, _, s, _, _ in done])
+            for li, c, s, _, _ in done:
                 self.state[li, s] = _READY
 
     def after_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
@@ -228,19 +243,41 @@ class ColdStaging:
         if miss.any():
             r, j = np.nonzero(miss)
             self.miss_bytes += int(self.chunk_bytes[lo + r, idx[r, j]].sum())
+            # a miss the policy had predicted (in the kept set at the last plan:
+            # its fill had not landed or been committed) or one it had not
+            predicted = self._last_rank[lo + r, idx[r, j]] < self.keep
+            self.misses_predicted += int(predicted.sum())
 
     def _plan(self, layers: np.ndarray, scores: np.ndarray) -> None:
         sc = np.where(np.isnan(scores), -np.inf, scores)
         order = np.argsort(-sc, axis=1, kind="stable")      # score desc, index asc
         rank = np.empty_like(order)
         np.put_along_axis(rank, order, np.arange(sc.shape[1])[None, :], axis=1)
+        self._last_rank[layers] = rank
         missing = (rank < self.keep) & (self.slot_of[layers] < 0)
-        if not missing.any():
-            return
+        evicted, fills = [], []
+        # keep `spare` slots per layer free or on their way to free, releasing
+        # the worst-ranked staged chunks outside the kept set, so a newly
+        # predicted chunk finds a slot without waiting for a release
+        for i, li in enumerate(layers):
+            st = self.state[li]
+            short = self.spare - int(((st == _FREE) | (st == _RELEASING)).sum())
+            if short <= 0:
+                continue
+            ready = np.flatnonzero(st == _READY)
+            if ready.size == 0:
+                continue
+            rk = rank[i][self.holds[li, ready]]
+            for j in np.argsort(-rk, kind="stable")[:short]:
+                if rk[j] < self.keep:
+                    break
+                s = int(ready[j])
+                evicted.append((int(li), int(self.holds[li, s]), s))
+                self.slot_of[li, self.holds[li, s]] = -1
+                self.state[li, s] = _RELEASING
         r, c = np.nonzero(missing)
         pri = np.lexsort((layers[r], rank[r, c]))           # best ranks first, then layer order
         budget = self.max_inflight - len(self._pending)
-        evicted, fills = [], []
         for i in pri:
             if budget <= 0:
                 break
@@ -255,7 +292,7 @@ class ColdStaging:
                         self.slot_of[li, self.holds[li, worst]] = -1
                         self.state[li, worst] = _RELEASING
                 continue
-            fills.append(self._reserve(li, ch, int(free[0])))
+            fills.append(self._reserve(li, ch, int(free[0]), bool(rk[ch] < self.top_k)))
             budget -= 1
         if fills:
             self._issue(fills)
@@ -266,27 +303,29 @@ class ColdStaging:
             ev.record(torch.cuda.current_stream(self.device))
             self._release_ev = ev
 
-    def _reserve(self, li: int, c: int, s: int) -> tuple:
+    def _reserve(self, li: int, c: int, s: int, urgent: bool) -> tuple:
         self.state[li, s] = _FILLING
         self.holds[li, s] = c
         self.slot_of[li, c] = s
         self.fills += 1
         self.fill_bytes += int(self.chunk_bytes[li, c])
-        return li, c, s
+        return li, c, s, urgent
 
     def _issue(self, fills: list) -> None:
-        """One batch of hipMemcpyAsync copies on the copy stream, one event
-        after them for every fill of the batch."""
-        arr = (nat.Fill * len(fills))()
-        for i, (li, c, s) in enumerate(fills):
-            arr[i].dst_k, arr[i].dst_v = int(self._dst[li, s, 0]), int(self._dst[li, s, 1])
-            arr[i].src_k, arr[i].src_v = int(self._src[li, c, 0]), int(self._src[li, c, 1])
-            arr[i].bytes = int(self._nbytes[li, c])
+        """hipMemcpyAsync copies on the copy stream in the given order (best
+        ranks first), each fill followed by its own event so it commits as
+        soon as it lands."""
         cs = copy_stream(self.device)
-        nat.check(nat.lib().halo_stage_fills(arr, len(fills), nat.stream_ptr(cs)), "halo_stage_fills")
-        ev = torch.cuda.Event()
-        ev.record(cs)
-        self._pending += [(li, c, s, ev) for li, c, s in fills]
+        L = nat.lib()
+        arr = nat.Fill()
+        for li, c, s, urgent in fills:
+            arr.dst_k, arr.dst_v = int(self._dst[li, s, 0]), int(self._dst[li, s, 1])
+            arr.src_k, arr.src_v = int(self._src[li, c, 0]), int(self._src[li, c, 1])
+            arr.bytes = int(self._nbytes[li, c])
+            nat.check(L.halo_stage_fills(ctypes.byref(arr), 1, nat.stream_ptr(cs)), "halo_stage_fills")
+            ev = torch.cuda.Event()
+            ev.record(cs)
+            self._pending.append((li, c, s, ev, urgent))
 
     # ----------------------------------------------------------------- control
     def clear(self) -> None:
@@ -296,6 +335,7 @@ class ColdStaging:
         self._seen = self._queued
         self.residency.fill_(-1)
         self.slot_of.fill(-1)
+        self._last_rank.fill(self.n_cold)
         self.state.fill(_FREE)
         self.holds.fill(-1)
         torch.cuda.synchronize(self.device)
@@ -307,6 +347,7 @@ class ColdStaging:
 
     def reset_counters(self) -> None:
         self.hits = self.misses = self.fills = self.fill_bytes = self.miss_bytes = 0
+        self.misses_predicted = 0
 
     def hit_rate(self) -> float:
         n = self.hits + self.misses

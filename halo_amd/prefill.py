@@ -25,7 +25,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _native as nat
-from .decode import ChunkRef, descs_to_device, pack_descs
+from .decode import ChunkRef, _to_device, descs_to_device, pack_descs
 
 
 def prefill_attention(q: torch.Tensor, chunks: Sequence[ChunkRef], *, scale: Optional[float] = None,
@@ -53,23 +53,26 @@ def prefill_attention(q: torch.Tensor, chunks: Sequence[ChunkRef], *, scale: Opt
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     if q_start is None:
         q_start = sum(c.T for c in chunks) - T_q
-    if not torch.is_tensor(q_start):
-        q_start = torch.full((B,), int(q_start), dtype=torch.int64)
-    q_start = q_start.to(device=q.device, dtype=torch.int64).reshape(B).contiguous()
     descs, keep = pack_descs(chunks, B=B, H_kv=H_kv, D=D, dtype=q.dtype)
-    d_descs = descs_to_device(descs, q.device)
-    out = torch.empty((B, H, T_q, D), device=q.device, dtype=out_dtype or q.dtype)
-    lse = torch.empty((B, H, T_q), device=q.device, dtype=torch.float32) if return_lse else None
-    nat.check(L.halo_prefill_attn(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), nat.dtype_code(q.dtype), B, H, H_kv, T_q, D,
-        q_start.data_ptr(), d_descs.data_ptr(), len(chunks), scale,
-        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), nat.dtype_code(out.dtype),
-        nat.ptr(lse), nat.stream_ptr(stream)), "halo_prefill_attn")
-    # The descriptor buffer is freed into torch's stream-ordered caching
-    # allocator, so later work on the launch stream cannot reuse it early;
-    # on another stream it is recorded.  The caller owns the K/V tensors.
-    if stream is not None:
-        d_descs.record_stream(stream)
+    # The uploads and the launch share one stream (the caller's, or the
+    # current one), so the kernel sees the tables; the tables are freed into
+    # torch's stream-ordered caching allocator on that stream.  q_start gets
+    # there without a blocking copy (a pageable host-to-device copy would
+    # hold the host until the stream drains).  The caller owns the K/V.
+    with torch.cuda.stream(stream) if stream is not None else _nullctx():
+        if not torch.is_tensor(q_start):
+            q_start = torch.full((B,), int(q_start), dtype=torch.int64, device=q.device)
+        elif q_start.device.type != "cuda":
+            q_start = _to_device(q_start.to(torch.int64).reshape(-1).expand(B).numpy(), q.device)
+        q_start = q_start.to(device=q.device, dtype=torch.int64).reshape(B).contiguous()
+        d_descs = descs_to_device(descs, q.device)
+        out = torch.empty((B, H, T_q, D), device=q.device, dtype=out_dtype or q.dtype)
+        lse = torch.empty((B, H, T_q), device=q.device, dtype=torch.float32) if return_lse else None
+        nat.check(L.halo_prefill_attn(
+            q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), nat.dtype_code(q.dtype), B, H, H_kv, T_q, D,
+            q_start.data_ptr(), d_descs.data_ptr(), len(chunks), scale,
+            out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), nat.dtype_code(out.dtype),
+            nat.ptr(lse), nat.stream_ptr(stream)), "halo_prefill_attn")
     del keep
     return (out, lse) if return_lse else out
 

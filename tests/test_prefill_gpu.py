@@ -33,13 +33,16 @@ def _case(seed, *, B, H, H_kv, T_prior, T_q, D, dtype, chunk):
     ("float16", 4, 4, 64, 256, 128, 64),        # MHA, d64
     ("bfloat16", 32, 8, 128, 1024, 256, 256),   # 8B GQA shape, small
     ("bfloat16", 4, 1, 128, 0, 300, 128),       # self chunk only
+    ("bfloat16", 14, 2, 128, 192, 77, 64),      # rep 7: flattened rows straddle positions, ragged last block
+    ("float16", 16, 2, 64, 130, 45, 64),        # rep 8, d64, ragged prior chunk
 ])
 def test_prefill_matches_closed_form(dev, dtype, H, H_kv, D, T_prior, T_q, chunk):
     from halo_amd.decode import ChunkRef
     from halo_amd.prefill import prefill_attention
     q, k, v = _case(7, B=1, H=H, H_kv=H_kv, T_prior=T_prior, T_q=T_q, D=D, dtype=dtype, chunk=chunk)
     qg, kg, vg = (_gpu(a, dtype, dev) for a in (q, k, v))
-    chunks = [ChunkRef(kg[:, :, s:s + chunk], vg[:, :, s:s + chunk], s, False) for s in range(0, T_prior, chunk)]
+    chunks = [ChunkRef(kg[:, :, s:min(s + chunk, T_prior)], vg[:, :, s:min(s + chunk, T_prior)], s, False)
+              for s in range(0, T_prior, chunk)]
     chunks.append(ChunkRef(kg[:, :, T_prior:], vg[:, :, T_prior:], T_prior, True))
     scale = 1 / math.sqrt(D)
     out, lse = prefill_attention(qg, chunks, scale=scale, return_lse=True)

@@ -888,12 +888,13 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
 
 // LDS bytes of the plain-row MFMA path (bf16/f16 K/V): per pair 2 p tiles
 // (K/V dtype, [head][row]) and 2 rescale vectors, the pair partials, then one
-// V tile per V-wave and one K tile per K-wave.
-template <int D, int REP, int NW>
+// V tile per V-wave and one K tile per K-wave.  TR: rows per wave tile (0:
+// 64 rows, fewer for wide rows); a smaller tile shrinks the footprint.
+template <int D, int REP, int NW, int TR = 0>
 struct PlainMfmaLds {
   static constexpr int RB = D * 2;
   static constexpr int SL = RB / 16;
-  static constexpr int TILE = SL <= 16 ? kWave : kWave * 16 / SL;
+  static constexpr int TILE = TR ? TR : (SL <= 16 ? kWave : kWave * 16 / SL);
   static constexpr int NP = NW / 2;
   static constexpr int SZ_P = NP * 2 * REP * TILE * 2;
   static constexpr int SZ_AL = (NP * 2 * REP * 4 + 15) / 16 * 16;
@@ -904,13 +905,28 @@ struct PlainMfmaLds {
 
 // One work item's rows [t0, t1) of a plain bf16/f16 K/V chunk on the matrix
 // cores; writes the item's partial at workspace slot wslot.
-template <int DT, int D, int REP, int NW>
-__device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, char* smem, float (*s_wm)[REP],
+// LDS regions of the plain-row path (sizes in PlainMfmaLds).
+struct PlainLds {
+  char* p;   // SZ_P: p tiles
+  char* al;  // SZ_AL: rescale factors
+  char* wo;  // SZ_WO: pair partials
+  char* vt;  // SZ_VT: V tiles
+  char* kt;  // SZ_VT: K tiles
+};
+template <int D, int REP, int NW, int TR = 0>
+__device__ __forceinline__ PlainLds plain_lds_at(char* smem) {
+  using L = PlainMfmaLds<D, REP, NW, TR>;
+  return PlainLds{smem, smem + L::SZ_P, smem + L::SZ_P + L::SZ_AL, smem + L::SZ_P + L::SZ_AL + L::SZ_WO,
+                  smem + L::SZ_P + L::SZ_AL + L::SZ_WO + L::SZ_VT};
+}
+
+template <int DT, int D, int REP, int NW, int TR = 0>
+__device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const PlainLds& lds, float (*s_wm)[REP],
                                                 float (*s_wl)[REP], const char* kbase, const char* vbase,
                                                 int64_t kst, int64_t vst, int t0, int t1, int b, int hq0,
                                                 int nvalid_h, int wslot) {
   using E = Elem<DT>;
-  using L = PlainMfmaLds<D, REP, NW>;
+  using L = PlainMfmaLds<D, REP, NW, TR>;
   constexpr int EP = E::per16;          // elements per 16-byte piece
   constexpr int SL = D / EP;            // pieces per row
   constexpr int RPI = kWave / SL;       // rows covered by one load instruction
@@ -925,11 +941,11 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, char* sme
   constexpr int KS2 = TILE / 32;        // 32-row k-steps of the P.V product
   static_assert(SL * RPI == kWave && PPL * RPI == TILE && REP <= 16 && VPB % 2 == 0 && NB * VPB == PPL,
                 "mfma tile shape");
-  float* s_pall = reinterpret_cast<float*>(smem);
-  float* s_alpha = reinterpret_cast<float*>(smem + L::SZ_P);
-  float* s_wo = reinterpret_cast<float*>(smem + L::SZ_P + L::SZ_AL);
-  char* s_vt = smem + L::SZ_P + L::SZ_AL + L::SZ_WO;
-  char* s_kt = s_vt + L::SZ_VT;
+  float* s_pall = reinterpret_cast<float*>(lds.p);
+  float* s_alpha = reinterpret_cast<float*>(lds.al);
+  float* s_wo = reinterpret_cast<float*>(lds.wo);
+  char* s_vt = lds.vt;
+  char* s_kt = lds.kt;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1255,7 +1271,8 @@ decode_attn_kernel(DecodeParams P) {
   const int voff0 = my_col * 16;
 
   if constexpr (kMfma) {
-    plain_rows_mfma<DT, D, REP, NW>(P, smem, s_wm, s_wl, kbase, vbase, kst, vst, t0, t1, b, hq0, nvalid_h, wslot);
+    plain_rows_mfma<DT, D, REP, NW>(P, plain_lds_at<D, REP, NW>(smem), s_wm, s_wl, kbase, vbase, kst, vst, t0, t1, b,
+                                    hq0, nvalid_h, wslot);
     return;
   } else {
     // ---- VALU path (fp32): K transposed through LDS, lane groups per head.
@@ -1470,8 +1487,9 @@ __device__ __forceinline__ uint4 mul8(const uint4& a, const uint4& b) {
 // Epilogue for o held as MFMA accumulators (lane l: heads 4*(l/16)..+4 of
 // columns 16*db + l%16) by NS partial owners: owner j contributes o (has_o)
 // and/or its (m, l) per head (has_ml); the NS partials are merged through
-// LDS into the work item's partial.
-template <int D, int REP, int NS, int DB>
+// LDS into the work item's partial.  Owner j's o goes to s_wo + j * OSTR
+// floats (OSTR >= REP * D).
+template <int D, int REP, int NS, int DB, int OSTR = REP * D>
 __device__ __forceinline__ void write_partial_owners(const DecodeParams& P, int wslot, int owner, bool has_o,
                                                      bool has_ml, const f32x4 (&acc)[DB], const float* m_run,
                                                      const float* l_head, float* s_wo, float (*s_wm)[REP],
@@ -1484,7 +1502,7 @@ __device__ __forceinline__ void write_partial_owners(const DecodeParams& P, int 
       const int h = 4 * (lane >> 4) + e;
       if (h < REP) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) s_wo[(owner * REP + h) * D + db * 16 + (lane & 15)] = acc[db][e];
+        for (int db = 0; db < DB; ++db) s_wo[owner * OSTR + h * D + db * 16 + (lane & 15)] = acc[db][e];
       }
     }
   }
@@ -1505,7 +1523,7 @@ __device__ __forceinline__ void write_partial_owners(const DecodeParams& P, int 
     const float Ms = (M == -INFINITY) ? 0.f : M;
     float acc_o = 0.f;
 #pragma unroll
-    for (int w = 0; w < NS; ++w) acc_o += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * REP * D + i];
+    for (int w = 0; w < NS; ++w) acc_o += __builtin_amdgcn_exp2f(s_wm[w][r] - Ms) * s_wo[w * OSTR + i];
     wso[i] = acc_o;
   }
   if (tid < REP) {
@@ -1536,25 +1554,23 @@ decode_attn_kivi_kernel(DecodeParams P) {
   constexpr int TB = D > 128 ? 2 : 4;         // blocks per wave tile (12 KiB at D = 128, 256)
   constexpr int TBYTES = TB * BB;
   constexpr int LPT = TBYTES / (16 * kWave);   // 16-byte loads per lane per tile
-  static_assert(TBYTES % (16 * kWave) == 0 && REP <= 16, "kivi tile shape");
+  static_assert(TBYTES % (16 * kWave) == 0 && REP <= 16 && TB % 2 == 0, "kivi tile shape");
   // K side of a block at offset 0: codes [0, CB), scale [CB, CB+2D), zero [CB+2D, CB+4D)
   // V side: codes (channel-major, 8 bytes per channel) at CB+4D, scale/zero (group-major)
   constexpr int VC = CB + 4 * D, VS = 2 * CB + 4 * D, VZ = 2 * CB + 6 * D;
 
-  // LDS: per wave a raw tile, the p of one block ([head][token]) and its
-  // rescale factors, then the wave partials; the plain-row path (the
-  // unquantised recent rows in the same launch) reuses the same bytes.
-  constexpr int SZ_RAW = NW * TBYTES;
-  constexpr int SZ_PB = NW * REP * 64 * 2;
-  constexpr int SZ_ALW = (NW * REP * 4 + 15) / 16 * 16;
-  constexpr int SZ_KL = SZ_RAW + SZ_PB + SZ_ALW + NW * REP * D * 4;
-  constexpr int SZ_PL = PlainMfmaLds<D, REP, NW>::bytes;
-  __shared__ __attribute__((aligned(16))) char smem[SZ_KL > SZ_PL ? SZ_KL : SZ_PL];
+  // LDS: one raw tile per wave (each wave reads only its own, in order, so
+  // no fence is needed between its stores and loads); a wave's partial goes
+  // into its own tile at the end.  The plain-row path (the unquantised
+  // recent rows in the same launch, 32-row tiles) lays its regions over the
+  // same bytes.
+  constexpr int PL_TR = 32;
+  using PL = PlainMfmaLds<D, REP, NW, PL_TR>;
+  constexpr int SZ_RAW = NW * TBYTES > PL::bytes ? NW * TBYTES : PL::bytes;
+  static_assert(TBYTES >= REP * D * 4, "a wave's partial fits in its raw tile");
+  __shared__ __attribute__((aligned(16))) char s_raw[SZ_RAW];
   __shared__ float s_wm[NW][REP], s_wl[NW][REP];
-  char (*s_raw)[TBYTES] = reinterpret_cast<char (*)[TBYTES]>(smem);
-  uint16_t (*s_p)[REP * 64] = reinterpret_cast<uint16_t (*)[REP * 64]>(smem + SZ_RAW);
-  float (*s_al)[REP] = reinterpret_cast<float (*)[REP]>(smem + SZ_RAW + SZ_PB);
-  float* s_wo = reinterpret_cast<float*>(smem + SZ_RAW + SZ_PB + SZ_ALW);
+  float* s_wo = reinterpret_cast<float*>(s_raw);  // wave w's partial at raw tile w
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1588,7 +1604,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
                      ((dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h) * E::size;
     const char* vb = reinterpret_cast<const char*>(dsc.v) +
                      ((dsc.batch < 0 ? (int64_t)b * dsc.v_stride_b : 0) + (int64_t)h_kv * dsc.v_stride_h) * E::size;
-    plain_rows_mfma<DT, D, REP, NW>(P, smem, s_wm, s_wl, kb, vb, dsc.k_stride_t * E::size, dsc.v_stride_t * E::size,
+    plain_rows_mfma<DT, D, REP, NW, PL_TR>(P, plain_lds_at<D, REP, NW, PL_TR>(s_raw), s_wm, s_wl, kb, vb, dsc.k_stride_t * E::size, dsc.v_stride_t * E::size,
                                     t0, t1, b, hq0, nvalid_h, wslot);
     return;
   }
@@ -1637,144 +1653,151 @@ decode_attn_kivi_kernel(DecodeParams P) {
   for (int gg = 0; gg < (DT == HALO_F16 ? NG : 1); ++gg) accz[gg] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
   float l_lane = 0.f;        // this lane's share of head hl's denominator
-  char* raw = s_raw[wave];
-  uint16_t* pw = s_p[wave];
-  float* alw = s_al[wave];
-
-  for (int it = wt0; it < wt1; it += 2) {
-    uint4 buf[2][LPT];
+  // One block pair staged at bkp, first token tokp: the score MFMAs of both
+  // blocks are independent and issue together, one online-softmax step
+  // covers their 64 tokens (one max, one rescale), and the P.V MFMAs of
+  // both follow; a second block past the range is all masked (its bytes
+  // read as zeros) and adds nothing.
+  auto do_pair = [&](const char* bkp, int tokp) {
+    const int nr0 = min(32, t1 - tokp);
+    const int nrw[2] = {nr0, min(32, t1 - (tokp + 32))};
+    // ---- scores: per block 2 row blocks of 16 tokens, code MFMAs + one zero-term MFMA per k-step
+    f32x4 sc[2][2], sz[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t off = (int64_t)(it + u - wt0) * TBYTES;
-      const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + wbyte0 + off, wbytes - off);
-#pragma unroll
-      for (int i = 0; i < LPT; ++i) buf[u][i] = buf_ld16(rr, (i * kWave + lane) * 16);
+    for (int pb = 0; pb < 2; ++pb) {
+      sc[pb][0] = sc[pb][1] = sz[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (it + u >= wt1) break;
+    for (int s = 0; s < KS; ++s) {
+      const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slab
 #pragma unroll
-      for (int i = 0; i < LPT; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[u][i];
-      wave_lds_fence();
-      const int tok0 = t0 + (it + u) * TB * 32;  // first token of the tile
-      // Blocks in pairs: the score MFMAs of both blocks are independent and
-      // issue together, one online-softmax step covers their 64 tokens
-      // (one max, one rescale), and the P.V MFMAs of both follow; a second
-      // block past the range is all masked (its tile bytes read as zeros)
-      // and adds nothing.
-      static_assert(TB % 2 == 0, "blocks are processed in pairs");
-      for (int bp = 0; bp < TB; bp += 2) {
-        const int nr0 = min(32, t1 - (tok0 + bp * 32));  // <= 0: pair past the range
-        if (nr0 <= 0) break;
-        const int nrw[2] = {nr0, min(32, t1 - (tok0 + (bp + 1) * 32))};
-        const char* bkp = raw + bp * BB;
-        // ---- scores: per block 2 row blocks of 16 tokens, code MFMAs + one zero-term MFMA per k-step
-        f32x4 sc[2][2], sz[2];
+      for (int pb = 0; pb < 2; ++pb) {
+        const char* bk = bkp + pb * BB;
+        const uint4 sk = *reinterpret_cast<const uint4*>(bk + CB + 2 * c0);
+        const uint4 zk = *reinterpret_cast<const uint4*>(bk + CB + 2 * D + 2 * c0);
+        uint4 qs, qs_lo;
+        if constexpr (DT == HALO_BF16) mul8_bf16_split(qb[s], sk, qs, qs_lo);
+        else qs = mul8<DT>(qb[s], sk);
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-          sc[pb][0] = sc[pb][1] = sz[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < 2; ++nb) {
+          const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
+          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
+          sc[pb][nb] = MfmaOp<DT>::run(cd, qs, sc[pb][nb]);
+          if constexpr (DT == HALO_BF16) sc[pb][nb] = MfmaOp<DT>::run(cd, qs_lo, sc[pb][nb]);
         }
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const int c0 = 32 * s + 8 * kg;  // first channel of this lane's k-slab
-#pragma unroll
-          for (int pb = 0; pb < 2; ++pb) {
-            const char* bk = bkp + pb * BB;
-            const uint4 sk = *reinterpret_cast<const uint4*>(bk + CB + 2 * c0);
-            const uint4 zk = *reinterpret_cast<const uint4*>(bk + CB + 2 * D + 2 * c0);
-            uint4 qs, qs_lo;
-            if constexpr (DT == HALO_BF16) mul8_bf16_split(qb[s], sk, qs, qs_lo);
-            else qs = mul8<DT>(qb[s], sk);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-              const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
-              const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
-              sc[pb][nb] = MfmaOp<DT>::run(cd, qs, sc[pb][nb]);
-              if constexpr (DT == HALO_BF16) sc[pb][nb] = MfmaOp<DT>::run(cd, qs_lo, sc[pb][nb]);
-            }
-            sz[pb] = MfmaOp<DT>::run(zk, qb[s], sz[pb]);
-          }
-        }
-        // ---- online softmax over the pair (lane: head hl, tokens 32pb + 16nb + 4kg + c)
-        float sv[2][2][4], bm = -INFINITY;
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const bool valid = nb * 16 + kg * 4 + c < nrw[pb];
-              const float s_code = DT == HALO_F16 ? sc[pb][nb][c] * kSub16Scale : sc[pb][nb][c];
-              sv[pb][nb][c] = valid ? (s_code + sz[pb][c]) * P.scale2 : -INFINITY;
-              bm = fmaxf(bm, sv[pb][nb][c]);
-            }
-        bm = rows4_max(bm);
-        const float m_new = fmaxf(m_lane, bm);
-        const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
-        m_lane = m_new;
-        float psum = 0.f;
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) {
-            float p4[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              p4[c] = __builtin_amdgcn_exp2f(sv[pb][nb][c] - ms);
-              psum += p4[c];
-            }
-            if (hl < REP)
-              *reinterpret_cast<uint2*>(pw + hl * 64 + pb * 32 + nb * 16 + kg * 4) =
-                  make_uint2(pack2<DT>(p4[0], p4[1]), pack2<DT>(p4[2], p4[3]));
-          }
-        l_lane = l_lane * alpha + psum;
-        if (lane < REP) alw[lane] = alpha;
-        wave_lds_fence();
-        // ---- P.V: per block and group, codes against p*s and the zeros against p
-        if (__builtin_amdgcn_read_exec() & __ballot(hl < REP && alpha != 1.f)) {  // some head's max moved
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = alw[min(4 * kg + e, REP - 1)];
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[db][e] *= a;
-            if constexpr (DT == HALO_F16) {
-#pragma unroll
-              for (int gg = 0; gg < NG; ++gg) accz[gg][e] *= a;
-            }
-          }
-        }
-#pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-          const char* bk = bkp + pb * BB;
-          const uint4 pa =
-              hl < REP ? *reinterpret_cast<const uint4*>(pw + hl * 64 + pb * 32 + kg * 8) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-          for (int gg = 0; gg < NG; ++gg) {
-            const uint4 sv8 = *reinterpret_cast<const uint4*>(bk + VS + 2 * (gg * 32 + kg * 8));
-            const uint4 zv8 = *reinterpret_cast<const uint4*>(bk + VZ + 2 * (gg * 32 + kg * 8));
-            uint4 ps, ps_lo;
-            if constexpr (DT == HALO_BF16) mul8_bf16_split(pa, sv8, ps, ps_lo);
-            else ps = mul8<DT>(pa, sv8);
-#pragma unroll
-            for (int d2 = 0; d2 < 2; ++d2) {
-              const int db = 2 * gg + d2;
-              const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
-              const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
-              acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
-              if constexpr (DT == HALO_BF16) {
-                acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
-                acc[db] = MfmaOp<DT>::run(pa, zv8, acc[db]);
-              }
-            }
-            // fp16: the code products carry 2^-24, so the zero term of the
-            // group (equal for all its columns) accumulates on its own
-            if constexpr (DT == HALO_F16) accz[gg] = MfmaOp<DT>::run(pa, zv8, accz[gg]);
-          }
-        }
-        wave_lds_fence();  // the next pair rewrites p and the rescale factors
+        sz[pb] = MfmaOp<DT>::run(zk, qb[s], sz[pb]);
       }
-      wave_lds_fence();  // the next tile rewrites raw
+    }
+    // ---- online softmax over the pair (lane: head hl, tokens 32pb + 16nb + 4kg + c)
+    float sv[2][2][4], bm = -INFINITY;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool valid = nb * 16 + kg * 4 + c < nrw[pb];
+          const float s_code = DT == HALO_F16 ? sc[pb][nb][c] * kSub16Scale : sc[pb][nb][c];
+          sv[pb][nb][c] = valid ? (s_code + sz[pb][c]) * P.scale2 : -INFINITY;
+          bm = fmaxf(bm, sv[pb][nb][c]);
+        }
+    bm = rows4_max(bm);
+    const float m_new = fmaxf(m_lane, bm);
+    const float ms = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+    m_lane = m_new;
+    // P operand of block pb in registers: the block's V slots 8kg..8kg+7 are
+    // tokens {4kg + c, 16 + 4kg + c} (c = 0..3), exactly this lane's scores
+    float psum = 0.f;
+    uint4 pa[2];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      float p8[8];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          p8[4 * nb + c] = __builtin_amdgcn_exp2f(sv[pb][nb][c] - ms);
+          psum += p8[4 * nb + c];
+        }
+      pa[pb] = hl < REP ? make_uint4(pack2<DT>(p8[0], p8[1]), pack2<DT>(p8[2], p8[3]), pack2<DT>(p8[4], p8[5]),
+                                     pack2<DT>(p8[6], p8[7]))
+                        : make_uint4(0, 0, 0, 0);
+    }
+    l_lane = l_lane * alpha + psum;
+    // ---- P.V: per block and group, codes against p*s and the zeros against p
+    if (__builtin_amdgcn_read_exec() & __ballot(hl < REP && alpha != 1.f)) {  // some head's max moved
+      // the output rows of this lane are heads 4kg + e; head r's factor sits on lane r
+      float ar[REP];
+#pragma unroll
+      for (int r = 0; r < REP; ++r) ar[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = ar[min(e, REP - 1)];
+#pragma unroll
+        for (int q4 = 1; q4 < 4; ++q4)
+          if (4 * q4 + e < REP) a = kg == q4 ? ar[4 * q4 + e] : a;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db][e] *= a;
+        if constexpr (DT == HALO_F16) {
+#pragma unroll
+          for (int gg = 0; gg < NG; ++gg) accz[gg][e] *= a;
+        }
+      }
+    }
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      const char* bk = bkp + pb * BB;
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg) {
+        const uint4 sv8 = *reinterpret_cast<const uint4*>(bk + VS + 2 * (gg * 32 + kg * 8));
+        const uint4 zv8 = *reinterpret_cast<const uint4*>(bk + VZ + 2 * (gg * 32 + kg * 8));
+        uint4 ps, ps_lo;
+        if constexpr (DT == HALO_BF16) mul8_bf16_split(pa[pb], sv8, ps, ps_lo);
+        else ps = mul8<DT>(pa[pb], sv8);
+#pragma unroll
+        for (int d2 = 0; d2 < 2; ++d2) {
+          const int db = 2 * gg + d2;
+          const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
+          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub(c16) : kivi_codes8<DT>(c16);
+          acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
+          if constexpr (DT == HALO_BF16) {
+            acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);
+            acc[db] = MfmaOp<DT>::run(pa[pb], zv8, acc[db]);
+          }
+        }
+        // fp16: the code products carry 2^-24, so the zero term of the
+        // group (equal for all its columns) accumulates on its own
+        if constexpr (DT == HALO_F16) accz[gg] = MfmaOp<DT>::run(pa[pb], zv8, accz[gg]);
+      }
+    }
+  };
+  // Tiles are software-pipelined through registers: tile i is staged in the
+  // wave's raw LDS tile, the loads of tile i+1 are issued into the same
+  // registers, and tile i's block pairs are computed while they are in
+  // flight.
+  char* raw = s_raw + wave * TBYTES;
+  uint4 buf[LPT];
+  auto load_tile = [&](int it) {
+    const int64_t off = (int64_t)(it - wt0) * TBYTES;
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + wbyte0 + off, wbytes - off);
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) buf[i] = buf_ld16(rr, (i * kWave + lane) * 16);
+  };
+  if (wt0 < wt1) load_tile(wt0);
+  for (int it = wt0; it < wt1; ++it) {
+    // the previous tile's reads were issued before these stores (LDS
+    // serves one wave's instructions in order)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[i];
+    asm volatile("" ::: "memory");
+    if (it + 1 < wt1) load_tile(it + 1);
+    const int tok0 = t0 + it * TB * 32;  // first token of the tile
+#pragma unroll
+    for (int bp = 0; bp < TB; bp += 2) {
+      if (tok0 + bp * 32 >= t1) break;  // pair past the range
+      do_pair(raw + bp * BB, tok0 + bp * 32);
     }
   }
   float m_run[REP], l_head[REP];
@@ -1790,7 +1813,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[db][e] = acc[db][e] * kSub16Scale + accz[db / 2][e];
   }
-  write_partial_owners<D, REP, NW, DB>(P, wslot, wave, true, true, acc, m_run, l_head, s_wo, s_wm, s_wl);
+  write_partial_owners<D, REP, NW, DB, TBYTES / 4>(P, wslot, wave, true, true, acc, m_run, l_head, s_wo, s_wm, s_wl);
 }
 
 // ---------------------------------------------------------------------------

@@ -19,19 +19,27 @@
 //   [C, C+2D)         K scale, D elements of the dtype (per channel)
 //   [C+2D, C+4D)      K zero
 //   [C+4D, 2C+4D)     V codes, channel-major rows of 32*bits/8 bytes, code
-//                     of token t at bit (t*bits) % 8 of byte t*bits/8
-//   [2C+4D, 2C+6D)    V scale, D/32 groups x 32 tokens (group-major)
+//                     of token slot s at bit (s*bits) % 8 of byte s*bits/8
+//   [2C+4D, 2C+6D)    V scale, D/32 groups x 32 token slots (group-major)
 //   [2C+6D, 2C+8D)    V zero
 // with C = 32*D*bits/8.  D=128, bits=2: 3072 bytes per block.  The V side
-// is transposed so that 8 consecutive tokens of one channel (the P.V
-// operand of one lane) are 16 contiguous bits, and 8 consecutive tokens'
-// scales (or zeros) of one group are 16 contiguous bytes.
+// is transposed, and its 32 tokens are stored in slot order: slot 8g + j
+// holds token 4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4), the tokens one
+// lane group g of a 16x16x32 MFMA holds in its score accumulator (rows
+// 4g..4g+3 of both 16-token halves).  So the P.V operand of one lane is 8
+// slots = 16 contiguous bits of one channel, its scales (or zeros) are 16
+// contiguous bytes of one group, and its p values are its own scores.
 
 #include "common.hpp"
 
 namespace halo {
 
 constexpr int kKiviG = 32;
+
+// token held by V slot s of a block, and the slot of token t
+__host__ __device__ constexpr int kivi_vtok(int s) { return (s & 4 ? 16 : 0) + 4 * (s >> 3) + (s & 3); }
+__host__ __device__ constexpr int kivi_vslot(int t) { return 8 * ((t >> 2) & 3) + 4 * (t >> 4) + (t & 3); }
+static_assert(kivi_vslot(kivi_vtok(13)) == 13 && kivi_vtok(kivi_vslot(21)) == 21, "V slot order");
 
 __host__ __device__ constexpr int kivi_code_bytes(int D, int bits) { return kKiviG * D * bits / 8; }
 __host__ __device__ constexpr int kivi_block_bytes(int D, int bits) { return 2 * kivi_code_bytes(D, bits) + 8 * D; }
@@ -143,7 +151,7 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
 #pragma unroll
     for (int c = 0; c < CPB; ++c) {
       wk |= (uint32_t)s_ck[q * CPB + c] << (c * BITS);
-      wv |= (uint32_t)s_cv[(t0 + c) * D + d] << (c * BITS);
+      wv |= (uint32_t)s_cv[kivi_vtok(t0 + c) * D + d] << (c * BITS);
     }
     out[q] = (uint8_t)wk;
     out[C + 4 * D + q] = (uint8_t)wv;
@@ -155,8 +163,9 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
     meta_k[D + d] = s_kz[d];
   }
   for (int i = tid; i < G * NG; i += 256) {
-    meta_v[i] = s_vs[i];
-    meta_v[G * NG + i] = s_vz[i];
+    const int src = (i / G) * G + kivi_vtok(i % G);  // group-major, slot order
+    meta_v[i] = s_vs[src];
+    meta_v[G * NG + i] = s_vz[src];
   }
 }
 
@@ -190,10 +199,11 @@ __global__ void __launch_bounds__(256) kivi_dequant_kernel(KiviDequantParams P) 
     const int t = e / D, d = e % D;
     const int bit = d * BITS;
     const uint32_t ck = (blk[t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
-    const int tbit = t * BITS;
+    const int ts = kivi_vslot(t);
+    const int tbit = ts * BITS;
     const uint32_t cv = (blk[C + 4 * D + d * (G * BITS / 8) + tbit / 8] >> (tbit % 8)) & MASK;
     const float sk = from_bits<DT>(meta_k[d]), zk = from_bits<DT>(meta_k[D + d]);
-    const float sv = from_bits<DT>(meta_v[(d / G) * G + t]), zv = from_bits<DT>(meta_v[G * NG + (d / G) * G + t]);
+    const float sv = from_bits<DT>(meta_v[(d / G) * G + ts]), zv = from_bits<DT>(meta_v[G * NG + (d / G) * G + ts]);
     // both fp32 results are materialised so the conversion rounds the fp32
     // sum (no mixed-precision fused add-and-convert)
     ko[(int64_t)t * P.kst + d] = bits_dt<DT>(opaque(opaque((float)ck * sk) + zk));

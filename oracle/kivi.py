@@ -104,9 +104,13 @@ def dequant_k(codes, scale, zero, *, group_size: int, dtype: str) -> np.ndarray:
 #   K codes (32 token rows x D*bits/8), K scale (D), K zero (D),
 #   V codes (D channel rows x 32*bits/8), V scale (D/32 groups x 32 tokens),
 #   V zero (D/32 x 32); scales/zeros in the storage dtype; within a row,
-#   element e of the row sits at bit (e*bits) % 8 of byte e*bits/8.
+#   element e of the row sits at bit (e*bits) % 8 of byte e*bits/8.  The V
+#   side's 32 tokens are stored in slot order: slot 8g + j holds token
+#   4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4).
 # ---------------------------------------------------------------------------
 GROUP = 32
+V_SLOT_TOKEN = np.array([(16 if s & 4 else 0) + 4 * (s >> 3) + (s & 3) for s in range(GROUP)])  # slot -> token
+V_TOKEN_SLOT = np.argsort(V_SLOT_TOKEN)                                                        # token -> slot
 
 
 def block_bytes(D: int, bits: int) -> int:
@@ -156,13 +160,13 @@ def pack_blocks(k: np.ndarray, v: np.ndarray, *, bits: int, dtype: str) -> np.nd
     ck = ck.reshape(B, H, nb, GROUP, D)
     cv = cv.reshape(B, H, nb, GROUP, D)
     NG = D // GROUP
-    sv = np.swapaxes(sv.reshape(B, H, nb, GROUP, NG), -1, -2)   # (.., NG, 32 tokens)
-    zv = np.swapaxes(zv.reshape(B, H, nb, GROUP, NG), -1, -2)
+    sv = np.swapaxes(sv.reshape(B, H, nb, GROUP, NG), -1, -2)[..., V_SLOT_TOKEN]   # (.., NG, 32 slots)
+    zv = np.swapaxes(zv.reshape(B, H, nb, GROUP, NG), -1, -2)[..., V_SLOT_TOKEN]
     parts = [
         _pack_codes(ck, bits).reshape(B, H, nb, -1),
         _dtype_bits(sk, dtype).view(np.uint8).reshape(B, H, nb, -1),
         _dtype_bits(zk, dtype).view(np.uint8).reshape(B, H, nb, -1),
-        _pack_codes(np.ascontiguousarray(np.swapaxes(cv, -1, -2)), bits).reshape(B, H, nb, -1),
+        _pack_codes(np.ascontiguousarray(np.swapaxes(cv, -1, -2)[..., V_SLOT_TOKEN]), bits).reshape(B, H, nb, -1),
         _dtype_bits(np.ascontiguousarray(sv), dtype).view(np.uint8).reshape(B, H, nb, -1),
         _dtype_bits(np.ascontiguousarray(zv), dtype).view(np.uint8).reshape(B, H, nb, -1),
     ]
@@ -181,11 +185,12 @@ def unpack_blocks(blocks: np.ndarray, *, D: int, bits: int, dtype: str):
     ck = _unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, GROUP, D * bits // 8), bits); o += C
     sk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
     zk = _bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype); o += 2 * D
-    cv = np.swapaxes(_unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, D, GROUP * bits // 8), bits), -1, -2); o += C
+    cv = np.swapaxes(_unpack_codes(blocks[..., o:o + C].reshape(B, H, nb, D, GROUP * bits // 8), bits)
+                     [..., V_TOKEN_SLOT], -1, -2); o += C
     sv = np.swapaxes(_bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype)
-                     .reshape(B, H, nb, D // GROUP, GROUP), -1, -2); o += 2 * D
+                     .reshape(B, H, nb, D // GROUP, GROUP)[..., V_TOKEN_SLOT], -1, -2); o += 2 * D
     zv = np.swapaxes(_bits_to_f32(blocks[..., o:o + 2 * D].copy().view(np.uint16), dtype)
-                     .reshape(B, H, nb, D // GROUP, GROUP), -1, -2)
+                     .reshape(B, H, nb, D // GROUP, GROUP)[..., V_TOKEN_SLOT], -1, -2)
     k = dequantize(ck, sk[:, :, :, None, :], zk[:, :, :, None, :], dtype=dtype)
     v = dequantize(cv, np.repeat(sv, GROUP, axis=-1), np.repeat(zv, GROUP, axis=-1), dtype=dtype)
     return k.reshape(B, H, nb * GROUP, D), v.reshape(B, H, nb * GROUP, D)

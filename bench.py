@@ -266,6 +266,53 @@ def bench_prefill_c3(torch, dev, *, reps: int):
     }
 
 
+def bench_dropin_c2(torch, dev, layers, qs, *, top_k: int, steps: int):
+    """The drop-in kernel module (halo_amd.triton_chunked, the import swap of
+    halo/triton_chunked.py) at the C2 layer shape: per layer one
+    ``triton_chunked_attention`` call over its 8 hot chunks plus 4 cold
+    chunks (the list the cache passes after its own selection), all in HBM.
+    Eager calls (host planning included; repeated chunk lists hit the plan
+    cache) and the same calls captured in one HIP graph per step."""
+    from halo_amd.triton_chunked import triton_chunked_attention
+
+    L = len(layers)
+    lists = [[(c.k, c.v, c.chunk_start, True) for c in lay.hot + lay.cold[:top_k]] for lay in layers]
+    q4 = [q.unsqueeze(2) for q in qs]
+
+    def step():
+        for li in range(L):
+            triton_chunked_attention(q4[li], lists[li])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(steps):
+            step()
+        e1.record(s)
+        torch.cuda.synchronize()
+        eager_us = e0.elapsed_time(e1) / steps / L * 1e3
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            step()
+        gr.replay()
+        e0.record(s)
+        for _ in range(steps):
+            gr.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    graph_us = e0.elapsed_time(e1) / steps / L * 1e3
+    return {
+        "workload": "halo_amd.triton_chunked.triton_chunked_attention per C2 layer: 12 chunks of 1024 rows "
+                    "(8 hot + 4 cold), bf16, 32/8 heads, d128, batch 1, 32 layers",
+        "eager_us_per_layer": eager_us, "graph_us_per_layer": graph_us,
+        "eager_tokens_per_s": 1e6 / (eager_us * L), "graph_tokens_per_s": 1e6 / (graph_us * L),
+    }
+
+
 def bench_kivi_c5(torch, dev, *, steps: int, layers: int = 28):
     """KIVI 2-bit cold tier, Qwen2-7B shape: 28/4 heads, d128, 131072
     context; all but the last 128 tokens in 2-bit blocks (K per channel, V per
@@ -408,7 +455,7 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c3", "c4", "c5"], default=None,
+    ap.add_argument("--only", choices=["c3", "c4", "c5", "dropin"], default=None,
                     help="run one secondary leg alone (chunked prefill, ragged batch, KIVI) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
@@ -426,13 +473,18 @@ def main() -> int:
 
     _native.lib()
     dev = torch.device("cuda:0")
+    L, H, H_kv, D, T, chunk, n_hot, top_k = args.layers, 32, 8, 128, 32768, 1024, 8, 4
     if args.only is not None:
+        def dropin():
+            lays, q_, _ = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
+                                      n_planted=4, sigma=8.0, dev=dev, seed=1)
+            return bench_dropin_c2(torch, dev, lays, q_, top_k=top_k, steps=max(1, args.steps))
         leg = {"c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
-               "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps))}[args.only]
+               "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
+               "dropin": dropin}[args.only]
         print(json.dumps({"leg": args.only, **leg()}), flush=True)
         return 0
-    L, H, H_kv, D, T, chunk, n_hot, top_k = args.layers, 32, 8, 128, 32768, 1024, 8, 4
     n_cold = T // chunk - n_hot
     scale = 1.0 / math.sqrt(D)
     log(f"building {L} layers of K/V ({L * 2 * H_kv * T * D * 2 / 2**30:.1f} GiB)")
@@ -577,6 +629,8 @@ def main() -> int:
         extra["prefill_c3"] = bench_prefill_c3(torch, dev, reps=10)
         log("ragged leg")
         extra["ragged_c4"] = bench_ragged_c4(torch, dev, steps=20)
+        log("drop-in API leg")
+        extra["dropin_c2"] = bench_dropin_c2(torch, dev, layers, qs, top_k=top_k, steps=20)
         log("kivi leg")
         del staging, staged
         torch.cuda.empty_cache()

@@ -13,6 +13,7 @@ per-launch arguments of ``update_chunk`` (halo/triton_chunked.py:151-192).
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import math
 from dataclasses import dataclass, field
@@ -355,6 +356,55 @@ def build_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype,
 # Launches of one plan are ordered when they share a stream; launching the
 # same plan on two streams at once needs a ``workspace=`` of its own for one.
 # ---------------------------------------------------------------------------
+# Plans of repeated calls: a plan's tables hold only addresses, strides,
+# chunk starts, flags and the work split, so a call whose chunk list has the
+# same addresses and layout (and the same planner options) can launch the
+# same plan again -- also when a tensor was freed and its memory reused with
+# that layout.  The launch stream is part of the key, so calls on different
+# streams never share a plan's workspace.  Least recently used plans are
+# dropped beyond PLAN_CACHE_SIZE.
+PLAN_CACHE_SIZE = 256
+_plan_cache: "collections.OrderedDict[tuple, DecodePlan]" = collections.OrderedDict()
+
+
+def _chunk_key(c) -> tuple:
+    if isinstance(c, SlotRef):
+        return ("slot", int(c.chunk_start), int(c.T), bool(c.causal), int(c.batch))
+    if hasattr(c, "blocks"):
+        b = c.blocks
+        return ("kivi", b.data_ptr(), tuple(b.shape), tuple(b.stride()), int(c.chunk_start), bool(c.causal),
+                int(c.bits), int(c.batch))
+    k, v = c.k, c.v
+    return (k.data_ptr(), tuple(k.shape), tuple(k.stride()), k.dtype, k.device,
+            v.data_ptr(), tuple(v.shape), tuple(v.stride()), v.dtype, v.device,
+            int(c.chunk_start), bool(c.causal), int(c.batch))
+
+
+def cached_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype, chunks: Sequence,
+                device, **opts) -> DecodePlan:
+    """``build_plan`` through the plan cache (same arguments).  The returned
+    plan does not keep the chunk tensors alive: the caller owns them, as for
+    a plan used once."""
+    dev = torch.device(device)
+    stream = torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0
+    key = (B, H, H_kv, D, dtype, str(dev), stream, tuple(_chunk_key(c) for c in chunks),
+           tuple(sorted((k, tuple(v) if isinstance(v, (list, tuple)) else v) for k, v in opts.items())))
+    plan = _plan_cache.get(key)
+    if plan is not None:
+        _plan_cache.move_to_end(key)
+        return plan
+    plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=chunks, device=device, **opts)
+    plan.keep = []
+    _plan_cache[key] = plan
+    while len(_plan_cache) > PLAN_CACHE_SIZE:
+        _plan_cache.popitem(last=False)
+    return plan
+
+
+def clear_plan_cache() -> None:
+    _plan_cache.clear()
+
+
 def workspace_bytes(n_work: int, rep_t: int, D: int) -> int:
     """Bytes of partials a launch with ``n_work`` items writes
     (``halo_decode_workspace_size``: n_work x rep_t x (D + 2) fp32)."""

@@ -116,7 +116,7 @@ def stream_cold_chunks(q3: torch.Tensor, cold_chunks_host: Sequence, *, scale: f
     attended as separate table entries.  ``after`` (an event) orders the
     first copy after work that fills the host chunks (e.g. the cold tier's
     device-to-host peel).  Returns the number of bytes copied."""
-    from .decode import ChunkRef, build_plan, launch
+    from .decode import ChunkRef, cached_plan, launch
     compute = torch.cuda.current_stream()
     cs = copy_stream(q3.device)
     B, H, D = q3.shape
@@ -146,7 +146,7 @@ def stream_cold_chunks(q3: torch.Tensor, cold_chunks_host: Sequence, *, scale: f
         compute.wait_event(copied[s])
         refs = [ChunkRef(kb[..., lo:hi, :], vb[..., lo:hi, :], int(c0), bool(causal))
                 for lo, hi, c0, causal in pieces]
-        plan = build_plan(B=B, H=H, H_kv=k_h.shape[1], D=D, dtype=dtype, chunks=refs, device=q3.device)
+        plan = cached_plan(B=B, H=H, H_kv=k_h.shape[1], D=D, dtype=dtype, chunks=refs, device=q3.device)
         launch(plan, q3, scale=scale, q_pos=q_pos, m=m, l=l, o=o, acc_mode=3)
         slot_free[s].record(compute)
     for kb, vb in slots:

@@ -19,7 +19,10 @@ Differences that are deliberate:
   * every function accepts ``return_lse=True`` to also return the
     log-sum-exp of the attended scores (the reference computes and drops it);
   * ``_single_launch`` attends the hot tensors in place instead of copying
-    them device-to-device into the staging buffer (:474-477).
+    them device-to-device into the staging buffer (:474-477);
+  * launch plans (descriptor and work tables on the device) are cached by
+    chunk addresses and layout (``decode.cached_plan``), so a call that
+    repeats a chunk list uploads nothing and can be captured in a HIP graph.
 """
 from __future__ import annotations
 
@@ -29,7 +32,7 @@ from typing import Optional
 import torch
 
 from . import _native as nat
-from .decode import ChunkRef, build_plan, launch
+from .decode import ChunkRef, cached_plan, launch
 
 HAS_TRITON = nat.available()
 HAS_HIP = HAS_TRITON
@@ -70,9 +73,9 @@ def update_chunk(
     if T_c == 0:
         return
     dtype = k.dtype
-    plan = build_plan(B=B, H=H, H_kv=H_KV, D=D, dtype=dtype,
-                      chunks=[ChunkRef(_al(k), _al(v), int(chunk_start), bool(apply_causal))],
-                      device=q.device)
+    plan = cached_plan(B=B, H=H, H_kv=H_KV, D=D, dtype=dtype,
+                       chunks=[ChunkRef(_al(k), _al(v), int(chunk_start), bool(apply_causal))],
+                       device=q.device)
     launch(plan, q, scale=float(scale), q_pos=q_pos, m=m, l=l, o=o, acc_mode=3)
 
 
@@ -142,8 +145,9 @@ def _run(q3: torch.Tensor, chunks: list, scale: float, q_pos: torch.Tensor,
          out_dtype, return_lse: bool, q_pos_host=None):
     B, H, D = q3.shape
     H_kv = chunks[0].k.shape[1]
-    plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=chunks[0].k.dtype, chunks=chunks,
-                      device=q3.device, q_pos_host=q_pos_host)
+    opts = {} if q_pos_host is None else {"q_pos_host": tuple(int(x) for x in q_pos_host)}
+    plan = cached_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=chunks[0].k.dtype, chunks=chunks,
+                       device=q3.device, **opts)
     out = torch.empty((B, H, D), device=q3.device, dtype=out_dtype)
     lse = torch.empty((B, H), device=q3.device, dtype=torch.float32) if return_lse else None
     launch(plan, q3, scale=scale, q_pos=q_pos, out=out, lse=lse)
@@ -212,8 +216,8 @@ def triton_chunked_attention_streamed(
     m, l, o = init_acc(B=B, H=H, D_v=D, device=q.device)
     if hot_chunks_gpu:
         refs = [ChunkRef(_al(k), _al(v), int(c0), True) for (k, v, c0) in hot_chunks_gpu]
-        plan = build_plan(B=B, H=H, H_kv=refs[0].k.shape[1], D=D, dtype=refs[0].k.dtype,
-                          chunks=refs, device=q.device)
+        plan = cached_plan(B=B, H=H, H_kv=refs[0].k.shape[1], D=D, dtype=refs[0].k.dtype,
+                           chunks=refs, device=q.device)
         launch(plan, q3, scale=float(scale), q_pos=qp, m=m, l=l, o=o, acc_mode=2)
     if cold_chunks_host:
         stream_cold_chunks(q3, cold_chunks_host, scale=float(scale), q_pos=qp,

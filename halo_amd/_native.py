@@ -106,6 +106,16 @@ _SIGNATURES = {
         _i32, _f32, _f32, _f32, _i32, _i32, _i32,  # normalize, alpha, beta, gamma, refresh, sink_pages, P_total
         _c_void_p,
     ]),
+    "halo_page_minmax": (_i32, [_c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
+                                _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
+    "halo_quest_score_topk": (_i32, [
+        _c_void_p, _i64, _i64, _i64, _i32,       # q, strides (b, h, t), dtype
+        _i32, _i32, _i32, _i32, _i32,            # B, H, H_kv, T_q, D
+        _c_void_p, _c_void_p, _i64, _i64, _i64,  # kmin, kmax, strides
+        _i32, _i32, _i32, _c_void_p,             # P, k, per_row, workspace
+        _c_void_p, _c_void_p, _c_void_p,         # dots_out, score_out, idx_out
+        _c_void_p,
+    ]),
     "halo_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64,
                                 _c_void_p, _i32, _c_void_p]),
     "halo_stage_fills": (_i32, [ctypes.POINTER(Fill), _i32, _c_void_p]),

@@ -299,6 +299,39 @@ int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           int refresh, int sink_pages, int P_total,
                           void* stream);
 
+/*
+ * Quest page metadata: channel-wise minima and maxima of `n_pages` pages of
+ * `page` rows starting at row `row0`, kmin[b,h,j,:] / kmax[b,h,j,:] in the
+ * key dtype (exact; a NaN in a channel propagates, as torch.amin / amax).
+ * Replaces the K_min / K_max build of _QuestScorerAdapter.observe_keys
+ * (baselines/quest_path_d.py:125-150); called once per page when it fills.
+ */
+int halo_page_minmax(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                     int dtype, int B, int H_kv, int D, int64_t row0, int page, int n_pages,
+                     void* kmin, void* kmax, int64_t km_stride_b, int64_t km_stride_h,
+                     int64_t km_stride_p, void* stream);
+
+/*
+ * Quest upper-bound page scores and top-k.  q (B, H, T_q, D) by strides;
+ * kmin / kmax (B, H_kv, P, D) share strides, P <= 8192, D % 16 == 0,
+ * D <= 256.  For every (b, h_kv, t) row:
+ *   bound[p] = sum_d max(qbar[d] * kmin[p,d], qbar[d] * kmax[p,d])
+ * with qbar the mean of the KV head's query heads rounded to the q dtype,
+ * fp32 products, summed in the fixed order of halo_chunk_score_topk.  The
+ * bounds go to dots_out (B, H_kv, T_q, P) fp32 when non-NULL (score_pages,
+ * baselines/quest_path_d.py:152-182).  Selection s (batch row s when
+ * per_row != 0, else all rows) scores page p as the max bound over its rows
+ * (NaN ranks as -inf), written to score_out[s*P + p] when non-NULL, and the
+ * top k pages go to idx_out[s*k + j] in descending score order, ties by
+ * lower page index (select_hot_pages, :185-205, whose torch.topk leaves
+ * ties undefined).  workspace: n_sel * P uint32 (n_sel = B if per_row else 1).
+ */
+int halo_quest_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                          int dtype, int B, int H, int H_kv, int T_q, int D,
+                          const void* kmin, const void* kmax, int64_t km_stride_b, int64_t km_stride_h,
+                          int64_t km_stride_p, int P, int k, int per_row, uint32_t* workspace,
+                          float* dots_out, float* score_out, int32_t* idx_out, void* stream);
+
 /* ---- HALOScorer: closed-form hotness and sorted top-k -------------------- */
 
 /*

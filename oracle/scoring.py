@@ -77,14 +77,21 @@ def ordered_dot(q_g: np.ndarray, k_mean: np.ndarray, dtype: str = "float32") -> 
     e < EP), each slice summed in (p, e) order with products and sums
     rounded to fp32 separately, then the G slice sums added as a balanced
     pairwise tree in slice order."""
-    D = q_g.shape[-1]
+    prod = (q_g.astype(np.float32)[..., None, :] * k_mean.astype(np.float32)).astype(np.float32)
+    return slice_order_sum(prod, dtype)
+
+
+def slice_order_sum(terms: np.ndarray, dtype: str = "float32") -> np.ndarray:
+    """Sum float32 ``terms`` (..., D) over the last axis in the kernels'
+    fixed order (the order ``ordered_dot`` describes), every addition
+    rounded to fp32.  Returns (...,) float32."""
+    D = terms.shape[-1]
     if D % 16:
         raise ValueError(f"head dim {D} must be a multiple of 16")
     EP = 4 if dtype == "float32" else 8
     G, PPS = D // 16, 16 // EP
-    prod = (q_g.astype(np.float32)[..., None, :] * k_mean.astype(np.float32)).astype(np.float32)
-    sl = prod.reshape(prod.shape[:-1] + (PPS, G, EP))
-    sl = np.swapaxes(sl, -3, -2).reshape(prod.shape[:-1] + (G, 16))  # (..., P, G, 16) in (p, e) order
+    sl = terms.astype(np.float32).reshape(terms.shape[:-1] + (PPS, G, EP))
+    sl = np.swapaxes(sl, -3, -2).reshape(terms.shape[:-1] + (G, 16))  # (..., G, 16) in (p, e) order
     part = np.zeros(sl.shape[:-1], np.float32)
     for j in range(16):
         part = (part + sl[..., j]).astype(np.float32)
@@ -209,3 +216,74 @@ def schedule(predicted: Iterable[int], *, block_size: int, locate, inflight: Opt
         inflight.add((layer, blk))
         fetch.append(blk)
     return hits, misses, fetch
+
+
+# ---------------------------------------------------------------------------
+# Quest bounding-box page scorer (baselines/quest_path_d.py:125-205)
+# ---------------------------------------------------------------------------
+
+def page_minmax(K: np.ndarray, page_size: int):
+    """Per-page channel-wise K_min / K_max over the full pages of K
+    (B, H_kv, T, D) (baselines/quest_path_d.py:125-150: ``amin`` / ``amax``
+    over the page's rows, kept in K's dtype, so exact).  A NaN in a
+    channel makes that channel's min and max NaN, as torch's amin/amax
+    propagate it.  Returns (k_min, k_max) (B, H_kv, n_full, D)."""
+    B, H_kv, T, D = K.shape
+    n_full = T // page_size
+    v = K[..., : n_full * page_size, :].reshape(B, H_kv, n_full, page_size, D)
+    return v.min(axis=-2), v.max(axis=-2)
+
+
+def quest_bound_dot(q_g: np.ndarray, k_min: np.ndarray, k_max: np.ndarray,
+                    dtype: str = "float32") -> np.ndarray:
+    """Quest's per-page upper bound sum_d max(q_d K_min_d, q_d K_max_d)
+    (baselines/quest_path_d.py:175-178) for q_g (..., D) against pages
+    (..., P, D): products rounded to fp32, the larger of the two taken
+    (NaN if either is NaN, as ``torch.maximum``), summed in the kernels'
+    fixed order (``slice_order_sum``; the reference's order is torch's).
+    Returns (..., P) float32."""
+    q = q_g.astype(np.float32)[..., None, :]
+    a = (q * k_min.astype(np.float32)).astype(np.float32)
+    b = (q * k_max.astype(np.float32)).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        m = np.maximum(a, b)  # np.maximum propagates NaN like torch.maximum
+    return slice_order_sum(m, dtype)
+
+
+def quest_scores(query: np.ndarray, k_min: np.ndarray, k_max: np.ndarray,
+                 dtype: str = "float32") -> np.ndarray:
+    """``score_pages`` (baselines/quest_path_d.py:152-182): the GQA-mean
+    query (rounded to the query dtype, kept as is when H == H_kv) against
+    every page's bounding box.  Returns (B, H_kv, T_q, P) float32."""
+    H_kv = k_min.shape[1]
+    q_g = gqa_mean_query(query, H_kv, dtype)  # (B, H_kv, T_q, D)
+    return quest_bound_dot(q_g, k_min[:, :, None], k_max[:, :, None], dtype)
+
+
+def quest_page_scores(query: np.ndarray, k_min: np.ndarray, k_max: np.ndarray,
+                      dtype: str = "float32") -> np.ndarray:
+    """Per-page score of ``select_hot_pages`` (baselines/quest_path_d.py:196):
+    the max of ``quest_scores`` over (b, h_kv, t_q).  NaN bounds are ranked
+    as -inf (the build's rule; torch.topk would rank NaN first).  Returns
+    (P,) float32."""
+    s = quest_scores(query, k_min, k_max, dtype)
+    s = np.where(np.isnan(s), -np.inf, s)
+    return s.max(axis=(0, 1, 2)).astype(np.float32)
+
+
+def quest_num_hot_pages(P: int, memory_ratio: float, min_pages_selected: int) -> int:
+    """K = min(P, max(min_pages_selected, int((P + r - 1) // r))) with the
+    reference's float ratio (baselines/quest_path_d.py:197-200)."""
+    K = max(int(min_pages_selected), int((P + memory_ratio - 1) // memory_ratio))
+    return min(K, P)
+
+
+def quest_select(query: np.ndarray, k_min: np.ndarray, k_max: np.ndarray, *, memory_ratio: float,
+                 min_pages_selected: int, dtype: str = "float32") -> np.ndarray:
+    """``select_hot_pages`` (baselines/quest_path_d.py:185-205): the top-K
+    pages by ``quest_page_scores`` in descending score order (as
+    ``torch.topk``), ties by lower page index.  Returns int64 (K,)."""
+    s = quest_page_scores(query, k_min, k_max, dtype).astype(np.float64)
+    K = quest_num_hot_pages(s.shape[0], memory_ratio, min_pages_selected)
+    order = np.lexsort((np.arange(s.shape[0]), -s))
+    return order[:K].astype(np.int64)

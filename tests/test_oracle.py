@@ -411,3 +411,112 @@ def test_kivi_blocks_roundtrip_equals_dequant():
     cv, sv, zv = K.quantize_v_per_token(x.v, bits=2, group_size=32, dtype="float16")
     assert np.array_equal(kd, K.dequant_k(ck, sk, zk, group_size=32, dtype="float16"))
     assert np.array_equal(vd, K.dequant_v(cv, sv, zv, group_size=32, dtype="float16"))
+
+
+# ---------------------------------------------------------------------------
+# Quest bounding-box scorer (baselines/quest_path_d.py:125-205)
+# ---------------------------------------------------------------------------
+
+def test_quest_page_minmax_is_the_page_extremes():
+    rng = np.random.default_rng(11)
+    K = rng.standard_normal((2, 3, 70, 16)).astype(np.float32)
+    kmin, kmax = S.page_minmax(K, 16)
+    assert kmin.shape == kmax.shape == (2, 3, 4, 16)  # the partial page is left out
+    for j in range(4):
+        rows = K[:, :, 16 * j:16 * j + 16]
+        assert np.array_equal(kmin[:, :, j], rows.min(axis=2))
+        assert np.array_equal(kmax[:, :, j], rows.max(axis=2))
+    K[0, 1, 20, 5] = np.nan  # a NaN in a page's channel makes both extremes NaN
+    kmin, kmax = S.page_minmax(K, 16)
+    assert np.isnan(kmin[0, 1, 1, 5]) and np.isnan(kmax[0, 1, 1, 5])
+    assert not np.isnan(kmin[0, 1, 1, 4]) and not np.isnan(kmin[0, 1, 0, 5])
+
+
+def test_quest_bound_is_an_upper_bound_of_every_row():
+    """sum_d max(q kmin, q kmax) >= q.k for every row of the page (a swapped
+    min/max, a dropped sign or a wrong channel breaks this), with equality
+    for page_size 1 (kmin = kmax = k), where the bound is exactly the
+    scorer's ordered dot product."""
+    rng = np.random.default_rng(12)
+    for D, dtype in ((64, "float32"), (128, "bfloat16")):
+        K = rng.standard_normal((1, 2, 64, D)).astype(np.float32)
+        q = rng.standard_normal((1, 8, 3, D)).astype(np.float32)
+        if dtype == "bfloat16":
+            K, q = round_bf16(K), round_bf16(q)
+        kmin, kmax = S.page_minmax(K, 8)
+        b = S.quest_scores(q, kmin, kmax, dtype).astype(np.float64)  # (1, 2, 3, 8)
+        qg = S.gqa_mean_query(q, 2, dtype).astype(np.float64)
+        dots = np.einsum("bhtd,bhsd->bhts", qg, K.astype(np.float64)).reshape(1, 2, 3, 8, 8)
+        slack = 1e-4 * np.abs(qg).sum(-1)[..., None]
+        assert (dots.max(axis=-1) <= b + slack).all()
+        # the bound is attained when every channel's extreme sits in one row
+        k1min, k1max = S.page_minmax(K, 1)
+        b1 = S.quest_scores(q, k1min, k1max, dtype)
+        assert np.array_equal(b1, S.ordered_dot(S.gqa_mean_query(q, 2, dtype), K[:, :, None], dtype))
+
+
+def test_quest_bound_known_answer_and_float64():
+    """A hand-computed bound, then random pages against the float64 closed
+    form within the fp32 summation bound."""
+    D = 16
+    q = np.zeros((1, 1, 1, D), np.float32)
+    q[..., 0], q[..., 1], q[..., 2] = 2.0, -3.0, 0.5
+    kmin = np.zeros((1, 1, 1, D), np.float32)
+    kmax = np.zeros((1, 1, 1, D), np.float32)
+    kmin[..., 0], kmax[..., 0] = -1.0, 4.0     # q > 0 takes kmax: 8
+    kmin[..., 1], kmax[..., 1] = -2.0, 5.0     # q < 0 takes kmin: 6
+    kmin[..., 2], kmax[..., 2] = -6.0, -1.0    # q > 0 takes kmax: -0.5
+    assert float(S.quest_scores(q, kmin, kmax)[0, 0, 0, 0]) == 13.5
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((2, 4, 2, 128)).astype(np.float32)
+    K = rng.standard_normal((2, 2, 160, 128)).astype(np.float32)
+    kmin, kmax = S.page_minmax(K, 16)
+    got = S.quest_scores(q, kmin, kmax).astype(np.float64)
+    qg = S.gqa_mean_query(q, 2).astype(np.float64)[:, :, :, None, :]
+    ref = np.maximum(qg * kmin[:, :, None].astype(np.float64), qg * kmax[:, :, None].astype(np.float64)).sum(-1)
+    mag = (np.abs(qg) * np.maximum(np.abs(kmin), np.abs(kmax))[:, :, None]).sum(-1)
+    assert (np.abs(got - ref) <= 24 * 2.0 ** -24 * mag).all()
+
+
+def test_quest_select_brute_force_and_budget():
+    rng = np.random.default_rng(14)
+    q = rng.standard_normal((2, 4, 3, 32)).astype(np.float32)
+    K = rng.standard_normal((2, 2, 12 * 8, 32)).astype(np.float32)
+    kmin, kmax = S.page_minmax(K, 8)
+    s = S.quest_page_scores(q, kmin, kmax)
+    assert np.array_equal(s, S.quest_scores(q, kmin, kmax).max(axis=(0, 1, 2)))
+    got = S.quest_select(q, kmin, kmax, memory_ratio=4.0, min_pages_selected=2)
+    brute = sorted(range(12), key=lambda p: (-float(s[p]), p))[:3]
+    assert got.tolist() == brute  # descending score order, K = ceil(12 / 4) = 3
+    # ties: equal scores rank by lower page index; NaN ranks last
+    kmin2, kmax2 = kmin.copy(), kmax.copy()
+    kmin2[:, :, 7], kmax2[:, :, 7] = kmin2[:, :, 2], kmax2[:, :, 2]
+    kmin2[:, :, 0, 0] = np.nan
+    order = S.quest_select(q, kmin2, kmax2, memory_ratio=1.0, min_pages_selected=1)
+    assert order[-1] == 0 and order.tolist().index(2) + 1 == order.tolist().index(7)
+    # the reference's float budget (baselines/quest_path_d.py:197-200)
+    assert S.quest_num_hot_pages(4, 2.0, 1) == 2
+    assert S.quest_num_hot_pages(3, 2.5, 1) == 1      # int(4.5 // 2.5), not ceil(1.2)
+    assert S.quest_num_hot_pages(10, 4.0, 4) == 4
+    assert S.quest_num_hot_pages(3, 4.0, 4) == 3      # capped at P
+
+
+def test_quest_scores_match_torch_ops():
+    """The reference test's recipe (tests/test_quest_path_d.py:147-188:
+    seeded K and q, pages of 4, torch amin/amax/maximum/sum) at D = 16,
+    against the oracle within fp32 reduction noise."""
+    torch = pytest.importorskip("torch")
+    torch.manual_seed(7)
+    B, H_kv, T, D = 1, 2, 16, 16
+    K = torch.randn(B, H_kv, T, D)
+    q = torch.randn(B, H_kv, 1, D)
+    kp = K.view(B, H_kv, 4, 4, D)
+    k_min, k_max = kp.amin(dim=-2), kp.amax(dim=-2)
+    expected = torch.maximum(q.unsqueeze(-2) * k_min.unsqueeze(-3), q.unsqueeze(-2) * k_max.unsqueeze(-3)).sum(-1)
+    omin, omax = S.page_minmax(K.numpy(), 4)
+    assert np.array_equal(omin, k_min.numpy()) and np.array_equal(omax, k_max.numpy())
+    got = S.quest_scores(q.numpy(), omin, omax)
+    assert got.shape == (B, H_kv, 1, 4)
+    np.testing.assert_allclose(got, expected.numpy(), atol=1e-5)
+    top = torch.topk(expected.amax(dim=(0, 1, 2)), 2).indices.tolist()
+    assert S.quest_select(q.numpy(), omin, omax, memory_ratio=2.0, min_pages_selected=1).tolist() == top

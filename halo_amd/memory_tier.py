@@ -223,6 +223,38 @@ class _FileBuffer:
         self._k.flush()
         self._v.flush()
 
+    def read_runs(self, layer: int, ids, out_k, out_v) -> None:
+        """Blocks ``ids`` (sorted, unique) of ``layer`` into the uint8 arrays
+        out_k / out_v (len(ids), per_block): one slice copy per run of
+        consecutive block indices."""
+        for i0, i1 in _runs_of(ids):
+            s, _ = self._range(layer, int(ids[i0]))
+            e = s + (i1 - i0) * self.per_block
+            out_k[i0:i1] = self._k[s:e].reshape(i1 - i0, self.per_block)
+            out_v[i0:i1] = self._v[s:e].reshape(i1 - i0, self.per_block)
+
+    def write_runs(self, layer: int, ids, src_k, src_v) -> None:
+        """The inverse of ``read_runs``; flushes once."""
+        for i0, i1 in _runs_of(ids):
+            s, _ = self._range(layer, int(ids[i0]))
+            e = s + (i1 - i0) * self.per_block
+            self._k[s:e] = src_k[i0:i1].reshape(-1)
+            self._v[s:e] = src_v[i0:i1].reshape(-1)
+        self._k.flush()
+        self._v.flush()
+
+
+def _runs_of(ids):
+    """(start, end) index ranges of runs of consecutive values in sorted ids."""
+    n = len(ids)
+    i = 0
+    while i < n:
+        j = i + 1
+        while j < n and int(ids[j]) == int(ids[j - 1]) + 1:
+            j += 1
+        yield i, j
+        i = j
+
 
 class TieredStorage:
     """Per-tier block stores and a per-(layer, block) tier directory
@@ -278,7 +310,7 @@ class TieredStorage:
         s, d = MemoryTier.from_name(src), MemoryTier.from_name(dst)
         if s == d:
             return
-        if MemoryTier.NVME in (s, d) or not self.on_device:
+        if not self.on_device:
             k, v = self._buffer(s).block(layer, block)
             self._buffer(d).write(layer, block, k, v)
             self.directory()[layer, block] = _TIER_CODE[d]
@@ -310,8 +342,11 @@ class TieredStorage:
             return
         if blocks.numel() == 0:
             return
-        if not self.on_device or MemoryTier.NVME in (s, d):
+        if not self.on_device:
             self._move_blocks_host(layer, blocks, s, d, only_if_in_src)
+            return
+        if MemoryTier.NVME in (s, d):
+            self._move_blocks_nvme(layer, blocks, s, d, only_if_in_src, stream)
             return
         L = nat.lib()
         blocks = blocks.to(device=self.gpu_device, dtype=torch.int32).contiguous()
@@ -337,6 +372,60 @@ class TieredStorage:
             flip.scatter_reduce_(0, idx, moved.to(torch.uint8), reduce="amax")
             dirl.copy_(torch.where(flip.bool(), torch.full_like(dirl, code_d), dirl))
         blocks.record_stream(strm)
+
+    def _move_blocks_nvme(self, layer: int, blocks: torch.Tensor, s: MemoryTier, d: MemoryTier,
+                          only_if_in_src: bool, stream: Optional[torch.cuda.Stream]) -> None:
+        """Moves to or from the NVMe tier of a device-backed store, batched:
+        one host read of the block list and of the layer's directory row, the
+        file touched once per run of consecutive blocks, one pinned staging
+        buffer, one host<->device copy and one gather (or scatter) kernel for
+        the GPU side, and the directory entries updated on the device.  File
+        I/O needs the bytes on the host, so a move out of the GPU waits for
+        its device-to-host copy (the reference's per-block ``.cpu()``,
+        halo/memory_tier.py:86-102, does the same once per block)."""
+        import numpy as np
+        strm = stream if stream is not None else torch.cuda.current_stream(self.gpu_device)
+        dirl = self.directory()[layer]
+        with torch.cuda.stream(strm):
+            ids = np.unique(blocks.reshape(-1).to("cpu").numpy().astype(np.int64))
+            ids = ids[(ids >= 0) & (ids < self.max_blocks)]
+            if only_if_in_src and ids.size:
+                codes = dirl.to("cpu").numpy()
+                ids = ids[codes[ids] == _TIER_CODE[s]]
+            if ids.size == 0:
+                return
+            n = int(ids.size)
+            ids_dev = torch.from_numpy(ids).to(self.gpu_device, non_blocking=True)
+            item = (self.num_kv_heads, self.block_size, self.head_dim)
+            sb, db = self._buffer(s), self._buffer(d)
+
+            def as_bytes(t: torch.Tensor):
+                return t.view(torch.uint8).numpy().reshape(t.shape[0], -1)
+
+            if s is MemoryTier.NVME:
+                stg_k = torch.empty((n,) + item, dtype=self.dtype, pin_memory=True)
+                stg_v = torch.empty_like(stg_k, pin_memory=True)
+                sb.read_runs(layer, ids, as_bytes(stg_k), as_bytes(stg_v))
+                if d is MemoryTier.GPU:
+                    db.keys[layer].index_copy_(0, ids_dev, stg_k.to(self.gpu_device, non_blocking=True))
+                    db.values[layer].index_copy_(0, ids_dev, stg_v.to(self.gpu_device, non_blocking=True))
+                else:  # DRAM: host memory, written in place after queued device work on it
+                    strm.synchronize()
+                    db.keys[layer][torch.from_numpy(ids)] = stg_k
+                    db.values[layer][torch.from_numpy(ids)] = stg_v
+            else:
+                if s is MemoryTier.GPU:
+                    stg_k = torch.empty((n,) + item, dtype=self.dtype, pin_memory=True)
+                    stg_v = torch.empty_like(stg_k, pin_memory=True)
+                    stg_k.copy_(sb.keys[layer].index_select(0, ids_dev), non_blocking=True)
+                    stg_v.copy_(sb.values[layer].index_select(0, ids_dev), non_blocking=True)
+                    strm.synchronize()
+                else:  # DRAM: read on the host once queued device writes to it landed
+                    strm.synchronize()
+                    idx = torch.from_numpy(ids)
+                    stg_k, stg_v = sb.keys[layer][idx], sb.values[layer][idx]
+                db.write_runs(layer, ids, as_bytes(stg_k), as_bytes(stg_v))
+            dirl.index_fill_(0, ids_dev, _TIER_CODE[d])
 
     def _move_blocks_host(self, layer: int, blocks: torch.Tensor, s: MemoryTier, d: MemoryTier,
                           only_if_in_src: bool) -> None:

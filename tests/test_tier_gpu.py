@@ -165,3 +165,50 @@ def test_chunk_scorer_plugin(dev, dtype):
                                     page_size=p)
     assert hot.tolist() == S.topk_indices(score, budget).tolist()
     assert sc.score_calls == 1 and sc.cumulative_hot_pages == budget
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_nvme_tier_batched_moves(dev, tmp_path, dtype):
+    """GPU <-> NVMe and DRAM <-> NVMe moves of block lists (duplicates, -1
+    padding, runs and gaps) are byte-exact against the file and the written
+    blocks, update the directory, skip blocks not in the source tier, and a
+    block written to NVMe survives a move back into a cleared GPU tier
+    (reference tests/test_memmap_nvme.py:14-74 on a GPU-backed store)."""
+    from halo_amd import MemoryTier, TieredStorage
+    st = TieredStorage(tiers=[MemoryTier.GPU, MemoryTier.DRAM, MemoryTier.NVME], num_layers=2, num_kv_heads=2,
+                       head_dim=64, block_size=16, dtype=dtype, device=dev, max_blocks=32,
+                       nvme_path=str(tmp_path / "nvme"))
+    data = _fill(st, 1, range(0, 20), "gpu", 3)
+    moved = [3, 4, 5, 9, 12, 13, 19]
+    blocks = torch.tensor([5, 3, -1, 4, 9, 5, 13, 12, 19, 40], dtype=torch.int32, device=dev)
+    st.move_blocks(layer=1, blocks=blocks, src="gpu", dst="nvme")
+    torch.cuda.synchronize()
+    for b in range(20):
+        assert st.locate_block(layer=1, block=b) == ("nvme" if b in moved else "gpu")
+    per = 2 * 16 * 64 * torch.tensor([], dtype=dtype).element_size()
+    raw_k = np.fromfile(tmp_path / "nvme" / "keys.bin", dtype=np.uint8)
+    for b in moved:
+        s = (1 * 32 + b) * per
+        assert np.array_equal(raw_k[s:s + per], data[b][0].contiguous().view(torch.uint8).numpy().reshape(-1))
+    # back into a cleared GPU tier; blocks not in NVMe (0, 1) are skipped
+    st._buffer(MemoryTier.GPU).keys.zero_()
+    st._buffer(MemoryTier.GPU).values.zero_()
+    st.move_blocks(layer=1, blocks=torch.tensor([0, 1] + moved, dtype=torch.int32, device=dev),
+                   src="nvme", dst="gpu")
+    torch.cuda.synchronize()
+    gk = st._buffer(MemoryTier.GPU).keys[1].cpu()
+    gv = st._buffer(MemoryTier.GPU).values[1].cpu()
+    for b in moved:
+        assert torch.equal(gk[b], data[b][0]) and torch.equal(gv[b], data[b][1])
+        assert st.locate_block(layer=1, block=b) == "gpu"
+    assert not gk[0].any() and not gk[1].any()
+    # DRAM <-> NVMe on the same store, and single-block moves
+    st.move_blocks(layer=1, blocks=torch.tensor([3, 4], dtype=torch.int32, device=dev), src="gpu", dst="dram")
+    st.move_blocks(layer=1, blocks=torch.tensor([4, 3], dtype=torch.int32, device=dev), src="dram", dst="nvme")
+    st.move_block(layer=1, block=3, src="nvme", dst="dram")
+    torch.cuda.synchronize()
+    assert st.locate_block(layer=1, block=3) == "dram" and st.locate_block(layer=1, block=4) == "nvme"
+    rk, rv = st.read_block(layer=1, block=3)
+    assert torch.equal(rk.cpu(), data[3][0]) and torch.equal(rv.cpu(), data[3][1])
+    rk, rv = st.read_block(layer=1, block=4)
+    assert torch.equal(rk.cpu(), data[4][0]) and torch.equal(rv.cpu(), data[4][1])

@@ -1772,32 +1772,38 @@ decode_attn_kivi_kernel(DecodeParams P) {
       }
     }
   };
-  // Tiles are software-pipelined through registers: tile i is staged in the
-  // wave's raw LDS tile, the loads of tile i+1 are issued into the same
-  // registers, and tile i's block pairs are computed while they are in
-  // flight.
+  // Tiles are software-pipelined through registers one block pair at a
+  // time: pair j of tile i is staged in the wave's raw LDS tile, the loads
+  // of pair j of tile i+1 are issued into the same registers, and pair j is
+  // computed while they and the rest of tile i are in flight.  The first
+  // pair's compute so waits for a pair's bytes, not a whole tile's.
+  constexpr int NSEG = TB / 2;     // block pairs per tile
+  constexpr int LPS = LPT / NSEG;  // 16-byte loads per lane per pair
+  static_assert(LPT % NSEG == 0 && LPS * 16 * kWave == 2 * BB, "a pair is a whole number of loads");
   char* raw = s_raw + wave * TBYTES;
   uint4 buf[LPT];
-  auto load_tile = [&](int it) {
+  auto load_pair = [&](int it, int sg) {
     const int64_t off = (int64_t)(it - wt0) * TBYTES;
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + wbyte0 + off, wbytes - off);
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) buf[i] = buf_ld16(rr, (i * kWave + lane) * 16);
+    for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) buf[i] = buf_ld16(rr, (i * kWave + lane) * 16);
   };
-  if (wt0 < wt1) load_tile(wt0);
-  for (int it = wt0; it < wt1; ++it) {
-    // the previous tile's reads were issued before these stores (LDS
-    // serves one wave's instructions in order)
-    asm volatile("" ::: "memory");
+  if (wt0 < wt1) {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[i];
-    asm volatile("" ::: "memory");
-    if (it + 1 < wt1) load_tile(it + 1);
+    for (int sg = 0; sg < NSEG; ++sg) load_pair(wt0, sg);
+  }
+  for (int it = wt0; it < wt1; ++it) {
     const int tok0 = t0 + it * TB * 32;  // first token of the tile
 #pragma unroll
-    for (int bp = 0; bp < TB; bp += 2) {
-      if (tok0 + bp * 32 >= t1) break;  // pair past the range
-      do_pair(raw + bp * BB, tok0 + bp * 32);
+    for (int sg = 0; sg < NSEG; ++sg) {
+      // the previous reads of this pair's bytes were issued before these
+      // stores (LDS serves one wave's instructions in order)
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[i];
+      asm volatile("" ::: "memory");
+      if (it + 1 < wt1) load_pair(it + 1, sg);
+      if (tok0 + 2 * sg * 32 < t1) do_pair(raw + 2 * sg * BB, tok0 + 2 * sg * 32);  // else: pair past the range
     }
   }
   float m_run[REP], l_head[REP];

@@ -385,6 +385,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][8 * u + e], P.scale2, -ms));
         psum += p[e];
       }
+      // keeps the row sum's additions next to their exponentials (sunk
+      // below the block they form one serial chain with the matrix pipe idle)
+      asm volatile("" : "+v"(psum));
       if (((i + 1) * EPM & 7) == 0) {
         pb[st] = make_uint4(PMfma<DT>::pack(p[0], p[1]), PMfma<DT>::pack(p[2], p[3]), PMfma<DT>::pack(p[4], p[5]),
                             PMfma<DT>::pack(p[6], p[7]));

@@ -1612,14 +1612,17 @@ decode_attn_kivi_kernel(DecodeParams P) {
   const char* base = reinterpret_cast<const char*>(dsc.k) +
                      (dsc.batch < 0 ? (int64_t)b * dsc.k_stride_b : 0) + (int64_t)h_kv * dsc.k_stride_h;
 
-  // this wave's run of tiles (token offsets relative to the chunk)
+  // this wave's run of block pairs (token offsets relative to the chunk),
+  // walked in tiles of TB blocks; the last tile of a run may be short
   const int nblk = (max(t1 - t0, 0) + 31) / 32;
-  const int ntiles = (nblk + TB - 1) / TB;
-  const int tpw = (ntiles + NW - 1) / NW;
-  const int wt0 = wave * tpw;
-  const int wt1 = min(ntiles, wt0 + tpw);
-  const int64_t wbyte0 = (int64_t)(t0 / 32 + wt0 * TB) * BB;               // first byte of the run
-  const int64_t wbytes = (int64_t)max(min(nblk, wt1 * TB) - wt0 * TB, 0) * BB;  // bytes of the run
+  const int npairs = (nblk + 1) / 2;
+  const int ppw = (npairs + NW - 1) / NW;
+  const int wb0 = min(nblk, 2 * wave * ppw);
+  const int wb1 = min(nblk, wb0 + 2 * ppw);
+  const int wtok1 = min(t1, t0 + wb1 * 32);                    // end of this wave's tokens
+  const int ntw = (wb1 - wb0 + TB - 1) / TB;                   // tiles of the run
+  const int64_t wbyte0 = (int64_t)(t0 / 32 + wb0) * BB;        // first byte of the run
+  const int64_t wbytes = (int64_t)(wb1 - wb0) * BB;            // bytes of the run
 
   const int hl = lane & 15;   // score layout: head / A-operand head
   const int kg = lane >> 4;   // score layout: row quad / lane group (8-element slab)
@@ -1783,17 +1786,17 @@ decode_attn_kivi_kernel(DecodeParams P) {
   char* raw = s_raw + wave * TBYTES;
   uint4 buf[LPT];
   auto load_pair = [&](int it, int sg) {
-    const int64_t off = (int64_t)(it - wt0) * TBYTES;
+    const int64_t off = (int64_t)it * TBYTES;
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(base + wbyte0 + off, wbytes - off);
 #pragma unroll
     for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) buf[i] = buf_ld16(rr, (i * kWave + lane) * 16);
   };
-  if (wt0 < wt1) {
+  if (ntw > 0) {
 #pragma unroll
-    for (int sg = 0; sg < NSEG; ++sg) load_pair(wt0, sg);
+    for (int sg = 0; sg < NSEG; ++sg) load_pair(0, sg);
   }
-  for (int it = wt0; it < wt1; ++it) {
-    const int tok0 = t0 + it * TB * 32;  // first token of the tile
+  for (int it = 0; it < ntw; ++it) {
+    const int tok0 = t0 + (wb0 + it * TB) * 32;  // first token of the tile
 #pragma unroll
     for (int sg = 0; sg < NSEG; ++sg) {
       // the previous reads of this pair's bytes were issued before these
@@ -1802,8 +1805,9 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
       for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[i];
       asm volatile("" ::: "memory");
-      if (it + 1 < wt1) load_pair(it + 1, sg);
-      if (tok0 + 2 * sg * 32 < t1) do_pair(raw + 2 * sg * BB, tok0 + 2 * sg * 32);  // else: pair past the range
+      if (it + 1 < ntw) load_pair(it + 1, sg);
+      // a pair past this wave's run belongs to the next wave (or to no one)
+      if (tok0 + 2 * sg * 32 < wtok1) do_pair(raw + 2 * sg * BB, tok0 + 2 * sg * 32);
     }
   }
   float m_run[REP], l_head[REP];

@@ -145,10 +145,10 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
 def choose_split(total_rows: int, n_cu: int, *, kivi: bool = False) -> int:
     """Rows per work item: aim for about 4 workgroups per CU, in whole
     4-wave x 64-row tiles, between 256 and 4096 rows.  KIVI items: about 2
-    per CU (the LDS-staged tiles allow 2 resident workgroups per CU), in
-    whole 4-wave x 128-token tiles."""
+    per CU (2 resident workgroups per CU), in whole 4-wave x 64-token block
+    pairs."""
     if kivi:
-        unit = _WAVES_PER_GROUP * 128
+        unit = _WAVES_PER_GROUP * 64
         target = max(1, total_rows // max(1, 2 * n_cu))
         split = unit * max(1, math.ceil(target / unit))
         return int(min(max(split, unit), 16 * unit))

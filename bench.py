@@ -85,6 +85,12 @@ def cpu_baseline(torch, kvs, qs, layers, *, chunk, n_hot, top_k, L, budget_s):
     share = os.environ.get("OMP_NUM_THREADS")
     if share and share.isdigit():
         threads = max(1, min(threads, int(share)))  # the host's CPU share for this GPU
+    try:  # a cgroup CPU quota below the affinity mask: more threads than that only thrash
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            threads = max(1, min(threads, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
     torch.set_num_threads(threads)
     n_sample = min(4, L)
     samples = []

@@ -1856,7 +1856,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
 // round trip; the TPC per-thread results are then combined in a fixed order
 // through LDS (deterministic run to run).
 // ---------------------------------------------------------------------------
-template <int D, int REP, int NT>
+template <int D, int REP, int NT, int MB>
 __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
   constexpr int C4 = D / 4;           // float4 columns of one head
   constexpr int TPC = NT / C4;        // threads sharing a column
@@ -1886,7 +1886,8 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
   float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
   const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4 + col;
   const float* wml = P.ws_ml + ((int64_t)gbeg * REP + r) * 2;
-  constexpr int MB = 8;  // partials per thread whose loads are issued together
+  // MB: partials per thread whose loads are issued together (one batch
+  // covers TPC * MB partials of the group)
   // Loads are unconditional (the slot index is clamped into the group) so
   // the batch is issued back to back; slots past the group are masked in
   // the merge arithmetic.
@@ -2060,12 +2061,19 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
                        st, p);
   }
   HALO_CHECK_HIP(hipGetLastError());
-  // Groups of more than 64 partials on average merge with 512 threads, so
-  // one batch of loads (8 partials per thread) covers a group.
-  if (n_work > 64 * n_groups) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512>), dim3(n_groups, REP), dim3(512), 0, st, mp);
+  // The merge block and its load batch are sized so that one batch of loads
+  // covers a group's partials where that is cheap: 256 threads x 8 partials,
+  // 512 x 8, and 512 x 9 for groups just past that (C5's 128 KIVI items plus
+  // the recent rows); a second batch is a second dependent round trip, but
+  // much larger batches measured slower (512 x 16 at 129 partials: +0.7 us).
+  const int per_group = (n_work + n_groups - 1) / n_groups;
+  constexpr int C4 = D / 4;
+  if (per_group <= (256 / C4) * 8) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 256, 8>), dim3(n_groups, REP), dim3(256), 0, st, mp);
+  } else if (per_group > (512 / C4) * 8 && per_group <= (512 / C4) * 9) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 9>), dim3(n_groups, REP), dim3(512), 0, st, mp);
   } else {
-    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 256>), dim3(n_groups, REP), dim3(256), 0, st, mp);
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 8>), dim3(n_groups, REP), dim3(512), 0, st, mp);
   }
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;

@@ -224,12 +224,14 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     link = (staging.fill_bytes + staging.miss_bytes) / steps
     log(f"{label}: {dt * 1e3:.3f} ms/step, hit rate {staging.hit_rate():.4f} over {sel} selections "
         f"({staging.misses_predicted} of {staging.misses} misses predicted), "
-        f"{staging.fills / steps:.2f} fills/step, link {link / 2**20:.1f} MiB/step")
+        f"{staging.fills / steps:.2f} fills/step, {staging.wa_commits / steps:.2f} write-allocated/step, "
+        f"link {link / 2**20:.1f} MiB/step")
     return {
         "tokens_per_s": 1.0 / dt, "ms_per_step": dt * 1e3, "hit_rate": staging.hit_rate(),
         "selections": sel, "hits": staging.hits, "misses": staging.misses,
         "misses_predicted": staging.misses_predicted,
         "fills_per_step": staging.fills / steps,
+        "write_allocated_per_step": staging.wa_commits / steps,
         "prefetch_bytes_per_step": staging.fill_bytes / steps,
         "in_place_miss_bytes_per_step": staging.miss_bytes / steps,
         "link_bytes_per_step": link, "link_gbps": link / dt / 1e9, "segments": segments,
@@ -454,6 +456,8 @@ def main() -> int:
     ap.add_argument("--slots", type=int, default=12, help="HBM staging slots per layer (of the 24 cold chunks)")
     ap.add_argument("--keep", type=int, default=6, help="best-scoring chunks per layer the cache stages")
     ap.add_argument("--max-inflight", type=int, default=16, help="host-to-device chunk copies in flight at once")
+    ap.add_argument("--write-allocate", action="store_true",
+                    help="headline cache with write-allocate (a missed chunk read in place also fills a slot)")
     ap.add_argument("--segments", type=int, default=4, help="graphs per step (layer segments) of the headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the drift / no-staging comparison legs")
@@ -510,7 +514,8 @@ def main() -> int:
     staged = [TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=lay.hot, cold=tiers[li],
                                 top_k=top_k, device=dev, cold_kmean=lay.kmean, split=args.split)
               for li, lay in enumerate(layers)]
-    staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight)
+    staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
+                          write_allocate=args.write_allocate)
     n_traj = args.warmup + args.steps
     qtraj = query_trajectory(torch, dev, steps=n_traj, L=L, H=H, D=D, rho=args.rho, seed=11)
     head = refetch_run(torch, staged, staging, qtraj, warmup=args.warmup, steps=args.steps, scale=scale,
@@ -584,7 +589,7 @@ def main() -> int:
             "chunk": chunk, "hot_chunks": n_hot, "cold_chunks": n_cold, "top_k": top_k,
             "query_drift_rho": args.rho, "staging_slots_per_layer": args.slots, "staging_keep": staging.keep,
             "staging_bytes": staging.slot_bytes, "max_fills_in_flight": args.max_inflight,
-            "segments": args.segments,
+            "write_allocate": staging.write_allocate, "segments": args.segments,
             "launch": "per step: query copy, fill commits, hip graph of 32 x (attention kernel with in-kernel "
                       "top-k selection + merge kernel), score read-back, staging policy",
         },
@@ -621,7 +626,16 @@ def main() -> int:
                                         label=f"staged, 16 slots, rho {args.rho}", warm_fills=10 ** 6,
                                         segments=args.segments)
         del big
-        staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight)
+        # the headline cache toggled between write-allocate on and off
+        other = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
+                            write_allocate=not args.write_allocate)
+        key = "no_write_allocate" if args.write_allocate else "write_allocate"
+        sweep[key] = refetch_run(torch, staged, other, qtraj, warmup=args.warmup, steps=100, scale=scale,
+                                 label=f"staged, {key.replace('_', ' ')}, rho {args.rho}", warm_fills=10 ** 6,
+                                 segments=args.segments)
+        del other
+        staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
+                              write_allocate=False)
         staging.clear()
         budget = staging.max_inflight
         staging.max_inflight = 0                # nothing staged: every selected chunk read over the host link

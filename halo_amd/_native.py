@@ -52,6 +52,7 @@ class SelectCfg(ctypes.Structure):
         ("score_out", _c_void_p),
         ("lead_items", _i32), ("n_slots", _i32),
         ("slot_catalog", _c_void_p), ("residency", _c_void_p), ("res_out", _c_void_p),
+        ("alloc_slot", _c_void_p),
     ]
 
 

@@ -256,7 +256,7 @@ constexpr int kSelMaxSlots = 64;  // HBM staging slots per selection
 // entry kSelMaxCold + r of the combined table is slot r) and the residency.
 constexpr int kSelCatOff = kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4;
 constexpr int kSelBytes = kSelCatOff + (kSelMaxCold + kSelMaxSlots) * (int)sizeof(halo_chunk_desc) + kSelMaxCold * 4;
-static_assert(sizeof(halo_select_cfg) == 120, "halo_select_cfg layout");
+static_assert(sizeof(halo_select_cfg) == 128, "halo_select_cfg layout");
 
 __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
   halo_chunk_desc u;
@@ -307,6 +307,8 @@ struct Selector {
   uint2 sw[CW];               // ... and of the staging-slot descriptors
   int rres;                   // residency of candidate tid (tid < n), -1 without staging
   int staged_slot;            // after finish(): staging slot of this slot's chunk, -1 when read in place
+  int wa_in;                  // the launch's write-allocate slot (-1: none)
+  int wa_slot;                // after finish(): slot this item writes its in-place rows into, -1: none
   // q pieces loaded up front, 8 x 16 bytes: per lane (qlane) the PPS pieces
   // of its own slice for the first QL query heads (qv[j * QL + h]), else the
   // first QB heads of the thread's share of the LDS-staged q-bar pieces
@@ -354,7 +356,13 @@ struct Selector {
       if (w < n * DW2) cw[k] = cat[w];
     }
     rres = -1;
+    wa_in = -1;
     if (S.residency != nullptr) {
+      // write-allocate: 16-bit rows (the MFMA path stores them) and one selection per launch
+      if (DT != HALO_F32 && S.alloc_slot != nullptr && !S.per_row) {
+        const int w = __builtin_amdgcn_readfirstlane(*S.alloc_slot);
+        wa_in = (w >= 0 && w < S.n_slots) ? w : -1;
+      }
       if (tid < n) rres = S.residency[(int64_t)sel * S.catalog_stride + tid];
       const uint2* scat = reinterpret_cast<const uint2*>(S.slot_catalog + (int64_t)sel * S.n_slots);
 #pragma unroll
@@ -641,15 +649,27 @@ struct Selector {
     }
     __syncthreads();
     const bool staged = S.residency != nullptr;
+    // write-allocate target: the first chosen chunk (pick order) that is not staged
+    int jm = -1;
+    if (staged && wa_in >= 0) {
+      for (int j = 0; j < kk; ++j)
+        if (s_res[s_pick[j]] < 0) {
+          jm = j;
+          break;
+        }
+    }
+    jm = __builtin_amdgcn_readfirstlane(jm);
     if (writer && S.idx_out) {
       for (int j = tid; j < S.top_k; j += NT) S.idx_out[(int64_t)sel * S.top_k + j] = j < kk ? s_pick[j] : -1;
     }
     if (writer && S.res_out) {
       for (int j = tid; j < S.top_k; j += NT)
-        S.res_out[(int64_t)sel * S.top_k + j] = (j < kk && staged) ? s_res[s_pick[j]] : -1;
+        S.res_out[(int64_t)sel * S.top_k + j] =
+            (j < kk && staged) ? (j == jm ? -2 - wa_in : s_res[s_pick[j]]) : -1;
     }
     const int pick = slot < kk ? s_pick[slot] : -1;
     staged_slot = __builtin_amdgcn_readfirstlane((pick >= 0 && staged) ? s_res[pick] : -1);
+    wa_slot = (slot == jm) ? wa_in : -1;
     return __builtin_amdgcn_readfirstlane(pick);
   }
 };
@@ -924,7 +944,8 @@ template <int DT, int D, int REP, int NW, int TR = 0>
 __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const PlainLds& lds, float (*s_wm)[REP],
                                                 float (*s_wl)[REP], const char* kbase, const char* vbase,
                                                 int64_t kst, int64_t vst, int t0, int t1, int b, int hq0,
-                                                int nvalid_h, int wslot) {
+                                                int nvalid_h, int wslot, char* kdst = nullptr,
+                                                char* vdst = nullptr, int64_t dkst = 0, int64_t dvst = 0) {
   using E = Elem<DT>;
   using L = PlainMfmaLds<D, REP, NW, TR>;
   constexpr int EP = E::per16;          // elements per 16-byte piece
@@ -1032,6 +1053,14 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const Pla
           const int r = i * RPI + my_row0;
           *reinterpret_cast<uint4*>(kt + r * RB + ((my_col ^ kswz<SL>(r)) << 4)) = buf[u][i];
         }
+        // write-allocate: the rows also go to their staging slot
+        if (kdst != nullptr) {
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const int r = i * RPI + my_row0;
+            if (r < nrows) *reinterpret_cast<uint4*>(kdst + (int64_t)(tb + r) * dkst + voff0) = buf[u][i];
+          }
+        }
         f32x4 sc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -1112,6 +1141,14 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const Pla
         for (int i = 0; i < PPL; ++i) {
           const int r = i * RPI + my_row0;
           *reinterpret_cast<uint4*>(vt + r * RB + ((my_col ^ vswz<SL>(r)) << 4)) = buf[u][i];
+        }
+        if (vdst != nullptr) {  // write-allocate
+          const int tb = ps + (it + u) * TILE;
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const int r = i * RPI + my_row0;
+            if (tb + r < pe) *reinterpret_cast<uint4*>(vdst + (int64_t)(tb + r) * dvst + voff0) = buf[u][i];
+          }
         }
         const uint16_t* pt = reinterpret_cast<const uint16_t*>(s_pall) + pair * 2 * REP * TILE +
                              ((it + u) & 1) * REP * TILE;
@@ -1202,6 +1239,8 @@ decode_attn_kernel(DecodeParams P) {
   const int h_kv = bh % P.H_kv;
   const int b = bh / P.H_kv;
   halo_chunk_desc dsc;
+  halo_chunk_desc wdst;  // write-allocate destination (selection slots that read a chunk in place)
+  bool wa = false;
   if (P.sel_on && item.x >= P.sel.slot0 && item.x < P.sel.slot0 + P.sel.top_k) {
     // selection slot: choose the chunk first (workgroup-uniform branch)
     const bool writer = (P.sel.per_row || b == 0) && h_kv == 0 && sub == 0 && item.x == P.sel.slot0 && item.z == 0;
@@ -1224,6 +1263,10 @@ decode_attn_kernel(DecodeParams P) {
         d.v_stride_t = sd.v_stride_t;
       }
       dsc = uniform_desc(d);
+      if (selr.wa_slot >= 0) {
+        wdst = uniform_desc(tbl[kSelMaxCold + selr.wa_slot]);
+        wa = true;
+      }
     } else {
       dsc = P.descs[item.x];
       dsc.T_c = 0;
@@ -1271,8 +1314,17 @@ decode_attn_kernel(DecodeParams P) {
   const int voff0 = my_col * 16;
 
   if constexpr (kMfma) {
+    char* kdst = nullptr;
+    char* vdst = nullptr;
+    if (wa) {
+      kdst = reinterpret_cast<char*>(const_cast<void*>(wdst.k)) +
+             ((dsc.batch < 0 ? (int64_t)b * wdst.k_stride_b : 0) + (int64_t)h_kv * wdst.k_stride_h) * E::size;
+      vdst = reinterpret_cast<char*>(const_cast<void*>(wdst.v)) +
+             ((dsc.batch < 0 ? (int64_t)b * wdst.v_stride_b : 0) + (int64_t)h_kv * wdst.v_stride_h) * E::size;
+    }
     plain_rows_mfma<DT, D, REP, NW>(P, plain_lds_at<D, REP, NW>(smem), s_wm, s_wl, kbase, vbase, kst, vst, t0, t1, b,
-                                    hq0, nvalid_h, wslot);
+                                    hq0, nvalid_h, wslot, kdst, vdst, wa ? wdst.k_stride_t * E::size : 0,
+                                    wa ? wdst.v_stride_t * E::size : 0);
     return;
   } else {
     // ---- VALU path (fp32): K transposed through LDS, lane groups per head.

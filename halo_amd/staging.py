@@ -38,6 +38,19 @@ segment's scores are planned while the later segments execute, so the
 scores of step t can decide that segment's residency from step t + 1 on.
 Hit and miss counts come from ``res_out``: the entry the kernel actually
 used for each chosen chunk.
+
+Write-allocate (16-bit layers, one selection per launch): each layer keeps
+two reserved free slots and names one of them in ``halo_select_cfg.
+alloc_slot`` for each launch, alternating between launches.  The launch's
+first chosen chunk that is not staged is read in place (a miss, as before)
+and its rows are also written into that slot by the kernel; ``res_out``
+reports it, and the host commits the slot as the chunk's residency when it
+processes that feedback, so a missed chunk crosses the host link once
+instead of being fetched again by a fill.  The two reservations alternate
+because feedback lags the launches: a reservation is named again only once
+the feedback of the launch that last named it has been processed (else the
+launch gets none), so a slot the host commits still holds what that launch
+wrote.
 """
 from __future__ import annotations
 
@@ -51,7 +64,7 @@ from . import _native as nat
 from .decode import ChunkRef, descs_to_device, pack_descs
 from .memory_tier import copy_stream
 
-_FREE, _FILLING, _READY, _RELEASING = 0, 1, 2, 3
+_FREE, _FILLING, _READY, _RELEASING, _RESERVED = 0, 1, 2, 3, 4
 
 
 class ColdStaging:
@@ -64,10 +77,14 @@ class ColdStaging:
     per layer are staged (default n_slots - 2); ``spare`` slots per layer are
     kept free or releasing (staged chunks outside the kept set are released
     worst rank first to keep them); ``max_inflight`` bounds the copies in
-    flight on the link."""
+    flight on the link; ``write_allocate`` reserves two slots per layer for
+    missed chunks the kernel writes while reading them (16-bit layers with
+    one selection per launch; ignored otherwise).  It pays when the
+    selection moves fast (fewer bytes over the link) and costs hits when it
+    moves slowly (the reserved slots are missing from the cache)."""
 
     def __init__(self, layers: Sequence, *, n_slots: int = 12, keep: Optional[int] = None,
-                 max_inflight: int = 8, spare: int = 0, ring: int = 16) -> None:
+                 max_inflight: int = 8, spare: int = 0, ring: int = 16, write_allocate: bool = False) -> None:
         if not layers:
             raise AssertionError("no layers")
         self.layers = list(layers)
@@ -94,7 +111,13 @@ class ColdStaging:
                         or not c.v.is_contiguous():
                     raise AssertionError(f"layer {li}: cold chunks must be contiguous pinned host tensors")
         dev = self.device
-        self.residency = torch.full((L, n), -1, dtype=torch.int32, device=dev)
+        # residency (L, n) and the per-layer write-allocate slot (L) in one
+        # device buffer, so one store kernel updates both
+        self._dev_i32 = torch.full((L * n + L,), -1, dtype=torch.int32, device=dev)
+        self.residency = self._dev_i32[:L * n].view(L, n)
+        self.alloc = self._dev_i32[L * n:]
+        self.write_allocate = bool(write_allocate) and self.n_slots >= self.top_k + 2 and all(
+            lay.dtype != torch.float32 and not lay.select_cfg.per_row for lay in self.layers)
         # one feedback row per layer: scores (fp32) | picks (int32) | residency used (int32)
         self._W = n + 2 * k
         self.feedback = torch.zeros((L, self._W), dtype=torch.float32, device=dev)
@@ -150,6 +173,13 @@ class ColdStaging:
             cfg.res_out = self.res_out[li].data_ptr()
             cfg.score_out = self.scores[li].data_ptr()
             cfg.idx_out = self.idx[li].data_ptr()
+            cfg.alloc_slot = self.alloc[li].data_ptr() if self.write_allocate else None
+        # write-allocate reservations (two per layer), launches queued and
+        # feedback rows processed per layer
+        self.wa = np.full((L, 2), -1, dtype=np.int64)
+        self._launches = np.zeros(L, dtype=np.int64)
+        self._processed = np.zeros(L, dtype=np.int64)
+        self._reserve_wa()
         self.reset_counters()
 
     # ----------------------------------------------------------------- per step
@@ -174,10 +204,22 @@ class ColdStaging:
             else:
                 rest.append(p)
         self._pending = rest
-        if done:
-            self._store([li * self.n_cold + c for li, c, _, _, _ in done], [s for _, _, s, _, _ in done])
-            for li, c, s, _, _ in done:
-                self.state[li, s] = _READY
+        idx = [li * self.n_cold + c for li, c, _, _, _ in done]
+        val = [s for _, _, s, _, _ in done]
+        for li, c, s, _, _ in done:
+            self.state[li, s] = _READY
+        if self.write_allocate:
+            base = len(self.layers) * self.n_cold
+            for li in range(lo, hi):
+                # a reservation is named again only after the feedback of the
+                # launch that last named it (two launches back) was processed
+                par = int(self._launches[li] & 1)
+                ok = self._launches[li] - self._processed[li] < 2
+                idx.append(base + li)
+                val.append(int(self.wa[li, par]) if ok else -1)
+        self._launches[lo:hi] += 1
+        if idx:
+            self._store(idx, val)
 
     def after_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
         """Queue the feedback rows of layers [lo, hi) (scores, picks,
@@ -220,6 +262,7 @@ class ColdStaging:
                 self.holds[li, s] = -1
             self._releasing = []
             self._release_ev = None
+            self._reserve_wa()
         if rows:
             self._plan(np.concatenate(rows), np.concatenate(scores))
 
@@ -229,7 +272,7 @@ class ColdStaging:
         pairs travel in the kernel arguments)."""
         idx = np.ascontiguousarray(flat_idx, dtype=np.int64)
         val = np.ascontiguousarray(values, dtype=np.int32)
-        nat.check(nat.lib().halo_store_i32(self.residency.data_ptr(), self.residency.numel(), idx.ctypes.data,
+        nat.check(nat.lib().halo_store_i32(self._dev_i32.data_ptr(), self._dev_i32.numel(), idx.ctypes.data,
                                            val.ctypes.data, len(idx), nat.stream_ptr()), "halo_store_i32")
 
     def _account(self, fb: np.ndarray, lo: int) -> None:
@@ -240,6 +283,28 @@ class ColdStaging:
         miss = valid & (res < 0)
         self.hits += int((valid & (res >= 0)).sum())
         self.misses += int(miss.sum())
+        self._processed[lo:lo + fb.shape[0]] += 1
+        if self.write_allocate:
+            wr, wj = np.nonzero(valid & (res <= -2))
+            commits_i, commits_v = [], []
+            for r, j in zip(wr.tolist(), wj.tolist()):
+                li, c, w = lo + r, int(idx[r, j]), -2 - int(res[r, j])
+                q = np.flatnonzero(self.wa[li] == w)
+                if q.size == 0:
+                    continue  # not a current reservation: nothing to commit
+                if self.slot_of[li, c] >= 0:
+                    self.wa_dups += 1  # staged or filling elsewhere meanwhile: keep the reservation
+                    continue
+                self.state[li, w] = _READY
+                self.holds[li, w] = c
+                self.slot_of[li, c] = w
+                commits_i.append(li * self.n_cold + c)
+                commits_v.append(w)
+                self.wa[li, q[0]] = -1
+                self.wa_commits += 1
+            if commits_i:
+                self._store(commits_i, commits_v)
+                self._reserve_wa()
         if miss.any():
             r, j = np.nonzero(miss)
             self.miss_bytes += int(self.chunk_bytes[lo + r, idx[r, j]].sum())
@@ -303,6 +368,18 @@ class ColdStaging:
             ev.record(torch.cuda.current_stream(self.device))
             self._release_ev = ev
 
+    def _reserve_wa(self) -> None:
+        """Give every empty write-allocate reservation a free slot (highest
+        index first, away from the fills, which take the lowest)."""
+        if not self.write_allocate:
+            return
+        for li, q in zip(*np.nonzero(self.wa < 0)):
+            free = np.flatnonzero(self.state[li] == _FREE)
+            if free.size:
+                s = int(free[-1])
+                self.state[li, s] = _RESERVED
+                self.wa[li, q] = s
+
     def _reserve(self, li: int, c: int, s: int, urgent: bool) -> tuple:
         self.state[li, s] = _FILLING
         self.holds[li, s] = c
@@ -333,11 +410,15 @@ class ColdStaging:
         torch.cuda.synchronize(self.device)
         self._pending, self._releasing, self._release_ev = [], [], None
         self._seen = self._queued
-        self.residency.fill_(-1)
+        self._dev_i32.fill_(-1)
         self.slot_of.fill(-1)
         self._last_rank.fill(self.n_cold)
         self.state.fill(_FREE)
         self.holds.fill(-1)
+        self.wa.fill(-1)
+        self._launches.fill(0)
+        self._processed.fill(0)
+        self._reserve_wa()
         torch.cuda.synchronize(self.device)
         self.reset_counters()
 
@@ -347,6 +428,7 @@ class ColdStaging:
 
     def reset_counters(self) -> None:
         self.hits = self.misses = self.fills = self.fill_bytes = self.miss_bytes = 0
+        self.wa_commits = self.wa_dups = 0
         self.misses_predicted = 0
 
     def hit_rate(self) -> float:

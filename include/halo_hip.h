@@ -166,6 +166,15 @@ typedef struct halo_select_cfg {
   const halo_chunk_desc* slot_catalog;
   const int32_t* residency;
   int32_t* res_out;
+  /* Write-allocate (NULL: off; needs residency, bf16/fp16, per_row == 0).
+   * *alloc_slot names a staging slot that no residency entry names (-1:
+   * none this launch).  The first chosen chunk (in pick order) that is not
+   * staged is read in place as usual and its rows are also written into
+   * that slot's storage by the same workgroups; res_out then holds
+   * -2 - slot for it.  The slot holds the chunk once the launch has
+   * finished, so a later launch may be pointed at it without a copy over
+   * the host link. */
+  const int32_t* alloc_slot;
 } halo_select_cfg;
 
 /*

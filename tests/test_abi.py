@@ -43,9 +43,10 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_select_cfg_layout_matches_header():
-    """halo_select_cfg: 8 pointers + 4 int64 + 6 int32 = 120 bytes, field order as declared."""
+    """halo_select_cfg: 9 pointers + 4 int64 + 6 int32 = 128 bytes, field order as declared."""
     from halo_amd import _native as nat
-    assert ctypes.sizeof(nat.SelectCfg) == 120
+    assert ctypes.sizeof(nat.SelectCfg) == 128
+    assert nat.SelectCfg.alloc_slot.offset == 120
     assert nat.SelectCfg.n_cold.offset == 56 and nat.SelectCfg.idx_out.offset == 72
     assert nat.SelectCfg.lead_items.offset == 88 and nat.SelectCfg.n_slots.offset == 92
     assert nat.SelectCfg.slot_catalog.offset == 96 and nat.SelectCfg.res_out.offset == 112

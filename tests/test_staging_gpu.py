@@ -134,3 +134,51 @@ def test_staging_validates_its_inputs(dev):
         ColdStaging(hbm, n_slots=4)              # cold chunks in HBM, not pinned host memory
     with pytest.raises(AssertionError):
         ColdStaging(staged, n_slots=4, keep=2)   # keep below top_k
+
+
+@pytest.mark.parametrize("write_allocate", [True, False])
+def test_write_allocate_commits_the_rows_read_in_place(dev, write_allocate):
+    """A missed chunk's rows, read in place over the host link, are also
+    written into the launch's reserved slot and committed as its residency:
+    every slot the cache calls resident holds its chunk's K/V bit for bit
+    (write-allocated or filled), results stay equal to the all-HBM layer, and
+    with write-allocate off nothing is committed that way."""
+    from halo_amd.staging import ColdStaging
+    hbm, staged, _, (H, D) = _setup(dev, seed=5)
+    st = ColdStaging(staged, n_slots=6, max_inflight=4, write_allocate=write_allocate)
+    assert st.write_allocate == write_allocate
+    L = len(hbm)
+    scale = 1 / math.sqrt(D)
+    reported = 0
+    for t, q in enumerate(_queries(dev, 40, L, H, D, 0.7, 6)):
+        st.before_step()
+        outs = []
+        for li in range(L):
+            o1 = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+            o2 = torch.empty_like(o1)
+            hbm[li].step(q[li], scale=scale, out=o1)
+            staged[li].step(q[li], scale=scale, out=o2)
+            outs.append((o1, o2))
+        st.after_step()
+        torch.cuda.synchronize()
+        for li, (o1, o2) in enumerate(outs):
+            assert torch.equal(o1, o2), (t, li)
+            res = st.res_out[li].cpu().numpy()
+            reported += int((res <= -2).sum())
+            # a reported write names one of the layer's reservations
+            for r in res[res <= -2]:
+                assert -2 - int(r) in set(int(w) for w in st.wa[li]) | set(range(st.n_slots))
+        st.service()
+    st.drain()
+    torch.cuda.synchronize()
+    if write_allocate:
+        assert reported > 0 and st.wa_commits > 0
+    else:
+        assert reported == 0 and st.wa_commits == 0
+    for li, lay in enumerate(staged):
+        for s in range(st.n_slots):
+            if st.state[li, s] != 2:  # READY
+                continue
+            c = int(st.holds[li, s])
+            assert torch.equal(st._slot_k[li][s].cpu(), lay.cold[c].k), (li, s, c)
+            assert torch.equal(st._slot_v[li][s].cpu(), lay.cold[c].v), (li, s, c)

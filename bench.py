@@ -276,7 +276,7 @@ def bench_prefill_c3(torch, dev, *, reps: int):
 
 def bench_dropin_c2(torch, dev, layers, qs, *, top_k: int, steps: int):
     """The drop-in kernel module (halo_amd.triton_chunked, the import swap of
-    halo/triton_chunked.py) at the C2 layer shape: per layer one
+    halo/triton_chunked.py) at the headline's layer shape: per layer one
     ``triton_chunked_attention`` call over its 8 hot chunks plus 4 cold
     chunks (the list the cache passes after its own selection), all in HBM.
     Eager calls (host planning included; repeated chunk lists hit the plan
@@ -314,7 +314,7 @@ def bench_dropin_c2(torch, dev, layers, qs, *, top_k: int, steps: int):
     torch.cuda.synchronize()
     graph_us = e0.elapsed_time(e1) / steps / L * 1e3
     return {
-        "workload": "halo_amd.triton_chunked.triton_chunked_attention per C2 layer: 12 chunks of 1024 rows "
+        "workload": "halo_amd.triton_chunked.triton_chunked_attention per 32k-context decode layer: 12 chunks of 1024 rows "
                     "(8 hot + 4 cold), bf16, 32/8 heads, d128, batch 1, 32 layers",
         "eager_us_per_layer": eager_us, "graph_us_per_layer": graph_us,
         "eager_tokens_per_s": 1e6 / (eager_us * L), "graph_tokens_per_s": 1e6 / (graph_us * L),
@@ -600,7 +600,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": "halo_decode_attn_tiered (decode_attn_kernel<bf16,128,4,4> + decode_merge_kernel<128,4>), "
-                      "one C2 layer with every selected chunk in HBM (kernel level)",
+                      "one 32k-context decode layer with every selected chunk in HBM (kernel level)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -2115,9 +2115,10 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
   HALO_CHECK_HIP(hipGetLastError());
   // The merge block and its load batch are sized so that one batch of loads
   // covers a group's partials where that is cheap: 256 threads x 8 partials,
-  // 512 x 8, and 512 x 9 for groups just past that (C5's 128 KIVI items plus
-  // the recent rows); a second batch is a second dependent round trip, but
-  // much larger batches measured slower (512 x 16 at 129 partials: +0.7 us).
+  // 512 x 8, and 512 x 9 for groups just past that (a 131072-token KIVI
+  // decode: 128 block items plus the recent rows); a second batch is a second
+  // dependent round trip, but much larger batches measured slower (512 x 16
+  // at 129 partials: +0.7 us).
   const int per_group = (n_work + n_groups - 1) / n_groups;
   constexpr int C4 = D / 4;
   if (per_group <= (256 / C4) * 8) {

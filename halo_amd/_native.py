@@ -165,13 +165,19 @@ def available() -> bool:
     return loadable() and torch.cuda.is_available()
 
 
+_gpu_seen = False
+
+
 def lib() -> ctypes.CDLL:
     """The loaded library; raises RuntimeError when it or the GPU is missing."""
+    global _gpu_seen
     handle = _load()
     if handle is None:
         raise RuntimeError(f"HALO HIP library unavailable: {_load_error}")
-    if not torch.cuda.is_available():
-        raise RuntimeError("HALO HIP kernels need a GPU (torch.cuda.is_available() is False)")
+    if not _gpu_seen:  # a GPU, once visible, stays visible for the process
+        if not torch.cuda.is_available():
+            raise RuntimeError("HALO HIP kernels need a GPU (torch.cuda.is_available() is False)")
+        _gpu_seen = True
     return handle
 
 

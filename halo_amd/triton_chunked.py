@@ -22,10 +22,14 @@ Differences that are deliberate:
     them device-to-device into the staging buffer (:474-477);
   * launch plans (descriptor and work tables on the device) are cached by
     chunk addresses and layout (``decode.cached_plan``), so a call that
-    repeats a chunk list uploads nothing and can be captured in a HIP graph.
+    repeats a chunk list uploads nothing and can be captured in a HIP graph;
+    ``triton_chunked_attention`` keeps, per chunk-list layout and stream, the
+    plan, its default query positions and the fixed launch arguments, so a
+    repeated call does one key build, two allocations and one library call.
 """
 from __future__ import annotations
 
+import collections
 import math
 from typing import Optional
 
@@ -142,7 +146,7 @@ def _qpos(q_pos, B: int, total_T: int, device) -> torch.Tensor:
 
 
 def _run(q3: torch.Tensor, chunks: list, scale: float, q_pos: torch.Tensor,
-         out_dtype, return_lse: bool, q_pos_host=None):
+         out_dtype, return_lse: bool, q_pos_host=None, want_plan: bool = False):
     B, H, D = q3.shape
     H_kv = chunks[0].k.shape[1]
     opts = {} if q_pos_host is None else {"q_pos_host": tuple(int(x) for x in q_pos_host)}
@@ -151,7 +155,39 @@ def _run(q3: torch.Tensor, chunks: list, scale: float, q_pos: torch.Tensor,
     out = torch.empty((B, H, D), device=q3.device, dtype=out_dtype)
     lse = torch.empty((B, H), device=q3.device, dtype=torch.float32) if return_lse else None
     launch(plan, q3, scale=scale, q_pos=q_pos, out=out, lse=lse)
-    return out, lse
+    return (out, lse, plan) if want_plan else (out, lse)
+
+
+# Repeated calls of triton_chunked_attention: key = the query's shape, dtype
+# and device, the stream, whether q_pos was given, and each chunk's K/V
+# addresses, shapes, strides, dtype, start and causal flag.  A chunk list
+# that needed a contiguous copy (misaligned rows) is never entered, so a hit
+# implies the checks the full path makes.  Least recently used entries go
+# beyond FAST_CACHE_SIZE.
+FAST_CACHE_SIZE = 256
+_fast: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+
+
+def clear_fast_cache() -> None:
+    _fast.clear()
+
+
+def _fast_key(q3: torch.Tensor, chunks, stream, default_pos: bool) -> tuple:
+    return (q3.shape, q3.dtype, q3.device, stream, default_pos,
+            *[(k.data_ptr(), k.shape, k.stride(), k.dtype, v.data_ptr(), v.shape, v.stride(), v.dtype,
+               int(c0), bool(causal)) for (k, v, c0, causal) in chunks])
+
+
+def _fast_entry(plan, q3: torch.Tensor, qp_default) -> tuple:
+    from .decode import plan_workspace
+    nbytes = int(nat.lib().halo_decode_workspace_size(plan.n_work, plan.rep_t, plan.D))
+    ws = plan_workspace(plan, q3.device)
+    if ws.numel() < nbytes:
+        raise AssertionError("plan workspace smaller than the launch needs")
+    mid = (plan.B, plan.H, plan.H_kv, plan.D, plan.rep_t, plan.descs.data_ptr(), plan.n_desc,
+           plan.work.data_ptr(), plan.n_work, None if plan.uniform_groups else plan.offsets.data_ptr(),
+           plan.n_groups)
+    return (plan, qp_default, mid, nat.dtype_code(plan.dtype), ws.data_ptr(), ws.numel())
 
 
 def triton_chunked_attention(
@@ -176,11 +212,32 @@ def triton_chunked_attention(
         if return_lse:
             return out, torch.full((B, H), float("-inf"), device=q.device)
         return out
-    _require()
+    L = nat.lib()  # raises RuntimeError when the library or the GPU is missing
+    stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
+    key = _fast_key(q3, chunks, stream, q_pos is None)
+    ent = _fast.get(key)
+    if ent is not None and q3.stride(-1) == 1:
+        _fast.move_to_end(key)
+        plan, qp_default, mid, dt, ws_ptr, ws_n = ent
+        qp = qp_default if q_pos is None else _qpos(q_pos, B, 0, q.device).contiguous()
+        if qp.numel() != B:
+            raise AssertionError(f"q_pos must have B={B} entries, got {qp.numel()}")
+        out = torch.empty((B, H, D), device=q.device, dtype=q.dtype)
+        lse = torch.empty((B, H), device=q.device, dtype=torch.float32) if return_lse else None
+        nat.check(L.halo_decode_attn(q3.data_ptr(), q3.stride(0), q3.stride(1), dt, *mid, qp.data_ptr(),
+                                     float(scale), None, None, None, H, 0, out.data_ptr(), dt, nat.ptr(lse),
+                                     ws_ptr, ws_n, stream), "halo_decode_attn")
+        out = out.unsqueeze(2)
+        return (out, lse) if return_lse else out
     total_T = sum(k.shape[-2] for (k, _, _, _) in chunks)
     qp = _qpos(q_pos, B, total_T, q.device)
     refs = [ChunkRef(_al(k), _al(v), int(c0), bool(causal)) for (k, v, c0, causal) in chunks]
-    out, lse = _run(q3, refs, float(scale), qp, q.dtype, return_lse)
+    out, lse, plan = _run(q3, refs, float(scale), qp, q.dtype, return_lse, want_plan=True)
+    copied = any(r.k is not k or r.v is not v for r, (k, v, _, _) in zip(refs, chunks))
+    if not copied and q3.dtype == plan.dtype and q3.is_cuda and not torch.cuda.is_current_stream_capturing():
+        _fast[key] = _fast_entry(plan, q3, qp if q_pos is None else None)
+        while len(_fast) > FAST_CACHE_SIZE:
+            _fast.popitem(last=False)
     out = out.unsqueeze(2)
     return (out, lse) if return_lse else out
 

@@ -77,3 +77,35 @@ def test_graph_capture_replays_the_eager_result(dev):
             assert torch.equal(out, eager), i
     torch.cuda.synchronize()
     assert torch.equal(triton_chunked_attention(q, chunks), ref)
+
+
+def test_repeated_calls_take_the_fast_path(dev):
+    """The second call with the same chunk layout and stream launches from
+    the fast cache: bit-identical results, with and without q_pos and LSE; a
+    misaligned chunk (copied to an aligned one) never enters the cache."""
+    from halo_amd import triton_chunked as tc
+    tc.clear_fast_cache()
+    k, v, chunks = _chunks(dev, seed=4)
+    q = torch.randn((1, 8, 1, 128), device=dev).to(torch.bfloat16)
+    o1, l1 = tc.triton_chunked_attention(q, chunks, return_lse=True)
+    assert len(tc._fast) == 1
+    for _ in range(3):
+        o2, l2 = tc.triton_chunked_attention(q, chunks, return_lse=True)
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    o3 = tc.triton_chunked_attention(q, chunks)
+    assert torch.equal(o3, o1) and len(tc._fast) == 1
+    qp = torch.tensor([700], device=dev)
+    o4 = tc.triton_chunked_attention(q, chunks, q_pos=qp)
+    o5 = tc.triton_chunked_attention(q, chunks, q_pos=qp)
+    assert len(tc._fast) == 2 and torch.equal(o4, o5)
+    torch.cuda.synchronize()
+    want, _ = A.attention_f64(q[:, :, 0].float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                              scale=1 / math.sqrt(128), q_pos=np.array([700]))
+    assert np.abs(o4[:, :, 0].float().cpu().numpy() - want).max() <= 2e-2
+    # a chunk whose rows are not 16-byte aligned goes through a copy each call
+    wide = torch.zeros((1, 2, 192, 129), device=dev, dtype=torch.bfloat16)
+    wide[..., :128] = k[:, :, :192]
+    odd = [(wide[..., :128], v[:, :, :192], 0, True)]
+    tc.triton_chunked_attention(q, odd)
+    tc.triton_chunked_attention(q, odd)
+    assert len(tc._fast) == 2

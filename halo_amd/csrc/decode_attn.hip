@@ -1765,18 +1765,36 @@ decode_attn_kivi_kernel(DecodeParams P) {
       }
     }
     // ---- online softmax over the pair (lane: head hl, tokens 32pb + 16nb + 4kg + c)
+    // score (log2 units) = (code product + zero term) * scale2, as one fma
+    // with the zero term prescaled; fp16 code products carry 2^-24
     float sv[2][2][4], bm = -INFINITY;
+    const float cs = DT == HALO_F16 ? kSub16Scale * P.scale2 : P.scale2;
+    float zs[2][4];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) zs[pb][c] = sz[pb][c] * P.scale2;
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bool valid = nb * 16 + kg * 4 + c < nrw[pb];
-          const float s_code = DT == HALO_F16 ? sc[pb][nb][c] * kSub16Scale : sc[pb][nb][c];
-          sv[pb][nb][c] = valid ? (s_code + sz[pb][c]) * P.scale2 : -INFINITY;
-          bm = fmaxf(bm, sv[pb][nb][c]);
-        }
+        for (int c = 0; c < 4; ++c) sv[pb][nb][c] = __builtin_fmaf(sc[pb][nb][c], cs, zs[pb][c]);
+    if (nrw[0] < 32 || nrw[1] < 32) {  // a short block (the run's last): mask rows past it
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (nb * 16 + kg * 4 + c >= nrw[pb]) sv[pb][nb][c] = -INFINITY;
+    }
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bm = fmaxf(bm, sv[pb][nb][c]);
     bm = rows4_max(bm);
     const float m_new = fmaxf(m_lane, bm);
     const float ms = (m_new == -INFINITY) ? 0.f : m_new;

@@ -344,7 +344,8 @@ struct Selector {
 #pragma unroll
     for (int k = 0; k < KU; ++k) {
       const int u = tid + k * NT;
-      const int t = min(u / G, triples - 1), sl = u % G;  // past the units: a valid row, loads unused
+      // past the units (or no candidates at all): a valid row, loads unused
+      const int t = min(u / G, max(triples - 1, 0)), sl = u % G;
       const char* row = km_row(S, t, P.H_kv);
 #pragma unroll
       for (int j = 0; j < PPS; ++j) kb[k][j] = *reinterpret_cast<const uint4*>(row + (sl + j * G) * 16);

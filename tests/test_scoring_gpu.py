@@ -263,17 +263,18 @@ def test_tiered_layer_in_hip_graph(dev, fused):
         assert torch.equal(got_o, out) and torch.equal(got_l, lse)
 
 
+@pytest.mark.parametrize("ctx", [[1024, 2560, 1536], [256, 2560, 512]])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
-def test_ragged_batched_decode(dev, dtype):
+def test_ragged_batched_decode(dev, dtype, ctx):
     """Per-sequence chunk tables of different lengths in one launch: each
     row scores its own cold chunks (bit-exact top-k against the oracle's
     selector, margin-checked), a row with fewer cold chunks than top_k leaves
-    -1 slots, and every row's output matches the float64 closed form over its
-    hot + selected rows."""
+    -1 slots (a row with no cold chunk at all, row 0 of the second case,
+    selects none and attends its hot rows), and every row's output matches
+    the float64 closed form over its hot + selected rows."""
     from halo_amd.decode import ChunkRef
     from halo_amd.tiered import RaggedTieredDecodeLayer
     H, H_kv, D, c, top_k = 8, 2, 128, 256, 4
-    ctx = [1024, 2560, 1536]
     rng = np.random.default_rng(17)
     rows, host = [], []
     for b, T in enumerate(ctx):

@@ -286,10 +286,15 @@ def bench_dropin_c2(torch, dev, layers, qs, *, top_k: int, steps: int):
     L = len(layers)
     lists = [[(c.k, c.v, c.chunk_start, True) for c in lay.hot + lay.cold[:top_k]] for lay in layers]
     q4 = [q.unsqueeze(2) for q in qs]
+    # the decode position is the context's last row: the default (the sum of
+    # the listed rows minus one) would place it inside the prefix and mask
+    # the hot chunks causally
+    ctx = max(c.chunk_start + c.T for c in layers[0].hot)
+    q_pos = torch.full((q4[0].shape[0],), ctx - 1, dtype=torch.int64, device=dev)
 
     def step():
         for li in range(L):
-            triton_chunked_attention(q4[li], lists[li])
+            triton_chunked_attention(q4[li], lists[li], q_pos=q_pos)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

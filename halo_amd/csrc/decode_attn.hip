@@ -1883,10 +1883,11 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
     for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) buf[i] = buf_ld16(rr, (i * kWave + lane) * 16);
   };
-  if (ntw > 0) {
-#pragma unroll
-    for (int sg = 0; sg < NSEG; ++sg) load_pair(0, sg);
-  }
+  // Every wave of the launch starts at once: the prologue asks HBM for the
+  // first pair only, so the queues hold one pair per wave and each wave's
+  // first pair lands after about half a tile's worth of chip-wide traffic;
+  // the rest of the first tile is asked for once that pair has landed.
+  if (ntw > 0) load_pair(0, 0);
   for (int it = 0; it < ntw; ++it) {
     const int tok0 = t0 + (wb0 + it * TB) * 32;  // first token of the tile
 #pragma unroll
@@ -1897,6 +1898,10 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
       for (int i = sg * LPS; i < (sg + 1) * LPS; ++i) *reinterpret_cast<uint4*>(raw + (i * kWave + lane) * 16) = buf[i];
       asm volatile("" ::: "memory");
+      if (sg == 0 && it == 0) {
+#pragma unroll
+        for (int s2 = 1; s2 < NSEG; ++s2) load_pair(0, s2);
+      }
       if (it + 1 < ntw) load_pair(it + 1, sg);
       // a pair past this wave's run belongs to the next wave (or to no one)
       if (tok0 + 2 * sg * 32 < wtok1) do_pair(raw + 2 * sg * BB, tok0 + 2 * sg * 32);

@@ -114,8 +114,11 @@ class KiviDecodeLayer:
         per = chunk_tokens // GROUP
         cold = [KiviChunkRef(cold_blocks[:, :, j:min(j + per, n)], j * GROUP, True) for j in range(0, n, per)]
         self.B, self.H, self.D = B, H, D
+        # The KIVI items fill the resident workgroup slots in the first
+        # round; the short recent-row items go last, into the slots that free
+        # up first, instead of holding back a KIVI item to a second round.
         self.plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=cold + list(recent or []),
-                               device=device, split=split)
+                               device=device, split=split, first=range(len(cold)))
 
     def step(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse=None, q_pos=None) -> None:
         from .decode import launch

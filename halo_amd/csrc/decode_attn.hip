@@ -1470,28 +1470,15 @@ decode_attn_kernel(DecodeParams P) {
 // over the dequantised cache only by the rounding of q*s and p*s (fp16: one
 // fp16 rounding; bf16: a head + remainder pair, about 2^-17).
 // ---------------------------------------------------------------------------
-// 8 consecutive 2-bit codes (16 bits) -> 8 small integers in the K/V dtype
-template <int DT>
-__device__ __forceinline__ uint4 kivi_codes8(uint32_t c16) {
+// One 16-bit word of 2-bit codes (8 elements: the even ones 2p at bits 2p,
+// the odd ones 2p+1 at bits 8+2p) -> 8 small integers in bf16, in element
+// order
+__device__ __forceinline__ uint4 kivi_codes8_bf16(uint32_t c16) {
   uint32_t w[4];
-  if constexpr (DT == HALO_F16) {
-    // t = c16 | c16 << 14 puts code 2p at bits 4p and code 2p+1 at bits
-    // 4p + 16 of (t >> 4p); 1024 + c is 0x6400 | c in fp16, and subtracting
-    // 1024 (packed) is exact
-    typedef __attribute__((ext_vector_type(2))) _Float16 h2;
-    const h2 off = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const uint32_t t = c16 | (c16 << 14);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t v = ((t >> (4 * p)) & 0x00030003u) | 0x64006400u;
-      w[p] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v) - off);
-    }
-  } else {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const bf16x2_t v = {(__bf16)(float)((c16 >> (4 * p)) & 3u), (__bf16)(float)((c16 >> (4 * p + 2)) & 3u)};
-      w[p] = __builtin_bit_cast(uint32_t, v);
-    }
+  for (int p = 0; p < 4; ++p) {
+    const bf16x2_t v = {(__bf16)(float)((c16 >> (2 * p)) & 3u), (__bf16)(float)((c16 >> (8 + 2 * p)) & 3u)};
+    w[p] = __builtin_bit_cast(uint32_t, v);
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
@@ -1510,30 +1497,25 @@ __device__ __forceinline__ void mul8_bf16_split(const uint4& a, const uint4& b, 
   hi = make_uint4(h[0], h[1], h[2], h[3]);
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
-// fp16 only: 8 consecutive 2-bit codes as the fp16 bit patterns 0..3, i.e.
-// the subnormals c * 2^-24 (exact; the matrix cores keep fp16 subnormal
-// inputs), so one shift and one mask place two codes.  Products against
-// them carry a factor 2^-24 that the caller removes exactly.
-__device__ __forceinline__ uint4 kivi_codes8_sub(uint32_t c16) {
-  const uint32_t t = c16 | (c16 << 14);
-  return make_uint4(t & 0x00030003u, (t >> 4) & 0x00030003u, (t >> 8) & 0x00030003u, (t >> 12) & 0x00030003u);
-}
-// The same codes with registers 1 and 2 masked in place instead of shifted
-// down: codes at bits 4-5 and 8-9 of each half are still fp16 subnormals,
-// c * 2^-20 and c * 2^-16, so those registers carry 2^4 and 2^8 on top of
-// the common 2^-24.  The other MFMA operand's registers 1 and 2 are scaled
-// by 2^-4 and 2^-8 (exact powers of two, kivi_prescale) to cancel them; 3
-// VALU instructions fewer per 8 codes.
+// fp16 only: one 16-bit word of 2-bit codes (8 elements: the even ones 2p
+// at bits 2p, the odd ones 2p+1 at bits 8+2p) as fp16 subnormals.  t = w |
+// w << 8 holds elements 2p and 2p+1 at bits 2p and 16+2p, so one mask per
+// register places a pair, in place: register p holds c * 4^p * 2^-24
+// (exact; the matrix cores keep fp16 subnormal inputs).  The other MFMA
+// operand's register p is scaled by 4^-p (kivi_prescale, exact powers of
+// two), and products carry a common 2^-24 that the caller removes exactly.
 __device__ __forceinline__ uint4 kivi_codes8_sub_inplace(uint32_t c16) {
-  const uint32_t t = c16 | (c16 << 14);
-  return make_uint4(t & 0x00030003u, t & 0x00300030u, t & 0x03000300u, (t >> 12) & 0x00030003u);
+  const uint32_t t = c16 | (c16 << 8);
+  return make_uint4(t & 0x00030003u, t & 0x000C000Cu, t & 0x00300030u, t & 0x00C000C0u);
 }
-// Registers 1 and 2 of an 8-element fp16 operand times 2^-4 and 2^-8.
+// Registers 1, 2 and 3 of an 8-element fp16 operand times 2^-2, 2^-4, 2^-6.
 __device__ __forceinline__ uint4 kivi_prescale(uint4 v) {
   typedef __attribute__((ext_vector_type(2))) _Float16 h2;
-  const h2 s4 = {(_Float16)0.0625f, (_Float16)0.0625f}, s8 = {(_Float16)0.00390625f, (_Float16)0.00390625f};
-  v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * s4);
-  v.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.z) * s8);
+  const h2 s2 = {(_Float16)0.25f, (_Float16)0.25f}, s4 = {(_Float16)0.0625f, (_Float16)0.0625f},
+           s6 = {(_Float16)0.015625f, (_Float16)0.015625f};
+  v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) * s2);
+  v.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.z) * s4);
+  v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) * s6);
   return v;
 }
 constexpr float kSub16Scale = 16777216.0f;  // 2^24
@@ -1719,7 +1701,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
       qb[s] = v;
     }
   }
-  uint4 qbs[DT == HALO_F16 ? KS : 1];  // fp16: q with registers 1, 2 prescaled for the in-place codes
+  uint4 qbs[DT == HALO_F16 ? KS : 1];  // fp16: q with registers 1-3 prescaled for the in-place codes
 #pragma unroll
   for (int s = 0; s < (DT == HALO_F16 ? KS : 1); ++s) qbs[s] = DT == HALO_F16 ? kivi_prescale(qb[s]) : qb[s];
   f32x4 acc[DB];
@@ -1758,7 +1740,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + (nb * 16 + hl) * RB2 + c0 / 4);
-          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub_inplace(c16) : kivi_codes8<DT>(c16);
+          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub_inplace(c16) : kivi_codes8_bf16(c16);
           sc[pb][nb] = MfmaOp<DT>::run(cd, qs, sc[pb][nb]);
           if constexpr (DT == HALO_BF16) sc[pb][nb] = MfmaOp<DT>::run(cd, qs_lo, sc[pb][nb]);
         }
@@ -1854,7 +1836,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
         for (int d2 = 0; d2 < 2; ++d2) {
           const int db = 2 * gg + d2;
           const uint32_t c16 = *reinterpret_cast<const uint16_t*>(bk + VC + (db * 16 + hl) * 8 + kg * 2);
-          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub_inplace(c16) : kivi_codes8<DT>(c16);
+          const uint4 cd = DT == HALO_F16 ? kivi_codes8_sub_inplace(c16) : kivi_codes8_bf16(c16);
           acc[db] = MfmaOp<DT>::run(ps, cd, acc[db]);
           if constexpr (DT == HALO_BF16) {
             acc[db] = MfmaOp<DT>::run(ps_lo, cd, acc[db]);

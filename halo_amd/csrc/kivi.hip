@@ -14,12 +14,12 @@
 // along the token axis).
 //
 // Block layout (one block = 32 tokens of one (b, h_kv); byte offsets):
-//   [0, C)            K codes, token-major rows of D*bits/8 bytes, code of
-//                     channel d at bit (d*bits) % 8 of byte d*bits/8
+//   [0, C)            K codes, token-major rows of D*bits/8 bytes (code
+//                     positions within a row below)
 //   [C, C+2D)         K scale, D elements of the dtype (per channel)
 //   [C+2D, C+4D)      K zero
-//   [C+4D, 2C+4D)     V codes, channel-major rows of 32*bits/8 bytes, code
-//                     of token slot s at bit (s*bits) % 8 of byte s*bits/8
+//   [C+4D, 2C+4D)     V codes, channel-major rows of 32*bits/8 bytes, one
+//                     code per token slot
 //   [2C+4D, 2C+6D)    V scale, D/32 groups x 32 token slots (group-major)
 //   [2C+6D, 2C+8D)    V zero
 // with C = 32*D*bits/8.  D=128, bits=2: 3072 bytes per block.  The V side
@@ -29,6 +29,11 @@
 // 4g..4g+3 of both 16-token halves).  So the P.V operand of one lane is 8
 // slots = 16 contiguous bits of one channel, its scales (or zeros) are 16
 // contiguous bytes of one group, and its p values are its own scores.
+// Code positions within a row: 4-bit codes, element e at bit 4e; 2-bit
+// codes, each 16-bit word holds 8 elements, the even ones (2j) at bits 2j
+// of its low byte and the odd ones (2j+1) at bits 8+2j of its high byte, so
+// that w | w << 8 holds elements 2j and 2j+1 at bits 2j and 16+2j: one mask
+// places a pair in the two fp16 halves of a register.
 
 #include "common.hpp"
 
@@ -40,6 +45,20 @@ constexpr int kKiviG = 32;
 __host__ __device__ constexpr int kivi_vtok(int s) { return (s & 4 ? 16 : 0) + 4 * (s >> 3) + (s & 3); }
 __host__ __device__ constexpr int kivi_vslot(int t) { return 8 * ((t >> 2) & 3) + 4 * (t >> 4) + (t & 3); }
 static_assert(kivi_vslot(kivi_vtok(13)) == 13 && kivi_vtok(kivi_vslot(21)) == 21, "V slot order");
+
+// element (within its row) of the code at bits [c*BITS, (c+1)*BITS) of byte q
+// of the row, and the bit position of element e (its inverse)
+template <int BITS>
+__host__ __device__ constexpr int kivi_elem(int q, int c) {
+  return BITS == 2 ? (q & ~1) * 4 + 2 * c + (q & 1) : q * (8 / BITS) + c;
+}
+template <int BITS>
+__host__ __device__ constexpr int kivi_bit(int e) {
+  return BITS == 2 ? 16 * (e >> 3) + 2 * ((e & 7) >> 1) + 8 * (e & 1) : e * BITS;
+}
+static_assert(kivi_bit<2>(kivi_elem<2>(5, 3)) == 5 * 8 + 3 * 2 && kivi_bit<2>(kivi_elem<2>(6, 1)) == 6 * 8 + 2 &&
+                  kivi_bit<4>(kivi_elem<4>(3, 1)) == 3 * 8 + 4,
+              "code positions");
 
 __host__ __device__ constexpr int kivi_code_bytes(int D, int bits) { return kKiviG * D * bits / 8; }
 __host__ __device__ constexpr int kivi_block_bytes(int D, int bits) { return 2 * kivi_code_bytes(D, bits) + 8 * D; }
@@ -145,13 +164,15 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
   __syncthreads();
   uint8_t* out = P.blocks + (int64_t)b * P.bsb + (int64_t)h * P.bsh + (int64_t)j * kivi_block_bytes(D, BITS);
   constexpr int VRB = G * BITS / 8;  // V code bytes per channel row
+  constexpr int RKB = D * BITS / 8;  // K code bytes per token row
   for (int q = tid; q < C; q += 256) {
     uint32_t wk = 0, wv = 0;
-    const int d = q / VRB, t0 = (q % VRB) * CPB;
+    const int d = q / VRB, qv = q % VRB;
 #pragma unroll
     for (int c = 0; c < CPB; ++c) {
-      wk |= (uint32_t)s_ck[q * CPB + c] << (c * BITS);
-      wv |= (uint32_t)s_cv[kivi_vtok(t0 + c) * D + d] << (c * BITS);
+      // K rows and V rows are whole 16-bit words: positions use the row's byte
+      wk |= (uint32_t)s_ck[(q / RKB) * D + kivi_elem<BITS>(q % RKB, c)] << (c * BITS);
+      wv |= (uint32_t)s_cv[kivi_vtok(kivi_elem<BITS>(qv, c)) * D + d] << (c * BITS);
     }
     out[q] = (uint8_t)wk;
     out[C + 4 * D + q] = (uint8_t)wv;
@@ -197,10 +218,10 @@ __global__ void __launch_bounds__(256) kivi_dequant_kernel(KiviDequantParams P) 
   uint16_t* vo = reinterpret_cast<uint16_t*>(P.v) + (int64_t)b * P.vsb + (int64_t)h * P.vsh + (int64_t)j * G * P.vst;
   for (int e = tid; e < G * D; e += 256) {
     const int t = e / D, d = e % D;
-    const int bit = d * BITS;
+    const int bit = kivi_bit<BITS>(d);
     const uint32_t ck = (blk[t * (D * BITS / 8) + bit / 8] >> (bit % 8)) & MASK;
     const int ts = kivi_vslot(t);
-    const int tbit = ts * BITS;
+    const int tbit = kivi_bit<BITS>(ts);
     const uint32_t cv = (blk[C + 4 * D + d * (G * BITS / 8) + tbit / 8] >> (tbit % 8)) & MASK;
     const float sk = from_bits<DT>(meta_k[d]), zk = from_bits<DT>(meta_k[D + d]);
     const float sv = from_bits<DT>(meta_v[(d / G) * G + ts]), zv = from_bits<DT>(meta_v[G * NG + (d / G) * G + ts]);

@@ -103,10 +103,12 @@ def dequant_k(codes, scale, zero, *, group_size: int, dtype: str) -> np.ndarray:
 # kivi_cache.py:50-53).  One block = 32 tokens of one (b, h_kv):
 #   K codes (32 token rows x D*bits/8), K scale (D), K zero (D),
 #   V codes (D channel rows x 32*bits/8), V scale (D/32 groups x 32 tokens),
-#   V zero (D/32 x 32); scales/zeros in the storage dtype; within a row,
-#   element e of the row sits at bit (e*bits) % 8 of byte e*bits/8.  The V
-#   side's 32 tokens are stored in slot order: slot 8g + j holds token
-#   4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4).
+#   V zero (D/32 x 32); scales/zeros in the storage dtype.  Within a row:
+#   4-bit codes, element e at bit 4e; 2-bit codes, each 16-bit word holds 8
+#   elements, the even ones (2j) at bits 2j of its low byte and the odd ones
+#   (2j+1) at bits 8+2j of its high byte.  The V side's 32 tokens are stored
+#   in slot order: slot 8g + j holds token 4g + j (j < 4) or 16 + 4g + j - 4
+#   (j >= 4).
 # ---------------------------------------------------------------------------
 GROUP = 32
 V_SLOT_TOKEN = np.array([(16 if s & 4 else 0) + 4 * (s >> 3) + (s & 3) for s in range(GROUP)])  # slot -> token
@@ -133,21 +135,29 @@ def _bits_to_f32(b: np.ndarray, dtype: str) -> np.ndarray:
     return bf16_bits_to_f32(b)
 
 
+def code_bit(n: int, bits: int) -> np.ndarray:
+    """Bit position, within a row, of each of the row's n elements."""
+    e = np.arange(n)
+    if bits == 2:
+        return 16 * (e >> 3) + 2 * ((e & 7) >> 1) + 8 * (e & 1)
+    return e * bits
+
+
 def _pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
-    """codes (..., D) uint8 -> (..., D*bits/8) bytes, low bits = lower index."""
-    per = 8 // bits
-    c = codes.reshape(*codes.shape[:-1], codes.shape[-1] // per, per).astype(np.uint32)
-    out = np.zeros(c.shape[:-1], np.uint32)
-    for i in range(per):
-        out |= c[..., i] << (i * bits)
+    """codes (..., D) uint8 -> (..., D*bits/8) bytes, element e at code_bit(D, bits)[e]."""
+    n = codes.shape[-1]
+    pos = code_bit(n, bits)
+    out = np.zeros((*codes.shape[:-1], n * bits // 8), np.uint32)
+    for e in range(n):
+        out[..., pos[e] >> 3] |= codes[..., e].astype(np.uint32) << np.uint32(pos[e] & 7)
     return out.astype(np.uint8)
 
 
 def _unpack_codes(packed: np.ndarray, bits: int) -> np.ndarray:
-    per = 8 // bits
-    p = packed.astype(np.uint32)[..., None]
-    sh = (np.arange(per, dtype=np.uint32) * bits)
-    return ((p >> sh) & ((1 << bits) - 1)).reshape(*packed.shape[:-1], packed.shape[-1] * per).astype(np.uint8)
+    n = packed.shape[-1] * 8 // bits
+    pos = code_bit(n, bits)
+    p = packed.astype(np.uint32)
+    return ((p[..., pos >> 3] >> (pos & 7).astype(np.uint32)) & np.uint32((1 << bits) - 1)).astype(np.uint8)
 
 
 def pack_blocks(k: np.ndarray, v: np.ndarray, *, bits: int, dtype: str) -> np.ndarray:

@@ -402,6 +402,37 @@ def test_kivi_block_layout_known_answer():
     assert (vs[:32] == np.float16(1.0)).all() and (vs[32:] == np.float16(0.0)).all()
 
 
+def test_kivi_code_positions_known_answer():
+    """2-bit code positions within a row, by hand: in every 16-bit word the
+    even elements 0, 2, 4, 6 sit at bits 0, 2, 4, 6 of the low byte and the
+    odd elements 1, 3, 5, 7 at bits 0, 2, 4, 6 of the high byte.  K channel d
+    ramps (t + d) % 4 over the tokens (scale 1, zero 0), so the code of
+    (token t, channel d) is (t + d) % 4; V channel 0 of token t is t % 4 with
+    channels 30 and 31 pinning the token's range to [0, 3], so the V row of
+    channel 0 holds code token % 4 at each slot (slot 8g + j: token 4g + j,
+    or 16 + 4g + j - 4 for j >= 4)."""
+    from oracle import kivi as K
+    D = 32
+    t = np.arange(32)
+    k = np.stack([(t + d) % 4 for d in range(D)], axis=-1).astype(np.float32)[None, None]
+    v = np.zeros((1, 1, 32, D), np.float32)
+    v[0, 0, :, 0] = t % 4
+    v[0, 0, :, 31] = 3.0
+    b = K.pack_blocks(k, v, bits=2, dtype="float16")[0, 0, 0]
+    rowb = D * 2 // 8
+    for tok in range(32):
+        for w in range(rowb // 2):
+            lo = sum(((tok + 8 * w + 2 * j) % 4) << (2 * j) for j in range(4))
+            hi = sum(((tok + 8 * w + 2 * j + 1) % 4) << (2 * j) for j in range(4))
+            assert (int(b[tok * rowb + 2 * w]), int(b[tok * rowb + 2 * w + 1])) == (lo, hi), (tok, w)
+    slot_token = [(16 if s & 4 else 0) + 4 * (s >> 3) + (s & 3) for s in range(32)]
+    vc = 32 * rowb + 4 * D
+    for w in range(4):                                              # channel 0: 8 bytes = 4 words
+        lo = sum((slot_token[8 * w + 2 * j] % 4) << (2 * j) for j in range(4))
+        hi = sum((slot_token[8 * w + 2 * j + 1] % 4) << (2 * j) for j in range(4))
+        assert (int(b[vc + 2 * w]), int(b[vc + 2 * w + 1])) == (lo, hi), w
+
+
 def test_kivi_blocks_roundtrip_equals_dequant():
     from oracle import kivi as K
     from oracle.inputs import decode_inputs

@@ -368,12 +368,16 @@ int halo_topk_sorted(const float* score, int K, int k, int64_t* idx_out, void* s
 /*
  * Block format: one block = 32 tokens of one (b, h_kv), all in one
  * contiguous record of halo_kivi_block_bytes(D, bits) bytes:
- *   K codes   32 token rows of D*bits/8 bytes (code of channel d at bit
- *             (d*bits) % 8 of byte d*bits/8; K is grouped per channel over
- *             the block's 32 tokens)
+ *   K codes   32 token rows of D*bits/8 bytes, one code per channel (K is
+ *             grouped per channel over the block's 32 tokens)
  *   K scale   D elements of the storage dtype, then K zero (D elements)
- *   V codes   as K codes (V is grouped per token over 32 channels)
- *   V scale   32 x D/32 elements (token-major), then V zero (same)
+ *   V codes   D channel rows of 32*bits/8 bytes, one code per token slot
+ *             (V is grouped per token over 32 channels); slot 8g + j holds
+ *             token 4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4)
+ *   V scale   D/32 groups x 32 token slots (group-major), then V zero (same)
+ * Code positions within a row: 4-bit codes, element e at bit 4e; 2-bit
+ * codes, each 16-bit word holds 8 elements, the even ones (2j) at bits 2j of
+ * its low byte and the odd ones (2j+1) at bits 8+2j of its high byte.
  * D=128, bits=2: 3072 bytes per block (5.33x smaller than fp16 K+V).
  * The reference keeps unpacked int8 codes plus separate scale/zero tensors
  * (baselines/kivi_cache.py:50-69, :121-195); this layout is this library's.

@@ -172,10 +172,40 @@ def clear_fast_cache() -> None:
     _fast.clear()
 
 
-def _fast_key(q3: torch.Tensor, chunks, stream, default_pos: bool) -> tuple:
+def _load_layout_key():
+    """The prebuilt host extension (halo_amd/_lib/fastkey_build, made by
+    build()) that reads the chunk list's layout in C++, or None."""
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "fastkey_build", "_halo_fastkey.so")
+    if not os.path.exists(path):
+        return None
+    spec = importlib.util.spec_from_file_location("_halo_fastkey", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.chunk_layout_key
+
+
+_layout_key = _load_layout_key()
+
+
+def _fast_key_py(q3: torch.Tensor, chunks, stream, default_pos: bool) -> tuple:
     return (q3.shape, q3.dtype, q3.device, stream, default_pos,
             *[(k.data_ptr(), k.shape, k.stride(), k.dtype, v.data_ptr(), v.shape, v.stride(), v.dtype,
                int(c0), bool(causal)) for (k, v, c0, causal) in chunks])
+
+
+def _fast_key(q3: torch.Tensor, chunks, stream, default_pos: bool) -> tuple:
+    """Key of the per-layout fast path: the query's shape, dtype and device,
+    the stream, whether q_pos was defaulted, and every chunk's K/V address,
+    dtype, sizes and strides with its start and causal flag (read in C++ when
+    the host extension is built: ~4 us instead of ~15 us for 12 chunks)."""
+    if _layout_key is not None:
+        try:
+            return (q3.shape, q3.dtype, q3.device, stream, default_pos, _layout_key(chunks))
+        except (TypeError, RuntimeError):
+            pass
+    return _fast_key_py(q3, chunks, stream, default_pos)
 
 
 def _fast_entry(plan, q3: torch.Tensor, qp_default) -> tuple:

@@ -169,18 +169,25 @@ def query_trajectory(torch, dev, *, steps, L, H, D, rho, seed):
     return out
 
 
-def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, warm_fills=None, segments=4):
+def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, warm_fills=None, segments=4,
+                record=None, lses=None):
     """Timed decode steps over the staged layers.  A step writes the next
     queries, then runs the layers as ``segments`` consecutive HIP graphs;
     before each segment the fills that landed for its layers are committed,
     after it its scores go back to the host, and while the next segment runs
     the host plans the previous segment's fills (so they have one step to
-    land).  Returns the reading."""
+    land).  Returns the reading.
+
+    ``record(t, lo, hi, outs)``, if given, is called right after segment
+    [lo, hi) of step t is replayed, on the replay stream (to enqueue copies
+    of that step's outputs: the loop itself never synchronises); ``lses``
+    (one (1, H) fp32 tensor per layer) makes the graphs write the LSEs too."""
     dev = qtraj.device
     L = len(staged)
     H, D = staged[0].H, staged[0].D
     qbuf = torch.empty((L, 1, H, D), device=dev, dtype=torch.bfloat16)
     outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    lse_of = (lambda li: lses[li]) if lses is not None else (lambda li: None)
     bounds = [(g * L // segments, (g + 1) * L // segments) for g in range(segments)]
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -189,13 +196,13 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     with torch.cuda.stream(s):
         qbuf.copy_(qtraj[0])
         for li in range(L):
-            staged[li].step(qbuf[li], scale=scale, out=outs[li])
+            staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li))
         torch.cuda.synchronize()
         for lo, hi in bounds:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
                 for li in range(lo, hi):
-                    staged[li].step(qbuf[li], scale=scale, out=outs[li])
+                    staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li))
             graphs.append(g)
         torch.cuda.synchronize()
         t0 = 0.0
@@ -214,6 +221,8 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
                 if lo == 0:
                     qbuf.copy_(qtraj[t % n_traj], non_blocking=True)
                 g.replay()
+                if record is not None:
+                    record(t, lo, hi, outs)
                 staging.after_step(lo, hi)
                 staging.service()
         torch.cuda.synchronize()

@@ -119,6 +119,7 @@ _SIGNATURES = {
     ]),
     "halo_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i32, _i64,
                                 _c_void_p, _i32, _c_void_p]),
+    "halo_set_tier": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p]),
     "halo_stage_fills": (_i32, [ctypes.POINTER(Fill), _i32, _c_void_p]),
     "halo_store_i32": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "halo_host_device_pointer": (_i32, [_c_void_p, ctypes.POINTER(_c_void_p)]),

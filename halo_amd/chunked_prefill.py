@@ -30,14 +30,17 @@ def _peel_all_layers(cache) -> None:
 def _pick(logits: torch.Tensor, do_sample: bool, temperature: float, top_p: float,
           generator: Optional[torch.Generator]) -> torch.Tensor:
     """Next token (B, 1): argmax, or a draw from the temperature / nucleus
-    filtered distribution."""
+    filtered distribution.  The nucleus keeps the sorted tokens whose
+    cumulative probability is at most ``top_p``, and always the most likely
+    one (halo/chunked_prefill.py:150-163)."""
     if not do_sample:
         return logits.argmax(dim=-1, keepdim=True)
     probs = torch.softmax(logits.float() / max(temperature, 1e-6), dim=-1)
     if top_p < 1.0:
         p_sorted, order = probs.sort(dim=-1, descending=True)
-        keep = p_sorted.cumsum(dim=-1) - p_sorted < top_p   # the first token always survives
-        p_sorted = torch.where(keep, p_sorted, torch.zeros_like(p_sorted))
+        drop = p_sorted.cumsum(dim=-1) > top_p
+        drop[..., 0] = False
+        p_sorted = torch.where(drop, torch.zeros_like(p_sorted), p_sorted)
         p_sorted = p_sorted / p_sorted.sum(dim=-1, keepdim=True)
         return order.gather(-1, torch.multinomial(p_sorted, 1, generator=generator))
     return torch.multinomial(probs, 1, generator=generator)

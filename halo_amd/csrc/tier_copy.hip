@@ -55,10 +55,37 @@ __global__ void __launch_bounds__(kCopyThreads)
   }
 }
 
+__global__ void __launch_bounds__(kCopyThreads)
+    set_tier_kernel(int8_t* tier_of, const int32_t* blocks, int n_blocks, int64_t max_blocks, int src_tier,
+                    int dst_tier) {
+  const int i = blockIdx.x * kCopyThreads + (int)threadIdx.x;
+  if (i >= n_blocks) return;
+  const int32_t b = blocks[i];
+  if (b < 0 || (int64_t)b >= max_blocks) return;
+  // A duplicate entry may already have written dst_tier: the store is the
+  // same either way.
+  if (src_tier >= 0 && (int)tier_of[b] != src_tier && (int)tier_of[b] != dst_tier) return;
+  tier_of[b] = (int8_t)dst_tier;
+}
+
 }  // namespace
 }  // namespace halo
 
 using namespace halo;
+
+extern "C" int halo_set_tier(int8_t* tier_of, const int32_t* blocks, int n_blocks, int64_t max_blocks,
+                             int src_tier, int dst_tier, void* stream) {
+  HALO_CHECK_ARG(n_blocks >= 0, "n_blocks < 0");
+  if (n_blocks == 0) return HALO_OK;
+  HALO_CHECK_ARG(tier_of && blocks, "null pointer argument");
+  HALO_CHECK_ARG(max_blocks > 0, "max_blocks must be positive");
+  HALO_CHECK_ARG(dst_tier >= 0 && dst_tier < 128 && src_tier < 128, "tier codes must fit int8");
+  const unsigned grid = (unsigned)((n_blocks + kCopyThreads - 1) / kCopyThreads);
+  hipLaunchKernelGGL(set_tier_kernel, dim3(grid), dim3(kCopyThreads), 0, static_cast<hipStream_t>(stream), tier_of,
+                     blocks, n_blocks, max_blocks, src_tier, dst_tier);
+  HALO_CHECK_HIP(hipGetLastError());
+  return HALO_OK;
+}
 
 extern "C" int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, const void* src_v,
                                 int64_t block_bytes, const int32_t* blocks, int n_blocks, int64_t max_blocks,

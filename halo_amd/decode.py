@@ -402,7 +402,47 @@ def cached_plan(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype, chunks
 
 
 def clear_plan_cache() -> None:
+    """Drop the cache of repeated plans.  Plans launched under graph capture
+    stay alive (``captured_plans``)."""
     _plan_cache.clear()
+
+
+# Plans (and launch arguments that hold device tensors) used by a launch
+# recorded into a HIP graph.  A captured launch holds raw addresses of the
+# plan's tables, workspace and default query positions, so these objects must
+# outlive every graph that recorded them.  Neither the plan cache's LRU nor
+# clear_plan_cache() drops them; a caller that has destroyed all of its graphs
+# may call release_captured_plans().
+_captured: dict = {}
+
+
+def keep_for_capture(obj, stream=None) -> None:
+    """Keep ``obj`` alive for the process (or until
+    ``release_captured_plans``) when ``stream`` (default: the current stream)
+    is capturing a graph; otherwise do nothing."""
+    if _capturing(stream):
+        _captured.setdefault(id(obj), obj)
+
+
+def _capturing(stream=None) -> bool:
+    if torch.cuda.is_current_stream_capturing():
+        return True
+    if stream is None or stream == torch.cuda.current_stream(stream.device):
+        return False
+    with torch.cuda.stream(stream):
+        return bool(torch.cuda.is_current_stream_capturing())
+
+
+def captured_plans() -> list:
+    """The objects kept alive for captured graphs (plans and launch entries)."""
+    return list(_captured.values())
+
+
+def release_captured_plans() -> None:
+    """Forget the objects kept for captured graphs.  Call only once every
+    graph that recorded a launch of them has been destroyed: a replay after
+    this may read freed tables and workspaces."""
+    _captured.clear()
 
 
 def workspace_bytes(n_work: int, rep_t: int, D: int) -> int:
@@ -466,6 +506,7 @@ def launch(plan: DecodePlan, q: torch.Tensor, *, scale: float,
         if t is not None and t.device != q.device:
             raise AssertionError("all tensors must be on the query's device")
     sp = nat.stream_ptr(stream)
+    keep_for_capture(plan, stream)
     if noalloc:
         if plan.kivi:
             raise AssertionError("the allocation-free entry point covers plain and tiered tables, not KIVI")

@@ -361,16 +361,11 @@ class TieredStorage:
                                          blocks.numel(), self.max_blocks,
                                          dirl.data_ptr() if only_if_in_src else None, code_s,
                                          nat.stream_ptr(strm)), "halo_copy_blocks")
-            # which blocks moved: one flag per block, combined over duplicate
-            # and padding entries with a max-reduction (no write races between
-            # list entries), then one elementwise update of the layer's entries
-            valid = (blocks >= 0) & (blocks < self.max_blocks)
-            idx = blocks.clamp(0, self.max_blocks - 1).long()
-            cur = dirl.index_select(0, idx)
-            moved = valid & ((cur == code_s) if only_if_in_src else torch.ones_like(valid))
-            flip = torch.zeros(self.max_blocks, dtype=torch.uint8, device=dirl.device)
-            flip.scatter_reduce_(0, idx, moved.to(torch.uint8), reduce="amax")
-            dirl.copy_(torch.where(flip.bool(), torch.full_like(dirl, code_d), dirl))
+            # the moved blocks' entries only (a whole-row rewrite would undo a
+            # concurrent move of other blocks on another stream)
+            nat.check(L.halo_set_tier(dirl.data_ptr(), blocks.data_ptr(), blocks.numel(), self.max_blocks,
+                                      code_s if only_if_in_src else -1, code_d, nat.stream_ptr(strm)),
+                      "halo_set_tier")
         blocks.record_stream(strm)
 
     def _move_blocks_nvme(self, layer: int, blocks: torch.Tensor, s: MemoryTier, d: MemoryTier,

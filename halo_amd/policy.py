@@ -208,9 +208,10 @@ def halo_chunked_attention(module, query, key, value, attention_mask=None, dropo
 
 
 def _install_generate_hook(model) -> None:
-    """Make ``model.generate`` hand the HALO cache to every call and reset it
-    first, unless the caller passes that cache itself (an already filled
-    cache from a chunked prefill), halo/policy.py:450-478."""
+    """Make ``model.generate`` hand the HALO cache to every call that passes
+    no cache of its own, resetting the HALO cache unless the caller passes
+    that cache itself (an already filled cache from a chunked prefill); a
+    caller's own ``past_key_values`` is kept (halo/policy.py:450-478)."""
     if getattr(model, "_halo_generate_patched", False) or not hasattr(model, "generate"):
         return
     inner = model.generate
@@ -219,7 +220,8 @@ def _install_generate_hook(model) -> None:
         cache = model._halo_cache
         if kwargs.get("past_key_values") is not cache:
             cache.reset()
-            kwargs["past_key_values"] = cache
+            if kwargs.get("past_key_values") is None:
+                kwargs["past_key_values"] = cache
         kwargs.setdefault("use_cache", True)
         return inner(*args, **kwargs)
 

@@ -36,7 +36,7 @@ from typing import Optional
 import torch
 
 from . import _native as nat
-from .decode import ChunkRef, cached_plan, launch
+from .decode import ChunkRef, cached_plan, keep_for_capture, launch
 
 HAS_TRITON = nat.available()
 HAS_HIP = HAS_TRITON
@@ -169,21 +169,31 @@ _fast: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
 
 
 def clear_fast_cache() -> None:
+    """Drop the per-layout entries.  Entries replayed under graph capture
+    stay alive (``decode.captured_plans``)."""
     _fast.clear()
 
 
-def _load_layout_key():
+def _load_layout_key(path=None):
     """The prebuilt host extension (halo_amd/_lib/fastkey_build, made by
-    build()) that reads the chunk list's layout in C++, or None."""
+    build()) that reads the chunk list's layout in C++, or None when it is
+    missing or cannot be loaded."""
     import importlib.util
     import os
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "fastkey_build", "_halo_fastkey.so")
+    if path is None:
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "fastkey_build",
+                            "_halo_fastkey.so")
     if not os.path.exists(path):
         return None
-    spec = importlib.util.spec_from_file_location("_halo_fastkey", path)
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
-    return mod.chunk_layout_key
+    try:
+        spec = importlib.util.spec_from_file_location("_halo_fastkey", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        return mod.chunk_layout_key
+    except (ImportError, OSError, AttributeError):
+        # built against another torch, or not a loadable module: the key is
+        # then built in Python (same fields, slower)
+        return None
 
 
 _layout_key = _load_layout_key()
@@ -248,6 +258,7 @@ def triton_chunked_attention(
     ent = _fast.get(key)
     if ent is not None and q3.stride(-1) == 1:
         _fast.move_to_end(key)
+        keep_for_capture(ent)
         plan, qp_default, mid, dt, ws_ptr, ws_n = ent
         qp = qp_default if q_pos is None else _qpos(q_pos, B, 0, q.device).contiguous()
         if qp.numel() != B:

@@ -448,6 +448,18 @@ int halo_copy_blocks(void* dst_k, const void* src_k, void* dst_v, const void* sr
                      int64_t block_bytes, const int32_t* blocks, int n_blocks, int64_t max_blocks,
                      const int8_t* tier_of, int src_tier, void* stream);
 
+/*
+ * Directory update after a move: for each i < n_blocks with b = blocks[i] in
+ * [0, max_blocks) and (src_tier < 0 or tier_of[b] == src_tier), set
+ * tier_of[b] = dst_tier.  Only the listed entries are written (duplicates
+ * write the same value), so moves of other blocks of the same layer enqueued
+ * on other streams are never undone.  One launch on `stream`; enqueue it
+ * after the halo_copy_blocks it records.  Replaces the directory write of
+ * TieredStorage.move_block (halo/memory_tier.py:150-157).
+ */
+int halo_set_tier(int8_t* tier_of, const int32_t* blocks, int n_blocks, int64_t max_blocks, int src_tier,
+                  int dst_tier, void* stream);
+
 /* ---- HBM staging of cold chunks ---------------------------------------- */
 
 /* One host-to-device chunk copy of the staging cache: bytes from src_k to

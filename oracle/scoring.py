@@ -130,7 +130,9 @@ def select_chunks(query: np.ndarray, k_mean: np.ndarray, eligible: np.ndarray, k
 
 
 def num_hot_pages(P: int, memory_ratio: int, min_pages_selected: int) -> int:
-    """_num_hot_pages (baselines/scorer_ablations.py:133-139)."""
+    """_num_hot_pages (baselines/scorer_ablations.py:133-139), with the
+    reference's float ratio.  Pinned by hand-worked known answers
+    (tests/test_oracle.py::test_num_hot_pages_known_answers)."""
     K = max(min_pages_selected, int((P + memory_ratio - 1) // memory_ratio))
     return min(K, P)
 
@@ -139,7 +141,10 @@ def halopress_page_scores(attn: np.ndarray, *, alpha: float, beta: float, gamma:
                           refresh_window: int, sink_tokens: int, page_size: int) -> np.ndarray:
     """Full page score of HALOPressScorerAdapter.select_hot_pages
     (baselines/scorer_ablations.py:238-263), fp32: min-max normalised
-    attention + recency + sink."""
+    attention + recency + sink.  Pinned by torch's CPU ops on the
+    reference's expression, the alpha-only min-max closed form, the
+    beta-only closed form exp(-(P-1-p)/W), hand-counted sink pages and the
+    additivity of the three terms (tests/test_oracle.py)."""
     a = attn.astype(np.float32) - attn.astype(np.float32).min()
     if float(a.max()) > 0.0:
         a = (a / a.max()).astype(np.float32)

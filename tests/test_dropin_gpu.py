@@ -109,3 +109,49 @@ def test_repeated_calls_take_the_fast_path(dev):
     tc.triton_chunked_attention(q, odd)
     tc.triton_chunked_attention(q, odd)
     assert len(tc._fast) == 2
+
+
+def test_captured_plan_outlives_cache_eviction(dev):
+    """A launch recorded into a graph keeps its plan (tables, workspace,
+    default query positions) alive: after 300 calls with other layouts
+    (beyond both caches' 256 entries), clear_plan_cache(),
+    clear_fast_cache() and junk allocations that reuse freed memory, every
+    replay still equals the eager result bit for bit."""
+    from halo_amd import decode
+    from halo_amd import triton_chunked as tc
+    decode.clear_plan_cache()
+    tc.clear_fast_cache()
+    decode.release_captured_plans()
+    k, v, chunks = _chunks(dev, n=4, T=256, seed=9)
+    q = torch.randn((1, 8, 1, 128), device=dev).to(torch.bfloat16)
+    qbuf = q.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        tc.triton_chunked_attention(qbuf, chunks)             # plans and enters the fast cache
+        tc.triton_chunked_attention(qbuf, chunks)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = tc.triton_chunked_attention(qbuf, chunks)
+    torch.cuda.synchronize()
+    assert len(decode.captured_plans()) >= 1
+    for i in range(300):  # other layouts: each moved start is a new plan and a new fast entry
+        moved = [(kk, vv, c0 + 1 + i, causal) for (kk, vv, c0, causal) in chunks[:2]]
+        tc.triton_chunked_attention(q, moved)
+    decode.clear_plan_cache()
+    tc.clear_fast_cache()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    junk = [torch.full((1 << 20,), 0x7f7f, device=dev, dtype=torch.int32) for _ in range(16)]
+    for i in range(3):
+        qbuf.copy_(q * (1 + i))
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        eager = tc.triton_chunked_attention(qbuf, chunks)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+    del junk
+    decode.release_captured_plans()
+    assert decode.captured_plans() == []

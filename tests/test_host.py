@@ -217,3 +217,72 @@ def test_host_resident_chunk_must_be_pinned():
     k = torch.zeros((1, 2, 64, 128), dtype=torch.bfloat16)
     with pytest.raises(AssertionError, match="pinned"):
         pack_descs([ChunkRef(k, k.clone(), 0, True)], B=1, H_kv=2, D=128, dtype=torch.bfloat16)
+
+
+def test_plans_used_under_capture_survive_cache_clears(monkeypatch):
+    """A plan launched while a graph is being captured is kept outside the
+    plan cache: clear_plan_cache() and LRU overflow do not drop it, only
+    release_captured_plans() does."""
+    from halo_amd import decode
+    decode.release_captured_plans()
+
+    class _Plan:  # stands for a DecodePlan; only its identity matters here
+        pass
+
+    captured, other = _Plan(), _Plan()
+    monkeypatch.setattr(decode, "_capturing", lambda stream=None: True)
+    decode.keep_for_capture(captured)
+    decode.keep_for_capture(captured)          # kept once
+    monkeypatch.setattr(decode, "_capturing", lambda stream=None: False)
+    decode.keep_for_capture(other)             # not capturing: not kept
+    for i in range(decode.PLAN_CACHE_SIZE + 10):
+        decode._plan_cache[("k", i)] = _Plan()
+        while len(decode._plan_cache) > decode.PLAN_CACHE_SIZE:
+            decode._plan_cache.popitem(last=False)
+    decode.clear_plan_cache()
+    assert decode.captured_plans() == [captured]
+    decode.release_captured_plans()
+    assert decode.captured_plans() == []
+
+
+def test_nucleus_filter_follows_the_reference_rule():
+    """halo/chunked_prefill.py:150-163: sorted tokens with cumulative
+    probability > top_p are dropped, except the most likely one.  For
+    probabilities [0.5, 0.3, 0.2] and top_p 0.7 only token 0 survives; at
+    top_p 0.85 tokens 0 and 1; at top_p 0.4 still token 0; at 0.999 the
+    last token (cumulative 1.0) is still dropped."""
+    from halo_amd.chunked_prefill import _pick
+    logits = torch.log(torch.tensor([[0.2, 0.5, 0.3]]))   # token 1 most likely, then 2, then 0
+    for top_p, allowed in ((0.7, {1}), (0.4, {1}), (0.85, {1, 2}), (0.999, {1, 2})):
+        g = torch.Generator().manual_seed(0)
+        seen = {int(_pick(logits, True, 1.0, top_p, g)) for _ in range(300)}
+        assert seen == allowed, (top_p, seen)
+    assert int(_pick(logits, False, 1.0, 0.1, None)) == 1
+
+
+def test_generate_hook_keeps_a_callers_own_cache():
+    """halo/policy.py:462-475: the HALO cache is reset unless it is the
+    cache passed; it is handed in only when the caller passes none; a
+    caller's own past_key_values goes through untouched."""
+    from halo_amd.policy import _install_generate_hook
+
+    class _Cache:
+        resets = 0
+
+        def reset(self):
+            self.resets += 1
+
+    class _Model:
+        def generate(self, *args, **kwargs):
+            return kwargs
+
+    m = _Model()
+    m._halo_cache = _Cache()
+    _install_generate_hook(m)
+    kw = m.generate()
+    assert kw["past_key_values"] is m._halo_cache and kw["use_cache"] is True and m._halo_cache.resets == 1
+    kw = m.generate(past_key_values=m._halo_cache)
+    assert kw["past_key_values"] is m._halo_cache and m._halo_cache.resets == 1
+    own = object()
+    kw = m.generate(past_key_values=own, use_cache=False)
+    assert kw["past_key_values"] is own and kw["use_cache"] is False and m._halo_cache.resets == 2

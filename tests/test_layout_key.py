@@ -52,3 +52,13 @@ def test_malformed_chunk_lists_fall_back_to_the_python_key():
     k = torch.zeros(1, 8, 16, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         tc._fast_key(q, [(k, k, 0)], 0, True)    # the Python key's own error for a 3-tuple
+
+
+def test_corrupt_extension_falls_back_to_the_python_key(tmp_path):
+    """A layout-key extension that cannot be loaded (another torch's build,
+    a truncated file) leaves the drop-in importable with the Python key."""
+    from halo_amd import triton_chunked as tc
+    bad = tmp_path / "_halo_fastkey.so"
+    bad.write_bytes(b"\x7fELF not really a shared object")
+    assert tc._load_layout_key(str(bad)) is None
+    assert tc._load_layout_key(str(tmp_path / "missing.so")) is None

@@ -551,3 +551,106 @@ def test_quest_scores_match_torch_ops():
     np.testing.assert_allclose(got, expected.numpy(), atol=1e-5)
     top = torch.topk(expected.amax(dim=(0, 1, 2)), 2).indices.tolist()
     assert S.quest_select(q.numpy(), omin, omax, memory_ratio=2.0, min_pages_selected=1).tolist() == top
+
+
+# ---------------------------------------------------------------- HALOPress page score and budget
+def _halopress(attn, **kw):
+    base = dict(alpha=0.0, beta=0.0, gamma=0.0, refresh_window=8, sink_tokens=4, page_size=16)
+    base.update(kw)
+    return S.halopress_page_scores(np.asarray(attn, np.float32), **base)
+
+
+@pytest.mark.parametrize("P,W,sink,page", [(37, 64, 4, 16), (50, 16, 40, 16), (5, 1, 0, 16),
+                                           (1, 8, 4, 16), (24, 3, 100, 8)])
+def test_halopress_page_scores_match_torch_ops(P, W, sink, page):
+    """baselines/scorer_ablations.py:238-263 evaluated with torch's CPU
+    kernels (its min/max/exp/sum and fp32 scalar products), against the
+    oracle within fp32 reduction noise."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(P * 7 + W)
+    attn = rng.standard_normal(P).astype(np.float32)
+    ours = S.halopress_page_scores(attn, alpha=1.0, beta=0.5, gamma=2.0, refresh_window=W,
+                                   sink_tokens=sink, page_size=page)
+    a = torch.from_numpy(attn.copy())
+    a = a - a.min()
+    if float(a.max().item()) > 0.0:
+        a = a / a.max()
+    positions = torch.arange(P, dtype=torch.float32)
+    rec = torch.exp(-(P - 1 - positions) / max(W, 1))
+    rec = rec / (rec.sum() + 1e-12)
+    rec = rec / (rec.max() + 1e-12)
+    sk = torch.zeros(P, dtype=torch.float32)
+    sk[: min(sink // max(page, 1) + 1, P)] = 1.0
+    ref = 1.0 * a.float() + 0.5 * rec + 2.0 * sk
+    np.testing.assert_allclose(ours, ref.numpy(), rtol=2e-6, atol=1e-7)
+
+
+def test_halopress_alpha_only_is_min_max_normalised():
+    """Closed form: with beta = gamma = 0 the score is (a - min) / (max - min):
+    exactly 0 at the minimum, exactly 1 at the maximum, and a constant
+    attention vector scores 0 everywhere (no division)."""
+    rng = np.random.default_rng(3)
+    attn = (rng.standard_normal(40) * 5 + 2).astype(np.float32)
+    s = _halopress(attn, alpha=1.0)
+    assert s[int(np.argmin(attn))] == 0.0 and s[int(np.argmax(attn))] == 1.0
+    a64 = attn.astype(np.float64)
+    np.testing.assert_allclose(s, (a64 - a64.min()) / (a64.max() - a64.min()), rtol=0, atol=4e-7)
+    assert np.array_equal(np.argsort(s, kind="stable"), np.argsort(attn, kind="stable"))
+    assert np.array_equal(_halopress(np.full(9, 3.5, np.float32), alpha=1.0), np.zeros(9, np.float32))
+    # alpha scales the normalised term only
+    np.testing.assert_allclose(_halopress(attn, alpha=0.25), 0.25 * s, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("P,W", [(1, 8), (2, 1), (32, 8), (64, 64), (100, 5)])
+def test_halopress_beta_only_recency_closed_form(P, W):
+    """Closed form: after normalising by the sum and then by the maximum,
+    the recency term is exp(-(P - 1 - p) / W): 1 on the newest page (the
+    highest index) and non-decreasing in p.  A reversed direction, a single
+    normalisation or a dropped window fails one of the checks."""
+    s = _halopress(np.zeros(P, np.float32), beta=1.0, refresh_window=W)
+    want = np.exp(-(P - 1 - np.arange(P, dtype=np.float64)) / W)
+    np.testing.assert_allclose(s, want, rtol=4e-6, atol=0)
+    assert abs(float(s[-1]) - 1.0) <= 2.0 ** -22
+    assert (np.diff(s) >= 0).all()
+    if P >= 2:
+        assert s[0] < s[-1]
+
+
+def test_halopress_gamma_only_sink_pages_known_answers():
+    """sink_tokens // page_size + 1 pages (capped at P) score gamma, the
+    rest 0 (baselines/scorer_ablations.py:253-257).  Counts worked by hand."""
+    cases = [  # (P, sink_tokens, page_size) -> number of sink pages
+        ((10, 4, 16), 1), ((10, 0, 16), 1), ((10, 15, 16), 1), ((10, 16, 16), 2),
+        ((10, 47, 16), 3), ((3, 100, 16), 3), ((6, 5, 1), 6), ((12, 5, 2), 3), ((1, 0, 16), 1),
+    ]
+    for (P, sink, page), n in cases:
+        s = _halopress(np.zeros(P, np.float32), gamma=2.0, sink_tokens=sink, page_size=page)
+        assert s.tolist() == [2.0] * n + [0.0] * (P - n), (P, sink, page)
+
+
+def test_halopress_terms_add():
+    """The three terms add: the full score equals the sum of the one-term
+    scores (each term is computed independently of the weights)."""
+    rng = np.random.default_rng(5)
+    attn = rng.standard_normal(30).astype(np.float32)
+    kw = dict(refresh_window=7, sink_tokens=20, page_size=8)
+    full = _halopress(attn, alpha=1.0, beta=0.5, gamma=2.0, **kw)
+    parts = (_halopress(attn, alpha=1.0, **kw).astype(np.float64) + _halopress(attn, beta=0.5, **kw)
+             + _halopress(attn, gamma=2.0, **kw))
+    np.testing.assert_allclose(full, parts, rtol=0, atol=4e-7)
+
+
+def test_num_hot_pages_known_answers():
+    """_num_hot_pages (baselines/scorer_ablations.py:133-139): max(min,
+    int((P + r - 1) // r)) capped at P, with the reference's float ratio
+    (default 4.0).  Values worked by hand."""
+    assert S.num_hot_pages(37, 4, 4) == 10      # ceil(37 / 4)
+    assert S.num_hot_pages(37, 4.0, 4) == 10
+    assert S.num_hot_pages(3, 4, 4) == 3        # floor 4, capped at P = 3
+    assert S.num_hot_pages(10, 4.0, 4) == 4     # ceil 3 < floor 4
+    assert S.num_hot_pages(100, 4.0, 4) == 25
+    assert S.num_hot_pages(101, 4.0, 4) == 26
+    assert S.num_hot_pages(10, 2.5, 1) == 4     # (11.5 // 2.5) = 4
+    assert S.num_hot_pages(3, 2.5, 1) == 1      # (4.5 // 2.5) = 1, not ceil(1.2) = 2
+    assert S.num_hot_pages(1, 4.0, 4) == 1
+    assert S.num_hot_pages(0, 4.0, 4) == 0

@@ -182,3 +182,68 @@ def test_write_allocate_commits_the_rows_read_in_place(dev, write_allocate):
             c = int(st.holds[li, s])
             assert torch.equal(st._slot_k[li][s].cpu(), lay.cold[c].k), (li, s, c)
             assert torch.equal(st._slot_v[li][s].cpu(), lay.cold[c].v), (li, s, c)
+
+
+def test_benchmark_loop_matches_all_hbm_every_step(dev):
+    """The timed loop of the benchmark (``bench.refetch_run``: segment
+    graphs, commits before each segment, feedback one segment late, fills
+    and evictions planned while the next segments run, no synchronisation
+    between steps), at a small scale with evictions (rho 0.8, 6 slots for
+    12 cold chunks): every step's output, LSE and picks, copied out in stream
+    order, equal those of the all-HBM layers bit for bit; fills, commits and
+    releases were issued while launches were still queued."""
+    import bench
+    hbm, staged, st, (H, D) = _setup(dev, L=8, n_chunks=16, chunk=1024, n_hot=4, top_k=3, slots=6, keep=4,
+                                     seed=11)
+    st.max_inflight = 6
+    L, steps, k = len(hbm), 24, 3
+    scale = 1 / math.sqrt(D)
+    qtraj = bench.query_trajectory(torch, dev, steps=steps, L=L, H=H, D=D, rho=0.8, seed=12)
+    out_hist = torch.zeros((steps, L, 1, H, D), device=dev, dtype=torch.bfloat16)
+    lse_hist = torch.zeros((steps, L, 1, H), device=dev)
+    idx_hist = torch.full((steps, L, k), -7, device=dev, dtype=torch.int32)
+    res_hist = torch.full((steps, L, k), -7, device=dev, dtype=torch.int32)
+    lses = [torch.zeros((1, H), device=dev) for _ in range(L)]
+
+    def record(t, lo, hi, outs):
+        for li in range(lo, hi):
+            out_hist[t, li].copy_(outs[li])
+            lse_hist[t, li].copy_(lses[li])
+        idx_hist[t, lo:hi].copy_(st.idx[lo:hi])
+        res_hist[t, lo:hi].copy_(st.res_out[lo:hi])
+
+    # what the cache issues, and whether the replay stream still had work queued then
+    log = []
+    issue, store = st._issue, st._store
+
+    def busy():
+        return not torch.cuda.current_stream(dev).query()
+
+    def _issue(fills):
+        log.append(("fill", busy(), len(fills)))
+        return issue(fills)
+
+    def _store(idx, val):
+        kinds = {"release" if v == -1 else "commit" for v in val}
+        for kind in kinds:
+            log.append((kind, busy(), len(val)))
+        return store(idx, val)
+
+    st._issue, st._store = _issue, _store
+    bench.refetch_run(torch, staged, st, qtraj, warmup=0, steps=steps, scale=scale, label="test", segments=2,
+                      record=record, lses=lses)
+    torch.cuda.synchronize()
+    st._issue, st._store = issue, store
+    for kind in ("fill", "commit", "release"):
+        assert any(kd == kind and b for kd, b, _ in log), (kind, [e for e in log if e[0] == kind][:5])
+    assert st.hits > 0 and st.misses > 0
+    res = res_hist.cpu().numpy()
+    assert (res >= 0).any() and ((res == -1).any())   # both slots and host reads served picks
+    o_ref = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+    l_ref = torch.empty((1, H), device=dev)
+    for t in range(steps):
+        for li in range(L):
+            hbm[li].step(qtraj[t % steps, li], scale=scale, out=o_ref, lse=l_ref)
+            assert torch.equal(out_hist[t, li], o_ref), (t, li)
+            assert torch.equal(lse_hist[t, li], l_ref), (t, li)
+            assert torch.equal(idx_hist[t, li], hbm[li].idx[0].to(torch.int32)), (t, li)

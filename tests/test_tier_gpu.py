@@ -66,6 +66,34 @@ def test_batched_moves_round_trip(dev):
     assert st.locate_block(layer=0, block=3) == "gpu"  # other layers untouched
 
 
+def test_concurrent_moves_on_two_streams_keep_both_directory_updates(dev):
+    """Two streams move different blocks of one layer (demotion of some, a
+    refetch of others) with no ordering between them: only the listed
+    directory entries are written, so neither move undoes the other's."""
+    st = _storage(dev)
+    _fill(st, 0, range(0, 32), "gpu", 2)
+    _fill(st, 0, range(32, 64), "dram", 3)
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    a.wait_stream(torch.cuda.current_stream())
+    b.wait_stream(torch.cuda.current_stream())
+    down = torch.arange(0, 32, 2, dtype=torch.int32, device=dev)      # even GPU blocks -> DRAM
+    up = torch.arange(33, 64, 2, dtype=torch.int32, device=dev)       # odd DRAM blocks -> GPU
+    for _ in range(3):  # and back, several rounds, the two streams racing each other
+        st.move_blocks(layer=0, blocks=down, src="gpu", dst="dram", stream=a)
+        st.move_blocks(layer=0, blocks=up, src="dram", dst="gpu", stream=b)
+        st.move_blocks(layer=0, blocks=down, src="dram", dst="gpu", stream=a)
+        st.move_blocks(layer=0, blocks=up, src="gpu", dst="dram", stream=b)
+    st.move_blocks(layer=0, blocks=down, src="gpu", dst="dram", stream=a)
+    st.move_blocks(layer=0, blocks=up, src="dram", dst="gpu", stream=b)
+    torch.cuda.synchronize()
+    for blk in range(64):
+        if blk < 32:
+            want = "dram" if blk % 2 == 0 else "gpu"
+        else:
+            want = "gpu" if blk % 2 == 1 else "dram"
+        assert st.locate_block(layer=0, block=blk) == want, blk
+
+
 def test_refetcher_reference_expectations(dev, small_config):
     """Blocks 0 (GPU) and 1 (DRAM): positions [0, 1, 4, 5] give one hit and
     one miss, and block 1 is on the GPU afterwards (reference

@@ -99,3 +99,51 @@ def test_noalloc_refuses_plans_beyond_the_scratch(dev):
     rc = f(*args, None, nat.stream_ptr())
     assert rc == nat.HALO_E_WORKSPACE
     assert b"static scratch" in nat.lib().halo_last_error()
+
+
+def _first_call_in_capture() -> None:
+    """Run in a fresh process: the first halo_decode_attn_noalloc call of the
+    process -- the one that looks up the scratch address -- is made while a
+    HIP graph is being captured; three replays (with eager work and a new
+    query between them) equal the workspace entry point bit for bit."""
+    from halo_amd import _native as nat
+    dev = torch.device("cuda:0")
+    f, _ = _fn()
+    lay, q0 = _layer(dev, 8, 1024, 4)
+    scale = 1 / math.sqrt(128)
+    q = q0.clone()
+    out = torch.full((1, 32, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    lse = torch.full((1, 32), float("nan"), device=dev, dtype=torch.float32)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        rc = f(*_args(lay.plan, q, scale, out, lse), ctypes.byref(lay.select_cfg), nat.stream_ptr(s))
+    nat.check(rc, "halo_decode_attn_noalloc (first call, under capture)")
+    out_ref = torch.empty_like(out)
+    lse_ref = torch.empty_like(lse)
+    for i in range(3):
+        q.copy_(q0 * (1 + 0.5 * i))
+        lay.step(q, scale=scale, out=out_ref, lse=lse_ref)      # workspace entry point, eager
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_ref) and torch.equal(lse, lse_ref), i
+    print("first-call-in-capture: 3 replays equal", flush=True)
+
+
+def test_noalloc_first_call_inside_graph_capture(dev):
+    """The documented use: a caller whose very first allocation-free call is
+    recorded into a graph (a fresh process, so the scratch address has not
+    been looked up yet)."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = ("import sys; sys.path[:0] = [%r, %r]; import test_zz_no_alloc as t; t._first_call_in_capture()"
+            % (here, os.path.dirname(here)))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=150)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "3 replays equal" in r.stdout

@@ -140,17 +140,19 @@ def cpu_baseline(torch, kvs, qs, layers, *, chunk, n_hot, top_k, L, budget_s):
 
 def host_tier(torch, layers):
     """The cold chunks of every layer as contiguous pinned host tensors (the
-    cold tier), copied from their HBM originals."""
+    cold tier), copied from their HBM originals: one pinned buffer per layer
+    holding each chunk's K rows followed by its V rows, so the staging cache
+    fills a chunk with one copy."""
     from halo_amd.decode import ChunkRef
     tiers = []
     for lay in layers:
+        shape = tuple(lay.cold[0].k.shape)
+        buf = torch.empty((len(lay.cold), 2) + shape, dtype=lay.cold[0].k.dtype, pin_memory=True)
         cold = []
-        for c in lay.cold:
-            hk = torch.empty(tuple(c.k.shape), dtype=c.k.dtype, pin_memory=True)
-            hv = torch.empty(tuple(c.v.shape), dtype=c.v.dtype, pin_memory=True)
-            hk.copy_(c.k)
-            hv.copy_(c.v)
-            cold.append(ChunkRef(hk, hv, c.chunk_start, c.causal))
+        for j, c in enumerate(lay.cold):
+            buf[j, 0].copy_(c.k)
+            buf[j, 1].copy_(c.v)
+            cold.append(ChunkRef(buf[j, 0], buf[j, 1], c.chunk_start, c.causal))
         tiers.append(cold)
     return tiers
 
@@ -473,6 +475,8 @@ def main() -> int:
     ap.add_argument("--write-allocate", action="store_true",
                     help="headline cache with write-allocate (a missed chunk read in place also fills a slot)")
     ap.add_argument("--segments", type=int, default=4, help="graphs per step (layer segments) of the headline")
+    ap.add_argument("--fill-mode", choices=["kernel", "dma"], default="dma",
+                    help="staging fills as copy kernels reading pinned memory in place, or hipMemcpyAsync")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the drift / no-staging comparison legs")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -529,7 +533,7 @@ def main() -> int:
                                 top_k=top_k, device=dev, cold_kmean=lay.kmean, split=args.split)
               for li, lay in enumerate(layers)]
     staging = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
-                          write_allocate=args.write_allocate)
+                          write_allocate=args.write_allocate, fill_mode=args.fill_mode)
     n_traj = args.warmup + args.steps
     qtraj = query_trajectory(torch, dev, steps=n_traj, L=L, H=H, D=D, rho=args.rho, seed=11)
     head = refetch_run(torch, staged, staging, qtraj, warmup=args.warmup, steps=args.steps, scale=scale,
@@ -603,7 +607,8 @@ def main() -> int:
             "chunk": chunk, "hot_chunks": n_hot, "cold_chunks": n_cold, "top_k": top_k,
             "query_drift_rho": args.rho, "staging_slots_per_layer": args.slots, "staging_keep": staging.keep,
             "staging_bytes": staging.slot_bytes, "max_fills_in_flight": args.max_inflight,
-            "write_allocate": staging.write_allocate, "segments": args.segments,
+            "write_allocate": staging.write_allocate, "segments": args.segments, "fill_mode": args.fill_mode,
+            "hbm_resident_fraction": (n_hot + args.slots) / (n_hot + n_cold),
             "launch": "per step: query copy, fill commits, hip graph of 32 x (attention kernel with in-kernel "
                       "top-k selection + merge kernel), score read-back, staging policy",
         },
@@ -629,20 +634,32 @@ def main() -> int:
     if not args.no_sweep:
         sweep = {}
         for rho in (0.95, 0.99):
-            staging.clear()
+            staging.clear()   # the headline's cache and fill mode
             qt = query_trajectory(torch, dev, steps=20 + 100, L=L, H=H, D=D, rho=rho, seed=12)
             sweep[f"rho_{rho}"] = refetch_run(torch, staged, staging, qt, warmup=20, steps=100, scale=scale,
                                               label=f"staged, rho {rho}", warm_fills=10 ** 6,
                                               segments=args.segments)
-        # a larger cache (16 slots per layer) on the headline trajectory
-        big = ColdStaging(staged, n_slots=16, keep=args.keep, max_inflight=args.max_inflight)
-        sweep["slots_16"] = refetch_run(torch, staged, big, qtraj, warmup=args.warmup, steps=100, scale=scale,
-                                        label=f"staged, 16 slots, rho {args.rho}", warm_fills=10 ** 6,
-                                        segments=args.segments)
-        del big
+        # smaller and larger caches (4, 6 and 16 slots per layer) on the headline trajectory
+        for n_sl in (4, 6, 16):
+            other = ColdStaging(staged, n_slots=n_sl, keep=min(args.keep, n_sl), max_inflight=args.max_inflight,
+                                fill_mode=args.fill_mode)
+            rd = refetch_run(torch, staged, other, qtraj, warmup=args.warmup, steps=100, scale=scale,
+                             label=f"staged, {n_sl} slots, rho {args.rho}", warm_fills=10 ** 6,
+                             segments=args.segments)
+            rd["hbm_resident_fraction"] = (n_hot + n_sl) / (n_hot + n_cold)
+            sweep[f"slots_{n_sl}"] = rd
+            del other
+        # the headline cache with the other fill mechanism
+        other_mode = "dma" if args.fill_mode == "kernel" else "kernel"
+        other = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
+                            write_allocate=args.write_allocate, fill_mode=other_mode)
+        sweep[f"{other_mode}_fills"] = refetch_run(torch, staged, other, qtraj, warmup=args.warmup, steps=100,
+                                                   scale=scale, label=f"staged, {other_mode} fills, rho {args.rho}",
+                                                   warm_fills=10 ** 6, segments=args.segments)
+        del other
         # the headline cache toggled between write-allocate on and off
         other = ColdStaging(staged, n_slots=args.slots, keep=args.keep, max_inflight=args.max_inflight,
-                            write_allocate=not args.write_allocate)
+                            write_allocate=not args.write_allocate, fill_mode=args.fill_mode)
         key = "no_write_allocate" if args.write_allocate else "write_allocate"
         sweep[key] = refetch_run(torch, staged, other, qtraj, warmup=args.warmup, steps=100, scale=scale,
                                  label=f"staged, {key.replace('_', ' ')}, rho {args.rho}", warm_fills=10 ** 6,

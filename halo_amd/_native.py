@@ -62,6 +62,24 @@ class Fill(ctypes.Structure):
                 ("bytes", _i64)]
 
 
+class StagingDesc(ctypes.Structure):
+    """halo_staging_desc (include/halo_hip.h)."""
+    _fields_ = [
+        ("n_layers", _i32), ("n_cold", _i32), ("n_slots", _i32), ("top_k", _i32), ("keep", _i32),
+        ("max_inflight", _i32), ("spare", _i32), ("ring", _i32),
+        ("write_allocate", _i32), ("fill_mode", _i32), ("track_busy", _i32), ("pad", _i32),
+        ("residency", _c_void_p), ("feedback", _c_void_p), ("slot_addr", _c_void_p), ("chunk_addr", _c_void_p),
+        ("chunk_nbytes", _c_void_p), ("copy_stream", _c_void_p), ("urgent_stream", _c_void_p),
+    ]
+
+
+class StagingStats(ctypes.Structure):
+    """halo_staging_stats (include/halo_hip.h)."""
+    _fields_ = [(name, _i64) for name in (
+        "hits", "misses", "misses_predicted", "fills", "fill_bytes", "miss_bytes", "wa_commits", "wa_dups",
+        "fills_while_busy", "commits_while_busy", "evictions_while_busy")]
+
+
 _DECODE_ARGS = [
     _c_void_p, _i64, _i64, _i32,             # q, q_stride_b, q_stride_h, dtype
     _i32, _i32, _i32, _i32, _i32,            # B, H, H_kv, D, rep_t
@@ -121,7 +139,16 @@ _SIGNATURES = {
                                 _c_void_p, _i32, _c_void_p]),
     "halo_set_tier": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i32, _i32, _c_void_p]),
     "halo_stage_fills": (_i32, [ctypes.POINTER(Fill), _i32, _c_void_p]),
+    "halo_stage_fills_read": (_i32, [ctypes.POINTER(Fill), _i32, _c_void_p]),
     "halo_store_i32": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
+    "halo_staging_create": (_i32, [ctypes.POINTER(StagingDesc), ctypes.POINTER(_c_void_p)]),
+    "halo_staging_destroy": (_i32, [_c_void_p]),
+    "halo_staging_before": (_i32, [_c_void_p, _i32, _i32, _c_void_p]),
+    "halo_staging_after": (_i32, [_c_void_p, _i32, _i32, _c_void_p]),
+    "halo_staging_service": (_i32, [_c_void_p, _i32, _c_void_p]),
+    "halo_staging_reset": (_i32, [_c_void_p]),
+    "halo_staging_set": (_i32, [_c_void_p, _i32, _i32]),
+    "halo_staging_get": (_i32, [_c_void_p, ctypes.POINTER(StagingStats), _c_void_p, _c_void_p, _c_void_p]),
     "halo_host_device_pointer": (_i32, [_c_void_p, ctypes.POINTER(_c_void_p)]),
     "halo_last_error": (ctypes.c_char_p, []),
     "halo_build_info": (ctypes.c_char_p, []),

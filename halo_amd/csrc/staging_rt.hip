@@ -1,0 +1,503 @@
+// Host runtime of the HBM staging cache for cold chunks kept in pinned host
+// memory: feedback ring, hit/miss accounting, the fill/evict policy, fill
+// issue and residency commits, one C call per segment of layers.
+//
+// The kernels that consume it are the fused selection of
+// halo_decode_attn_tiered (residency entries, slot catalog, feedback row);
+// this file only enqueues work on HIP streams (hipMemcpyAsync, events, the
+// int32 store kernel) and keeps the host mirror of the cache.
+//
+// Reference policy: HALORefetcher.predict_hot / schedule / _issue / wait
+// (halo/refetcher.py:38-114): the next hot set is the top (hot + lookahead)
+// by the last score, and what is missing is fetched on a side stream.  Here
+// the scores are the ones the selection itself wrote, the predicted set is
+// the `keep` best per layer, and the fetch is a chunk copy into an HBM slot.
+//
+// Ordering (no kernel observes a change while it runs):
+//  * a fill copies a chunk into a slot that no residency entry names, on a
+//    copy stream, followed by an event;
+//  * a fill is committed (its residency entry stored on the compute stream)
+//    before the next launches of its layer once its event has completed --
+//    or at once after a compute-stream wait for the event when it is urgent
+//    (the chunk was among the layer's current top-k, so the next launch
+//    would otherwise read it over the link);
+//  * evictions are decided only for layers whose feedback rows came back:
+//    every launch of such a layer has finished (the feedback copy ran
+//    behind it) and its next launch is not enqueued yet, so the -1 store on
+//    the compute stream precedes every later read and the slot can take a
+//    fill at once.
+#include <algorithm>
+#include <numeric>
+#include <vector>
+
+#include "common.hpp"
+
+namespace halo {
+namespace {
+
+enum : int8_t { kFree = 0, kFilling = 1, kReady = 2, kReserved = 4 };
+
+struct Pending {
+  int layer, chunk, slot;
+  bool urgent;
+};
+
+}  // namespace
+}  // namespace halo
+
+struct halo_staging {
+  int L = 0, n = 0, S = 0, k = 0, keep = 0, max_inflight = 0, spare = 0, ring_n = 0, W = 0;
+  bool wa = false, kernel_fills = false, track_busy = false;
+  int32_t* dev_i32 = nullptr;  // residency (L * n) then the write-allocate slot per layer (L)
+  const float* feedback = nullptr;
+  hipStream_t copy = nullptr, urgent = nullptr;
+  std::vector<uint64_t> dst, src;       // (L, S, 2) slot K/V, (L, n, 2) chunk K/V addresses
+  std::vector<int64_t> nbytes;          // (L, n) bytes per K (or V) tensor
+  std::vector<float*> ring;             // pinned (L, W) rows per ring entry
+  std::vector<hipEvent_t> ring_ev;
+  std::vector<std::pair<int, int>> ring_rows;
+  int64_t queued = 0, seen = 0;
+  std::vector<int64_t> slot_of, holds, last_rank, wa_slot, launches, processed;
+  std::vector<int8_t> state;
+  std::vector<hipEvent_t> fill_ev;      // (L, S): the event of the slot's fill in flight
+  std::vector<halo::Pending> pending;
+  halo_staging_stats st{};
+  // scratch reused across calls
+  std::vector<int64_t> idx_buf;
+  std::vector<int32_t> val_buf;
+
+  int64_t& slot_of_at(int li, int c) { return slot_of[(size_t)li * n + c]; }
+  int8_t& state_at(int li, int s) { return state[(size_t)li * S + s]; }
+  int64_t& holds_at(int li, int s) { return holds[(size_t)li * S + s]; }
+  int64_t chunk_bytes(int li, int c) const { return 2 * nbytes[(size_t)li * n + c]; }
+};
+
+namespace halo {
+namespace {
+
+bool stream_busy(hipStream_t s) {
+  const hipError_t e = hipStreamQuery(s);
+  if (e == hipErrorNotReady) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return false;
+}
+
+int store(halo_staging* h, hipStream_t compute) {
+  if (h->idx_buf.empty()) return HALO_OK;
+  const int rc = halo_store_i32(h->dev_i32, (int64_t)h->L * h->n + h->L, h->idx_buf.data(), h->val_buf.data(),
+                                (int)h->idx_buf.size(), compute);
+  h->idx_buf.clear();
+  h->val_buf.clear();
+  return rc;
+}
+
+// Give every empty write-allocate reservation a free slot (highest index
+// first, away from the fills, which take the lowest).
+void reserve_wa(halo_staging* h) {
+  if (!h->wa) return;
+  for (int li = 0; li < h->L; ++li) {
+    for (int q = 0; q < 2; ++q) {
+      if (h->wa_slot[(size_t)li * 2 + q] >= 0) continue;
+      for (int s = h->S - 1; s >= 0; --s) {
+        if (h->state_at(li, s) == kFree) {
+          h->state_at(li, s) = kReserved;
+          h->wa_slot[(size_t)li * 2 + q] = s;
+          break;
+        }
+      }
+    }
+  }
+}
+
+// Hit/miss accounting of the feedback rows of layers [lo, hi) and the
+// commits of slots the kernel wrote (write-allocate).
+int account(halo_staging* h, const float* fb, int lo, int hi, hipStream_t compute) {
+  const int n = h->n, k = h->k;
+  for (int li = lo; li < hi; ++li) h->processed[li] += 1;
+  bool committed = false;
+  for (int li = lo; li < hi; ++li) {
+    const float* row = fb + (size_t)(li - lo) * h->W;
+    const int32_t* idx = reinterpret_cast<const int32_t*>(row + n);
+    const int32_t* res = reinterpret_cast<const int32_t*>(row + n + k);
+    for (int j = 0; j < k; ++j) {
+      const int c = idx[j];
+      if (c < 0 || c >= n) continue;
+      const int r = res[j];
+      if (r >= 0) {
+        h->st.hits += 1;
+        continue;
+      }
+      h->st.misses += 1;
+      h->st.miss_bytes += h->chunk_bytes(li, c);
+      if (h->last_rank[(size_t)li * n + c] < h->keep) h->st.misses_predicted += 1;
+      if (h->wa && r <= -2) {
+        const int w = -2 - r;
+        int q = -1;
+        for (int t = 0; t < 2; ++t)
+          if (h->wa_slot[(size_t)li * 2 + t] == w) q = t;
+        if (q < 0) continue;  // not a current reservation: nothing to commit
+        if (h->slot_of_at(li, c) >= 0) {
+          h->st.wa_dups += 1;  // staged or filling elsewhere meanwhile: keep the reservation
+          continue;
+        }
+        h->state_at(li, w) = kReady;
+        h->holds_at(li, w) = c;
+        h->slot_of_at(li, c) = w;
+        h->idx_buf.push_back((int64_t)li * n + c);
+        h->val_buf.push_back(w);
+        h->wa_slot[(size_t)li * 2 + q] = -1;
+        h->st.wa_commits += 1;
+        committed = true;
+      }
+    }
+  }
+  if (committed) {
+    if (h->track_busy && stream_busy(compute)) h->st.commits_while_busy += 1;
+    const int rc = store(h, compute);
+    if (rc != HALO_OK) return rc;
+    reserve_wa(h);
+  }
+  return HALO_OK;
+}
+
+int issue(halo_staging* h, const Pending& p) {
+  hipStream_t s = (p.urgent && h->urgent != nullptr) ? h->urgent : h->copy;
+  const size_t sk = ((size_t)p.layer * h->S + p.slot) * 2, ck = ((size_t)p.layer * h->n + p.chunk) * 2;
+  const int64_t nb = h->nbytes[(size_t)p.layer * h->n + p.chunk];
+  halo_fill f;
+  f.dst_k = reinterpret_cast<void*>(h->dst[sk]);
+  f.dst_v = reinterpret_cast<void*>(h->dst[sk + 1]);
+  f.src_k = reinterpret_cast<const void*>(h->src[ck]);
+  f.src_v = reinterpret_cast<const void*>(h->src[ck + 1]);
+  f.bytes = nb;
+  if (h->src[ck + 1] == h->src[ck] + (uint64_t)nb && h->dst[sk + 1] == h->dst[sk] + (uint64_t)nb) {
+    f.bytes = 2 * nb;  // K rows then V rows on both sides: one copy
+    f.dst_v = nullptr;
+    f.src_v = nullptr;
+  }
+  const int rc = h->kernel_fills ? halo_stage_fills_read(&f, 1, s) : halo_stage_fills(&f, 1, s);
+  if (rc != HALO_OK) return rc;
+  HALO_CHECK_HIP(hipEventRecord(h->fill_ev[(size_t)p.layer * h->S + p.slot], s));
+  h->pending.push_back(p);
+  return HALO_OK;
+}
+
+// Plan evictions and fills for the layers whose feedback was just processed
+// (scores rows in `sc`, one per layer of `layers`).
+int plan(halo_staging* h, const std::vector<int>& layers, const std::vector<float>& sc, hipStream_t compute) {
+  const int n = h->n, S = h->S;
+  std::vector<int> order(n);
+  std::vector<int64_t> rank((size_t)layers.size() * n);
+  struct Miss {
+    int64_t rank;
+    int layer, chunk, row;
+  };
+  std::vector<Miss> missing;
+  for (size_t i = 0; i < layers.size(); ++i) {
+    const float* s = sc.data() + i * n;
+    auto key = [&](int c) { return std::isnan(s[c]) ? -INFINITY : s[c]; };
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) > key(b); });
+    int64_t* rk = rank.data() + i * n;
+    for (int r = 0; r < n; ++r) rk[order[r]] = r;
+    const int li = layers[i];
+    std::copy(rk, rk + n, h->last_rank.begin() + (size_t)li * n);
+    for (int c = 0; c < n; ++c)
+      if (rk[c] < h->keep && h->slot_of_at(li, c) < 0) missing.push_back({rk[c], li, c, (int)i});
+  }
+  bool evicted = false;
+  auto evict = [&](int li, int s) {
+    const int64_t c = h->holds_at(li, s);
+    h->idx_buf.push_back((int64_t)li * n + c);
+    h->val_buf.push_back(-1);
+    h->slot_of_at(li, (int)c) = -1;
+    h->state_at(li, s) = kFree;
+    h->holds_at(li, s) = -1;
+    evicted = true;
+  };
+  // keep `spare` slots per layer free, evicting the worst-ranked staged
+  // chunks outside the kept set
+  if (h->spare > 0) {
+    for (size_t i = 0; i < layers.size(); ++i) {
+      const int li = layers[i];
+      const int64_t* rk = rank.data() + i * n;
+      int free_n = 0;
+      std::vector<int> ready;
+      for (int s = 0; s < S; ++s) {
+        if (h->state_at(li, s) == kFree) ++free_n;
+        if (h->state_at(li, s) == kReady) ready.push_back(s);
+      }
+      int short_n = h->spare - free_n;
+      std::stable_sort(ready.begin(), ready.end(),
+                       [&](int a, int b) { return rk[h->holds_at(li, a)] > rk[h->holds_at(li, b)]; });
+      for (size_t j = 0; j < ready.size() && short_n > 0; ++j, --short_n) {
+        if (rk[h->holds_at(li, ready[j])] < h->keep) break;
+        evict(li, ready[j]);
+      }
+    }
+  }
+  // best ranks first, then layer order
+  std::stable_sort(missing.begin(), missing.end(), [](const Miss& a, const Miss& b) {
+    return a.rank != b.rank ? a.rank < b.rank : a.layer < b.layer;
+  });
+  int budget = h->max_inflight - (int)h->pending.size();
+  std::vector<Pending> fills;
+  for (const Miss& m : missing) {
+    if (budget <= 0) break;
+    const int li = m.layer;
+    const int64_t* rk = rank.data() + (size_t)m.row * n;
+    int slot = -1;
+    for (int s = 0; s < S && slot < 0; ++s)
+      if (h->state_at(li, s) == kFree) slot = s;
+    if (slot < 0) {
+      // no free slot: take the one of the worst-ranked staged chunk outside
+      // the kept set, if there is one
+      int worst = -1;
+      for (int s = 0; s < S; ++s)
+        if (h->state_at(li, s) == kReady && (worst < 0 || rk[h->holds_at(li, s)] > rk[h->holds_at(li, worst)]))
+          worst = s;
+      if (worst < 0 || rk[h->holds_at(li, worst)] < h->keep) continue;
+      evict(li, worst);
+      slot = worst;
+    }
+    h->state_at(li, slot) = kFilling;
+    h->holds_at(li, slot) = m.chunk;
+    h->slot_of_at(li, m.chunk) = slot;
+    h->st.fills += 1;
+    h->st.fill_bytes += h->chunk_bytes(li, m.chunk);
+    fills.push_back({li, m.chunk, slot, m.rank < h->k});
+    --budget;
+  }
+  if (evicted) {
+    if (h->track_busy && stream_busy(compute)) h->st.evictions_while_busy += 1;
+    const int rc = store(h, compute);
+    if (rc != HALO_OK) return rc;
+    reserve_wa(h);
+  }
+  if (!fills.empty() && h->track_busy && stream_busy(compute)) h->st.fills_while_busy += 1;
+  for (const Pending& p : fills) {
+    const int rc = issue(h, p);
+    if (rc != HALO_OK) return rc;
+  }
+  return HALO_OK;
+}
+
+}  // namespace
+}  // namespace halo
+
+using namespace halo;
+
+extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** out) {
+  HALO_CHECK_ARG(d != nullptr && out != nullptr, "null pointer argument");
+  *out = nullptr;
+  HALO_CHECK_ARG(d->n_layers > 0 && d->n_cold > 0 && d->top_k > 0, "empty staging cache");
+  HALO_CHECK_ARG(d->n_slots >= 1 && d->n_slots <= 64, "n_slots must be in [1, 64]");
+  HALO_CHECK_ARG(d->top_k <= d->keep && d->keep <= d->n_slots, "keep must be in [top_k, n_slots]");
+  HALO_CHECK_ARG(d->ring >= 2 && d->max_inflight >= 0 && d->spare >= 0, "bad ring / max_inflight / spare");
+  HALO_CHECK_ARG(d->residency && d->feedback && d->slot_addr && d->chunk_addr && d->chunk_nbytes && d->copy_stream,
+                 "null pointer in the staging description");
+  auto h = new halo_staging();
+  h->L = d->n_layers;
+  h->n = d->n_cold;
+  h->S = d->n_slots;
+  h->k = d->top_k;
+  h->keep = d->keep;
+  h->max_inflight = d->max_inflight;
+  h->spare = d->spare;
+  h->ring_n = d->ring;
+  h->W = d->n_cold + 2 * d->top_k;
+  h->wa = d->write_allocate != 0;
+  h->kernel_fills = d->fill_mode == 1;
+  h->track_busy = d->track_busy != 0;
+  h->dev_i32 = d->residency;
+  h->feedback = d->feedback;
+  h->copy = static_cast<hipStream_t>(d->copy_stream);
+  h->urgent = static_cast<hipStream_t>(d->urgent_stream);
+  const size_t L = h->L, n = h->n, S = h->S;
+  h->dst.assign(d->slot_addr, d->slot_addr + L * S * 2);
+  h->src.assign(d->chunk_addr, d->chunk_addr + L * n * 2);
+  h->nbytes.assign(d->chunk_nbytes, d->chunk_nbytes + L * n);
+  h->slot_of.assign(L * n, -1);
+  h->last_rank.assign(L * n, (int64_t)n);
+  h->holds.assign(L * S, -1);
+  h->state.assign(L * S, kFree);
+  h->wa_slot.assign(L * 2, -1);
+  h->launches.assign(L, 0);
+  h->processed.assign(L, 0);
+  h->fill_ev.assign(L * S, nullptr);
+  h->ring.assign(h->ring_n, nullptr);
+  h->ring_ev.assign(h->ring_n, nullptr);
+  h->ring_rows.assign(h->ring_n, {0, 0});
+  int rc = HALO_OK;
+  for (auto& e : h->fill_ev)
+    if (rc == HALO_OK && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) rc = HALO_E_HIP;
+  for (int r = 0; r < h->ring_n && rc == HALO_OK; ++r) {
+    if (hipEventCreateWithFlags(&h->ring_ev[r], hipEventDisableTiming) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&h->ring[r]), L * h->W * sizeof(float), hipHostMallocDefault) !=
+            hipSuccess)
+      rc = HALO_E_HIP;
+  }
+  if (rc != HALO_OK) {
+    set_error("halo_staging_create: event or pinned ring allocation failed");
+    halo_staging_destroy(h);
+    return rc;
+  }
+  reserve_wa(h);
+  *out = h;
+  return HALO_OK;
+}
+
+extern "C" int halo_staging_destroy(halo_staging* h) {
+  if (h == nullptr) return HALO_OK;
+  // pending copies and feedback reads must end before their events and the
+  // ring go away
+  for (auto e : h->ring_ev)
+    if (e) (void)hipEventSynchronize(e);
+  for (auto e : h->fill_ev)
+    if (e) (void)hipEventSynchronize(e);
+  for (auto e : h->ring_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (auto e : h->fill_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (auto p : h->ring)
+    if (p) (void)hipHostFree(p);
+  (void)hipGetLastError();
+  delete h;
+  return HALO_OK;
+}
+
+extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream) {
+  HALO_CHECK_ARG(h != nullptr && 0 <= lo && lo <= hi && hi <= h->L, "bad staging segment");
+  hipStream_t compute = static_cast<hipStream_t>(stream);
+  std::vector<Pending> rest;
+  rest.reserve(h->pending.size());
+  bool any = false;
+  for (const Pending& p : h->pending) {
+    bool take = false;
+    if (lo <= p.layer && p.layer < hi) {
+      hipEvent_t ev = h->fill_ev[(size_t)p.layer * h->S + p.slot];
+      if (p.urgent) {
+        HALO_CHECK_HIP(hipStreamWaitEvent(compute, ev, 0));
+        take = true;
+      } else {
+        const hipError_t e = hipEventQuery(ev);
+        if (e == hipSuccess) {
+          take = true;
+        } else if (e != hipErrorNotReady) {
+          HALO_CHECK_HIP(e);
+        } else {
+          (void)hipGetLastError();
+        }
+      }
+    }
+    if (take) {
+      h->state_at(p.layer, p.slot) = kReady;
+      h->idx_buf.push_back((int64_t)p.layer * h->n + p.chunk);
+      h->val_buf.push_back(p.slot);
+      any = true;
+    } else {
+      rest.push_back(p);
+    }
+  }
+  h->pending.swap(rest);
+  if (h->wa) {
+    const int64_t base = (int64_t)h->L * h->n;
+    for (int li = lo; li < hi; ++li) {
+      // a reservation is named again only after the feedback of the launch
+      // that last named it (two launches back) was processed
+      const int par = (int)(h->launches[li] & 1);
+      const bool ok = h->launches[li] - h->processed[li] < 2;
+      h->idx_buf.push_back(base + li);
+      h->val_buf.push_back(ok ? (int32_t)h->wa_slot[(size_t)li * 2 + par] : -1);
+    }
+  }
+  for (int li = lo; li < hi; ++li) h->launches[li] += 1;
+  if (any && h->track_busy && stream_busy(compute)) h->st.commits_while_busy += 1;
+  return store(h, compute);
+}
+
+extern "C" int halo_staging_after(halo_staging* h, int lo, int hi, void* stream) {
+  HALO_CHECK_ARG(h != nullptr && 0 <= lo && lo < hi && hi <= h->L, "bad staging segment");
+  if (h->queued - h->seen >= h->ring_n) {
+    set_error("feedback ring overrun: call halo_staging_service after every halo_staging_after");
+    return HALO_E_INVALID;
+  }
+  hipStream_t compute = static_cast<hipStream_t>(stream);
+  const int r = (int)(h->queued % h->ring_n);
+  const size_t off = (size_t)lo * h->W, bytes = (size_t)(hi - lo) * h->W * sizeof(float);
+  HALO_CHECK_HIP(hipMemcpyAsync(h->ring[r] + off, h->feedback + off, bytes, hipMemcpyDeviceToHost, compute));
+  HALO_CHECK_HIP(hipEventRecord(h->ring_ev[r], compute));
+  h->ring_rows[r] = {lo, hi};
+  h->queued += 1;
+  return HALO_OK;
+}
+
+extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
+  HALO_CHECK_ARG(h != nullptr && lag >= 0, "bad staging service call");
+  hipStream_t compute = static_cast<hipStream_t>(stream);
+  const int64_t target = h->queued - lag;
+  std::vector<int> layers;
+  std::vector<float> scores;
+  while (h->seen < h->queued) {
+    const int r = (int)(h->seen % h->ring_n);
+    if (h->seen < target) {
+      HALO_CHECK_HIP(hipEventSynchronize(h->ring_ev[r]));
+    } else {
+      const hipError_t e = hipEventQuery(h->ring_ev[r]);
+      if (e == hipErrorNotReady) {
+        (void)hipGetLastError();
+        break;
+      }
+      HALO_CHECK_HIP(e);
+    }
+    const int lo = h->ring_rows[r].first, hi = h->ring_rows[r].second;
+    const float* fb = h->ring[r] + (size_t)lo * h->W;
+    const int rc = account(h, fb, lo, hi, compute);
+    if (rc != HALO_OK) return rc;
+    for (int li = lo; li < hi; ++li) {
+      layers.push_back(li);
+      const float* row = fb + (size_t)(li - lo) * h->W;
+      scores.insert(scores.end(), row, row + h->n);
+    }
+    h->seen += 1;
+  }
+  if (layers.empty()) return HALO_OK;
+  return plan(h, layers, scores, compute);
+}
+
+extern "C" int halo_staging_reset(halo_staging* h) {
+  HALO_CHECK_ARG(h != nullptr, "null staging cache");
+  for (auto e : h->ring_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
+  for (auto e : h->fill_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
+  h->pending.clear();
+  h->seen = h->queued;
+  std::fill(h->slot_of.begin(), h->slot_of.end(), -1);
+  std::fill(h->last_rank.begin(), h->last_rank.end(), (int64_t)h->n);
+  std::fill(h->state.begin(), h->state.end(), (int8_t)kFree);
+  std::fill(h->holds.begin(), h->holds.end(), -1);
+  std::fill(h->wa_slot.begin(), h->wa_slot.end(), -1);
+  std::fill(h->launches.begin(), h->launches.end(), 0);
+  std::fill(h->processed.begin(), h->processed.end(), 0);
+  reserve_wa(h);
+  h->st = halo_staging_stats{};
+  return HALO_OK;
+}
+
+extern "C" int halo_staging_set(halo_staging* h, int max_inflight, int reset_counters) {
+  HALO_CHECK_ARG(h != nullptr && max_inflight >= 0, "bad staging setting");
+  h->max_inflight = max_inflight;
+  if (reset_counters) h->st = halo_staging_stats{};
+  return HALO_OK;
+}
+
+extern "C" int halo_staging_get(const halo_staging* h, halo_staging_stats* stats, int8_t* state, int64_t* holds,
+                                int64_t* wa_slot) {
+  HALO_CHECK_ARG(h != nullptr, "null staging cache");
+  if (stats) *stats = h->st;
+  if (state) std::copy(h->state.begin(), h->state.end(), state);
+  if (holds) std::copy(h->holds.begin(), h->holds.end(), holds);
+  if (wa_slot) std::copy(h->wa_slot.begin(), h->wa_slot.end(), wa_slot);
+  return HALO_OK;
+}

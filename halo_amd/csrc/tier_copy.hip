@@ -128,6 +128,49 @@ __global__ void store_i32_kernel(int32_t* base, int64_t n_elems, StorePairs p) {
   const int i = threadIdx.x;
   if (i < p.n && p.idx[i] >= 0 && p.idx[i] < n_elems) base[p.idx[i]] = p.val[i];
 }
+
+// Fills read by a kernel: up to kFillBatch fills per launch, each split into
+// K and V tensors of `pieces` 64 KiB pieces; workgroup w copies piece
+// w % pieces of tensor (w / pieces) % 2 of fill w / (2 * pieces).  Pieces of
+// one fill are dispatched together, so the batch's fills land in list order.
+constexpr int kFillBatch = 16;
+struct FillBatch {
+  halo_fill f[kFillBatch];
+  int n;
+  int pieces;  // pieces per tensor (of the largest fill in the batch)
+};
+
+__global__ void __launch_bounds__(kCopyThreads) fill_read_kernel(FillBatch b) {
+  const int per_fill = 2 * b.pieces;
+  const int fi = blockIdx.x / per_fill;
+  if (fi >= b.n) return;
+  const int r = blockIdx.x % per_fill;
+  const halo_fill& f = b.f[fi];
+  const bool v = r >= b.pieces;
+  const int piece = v ? r - b.pieces : r;
+  const char* src = static_cast<const char*>(v ? f.src_v : f.src_k);
+  char* dst = static_cast<char*>(v ? f.dst_v : f.dst_k);
+  if (src == nullptr || dst == nullptr) return;
+  const int64_t lo = (int64_t)piece * kCopyPiece;
+  if (lo >= f.bytes) return;
+  const int64_t hi = min(lo + kCopyPiece, f.bytes);
+  const uint4* s = reinterpret_cast<const uint4*>(src + lo);
+  uint4* d = reinterpret_cast<uint4*>(dst + lo);
+  const int n16 = (int)((hi - lo) / 16);
+  for (int base = 0; base < n16; base += kCopyThreads * kCopyUnroll) {
+    uint4 t[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int j = base + u * kCopyThreads + (int)threadIdx.x;
+      if (j < n16) t[u] = s[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int j = base + u * kCopyThreads + (int)threadIdx.x;
+      if (j < n16) d[j] = t[u];
+    }
+  }
+}
 }  // namespace
 }  // namespace halo
 
@@ -140,6 +183,33 @@ extern "C" int halo_stage_fills(const halo_fill* fills, int n, void* stream) {
     if (f.bytes == 0) continue;
     HALO_CHECK_HIP(hipMemcpyAsync(f.dst_k, f.src_k, (size_t)f.bytes, hipMemcpyHostToDevice, st));
     if (f.dst_v != nullptr) HALO_CHECK_HIP(hipMemcpyAsync(f.dst_v, f.src_v, (size_t)f.bytes, hipMemcpyHostToDevice, st));
+  }
+  return HALO_OK;
+}
+
+extern "C" int halo_stage_fills_read(const halo_fill* fills, int n, void* stream) {
+  HALO_CHECK_ARG(n >= 0 && (n == 0 || fills != nullptr), "bad fill list");
+  auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  for (int i0 = 0; i0 < n; i0 += kFillBatch) {
+    FillBatch b{};
+    b.n = n - i0 < kFillBatch ? n - i0 : kFillBatch;
+    int64_t most = 0;
+    for (int j = 0; j < b.n; ++j) {
+      const halo_fill& f = fills[i0 + j];
+      HALO_CHECK_ARG(f.bytes >= 0 && f.bytes % 16 == 0, "fill: bytes must be a non-negative multiple of 16");
+      HALO_CHECK_ARG(f.bytes == 0 || (f.dst_k && f.src_k), "fill: null pointer");
+      HALO_CHECK_ARG(aligned(f.dst_k) && aligned(f.src_k) && aligned(f.dst_v) && aligned(f.src_v),
+                     "fill: addresses must be 16-byte aligned");
+      HALO_CHECK_ARG((f.dst_v == nullptr) == (f.src_v == nullptr), "fill: dst_v and src_v must both be set or NULL");
+      b.f[j] = f;
+      most = f.bytes > most ? f.bytes : most;
+    }
+    if (most == 0) continue;
+    b.pieces = (int)((most + kCopyPiece - 1) / kCopyPiece);
+    HALO_CHECK_ARG((int64_t)b.pieces * 2 * b.n < (int64_t)1 << 31, "fill too large");
+    hipLaunchKernelGGL(fill_read_kernel, dim3((unsigned)(2 * b.pieces * b.n)), dim3(kCopyThreads), 0,
+                       static_cast<hipStream_t>(stream), b);
+    HALO_CHECK_HIP(hipGetLastError());
   }
   return HALO_OK;
 }

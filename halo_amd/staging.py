@@ -9,6 +9,11 @@ residency entry (``halo_select_cfg.residency``): a chosen chunk whose entry
 names a slot is read from HBM (a hit), otherwise in place from host memory
 (a miss, still exact: the rows are the same).
 
+The host side (feedback ring, accounting, policy, fill issue, commits) is
+the library's native runtime (``halo_staging_*`` in include/halo_hip.h), one
+C call per segment of layers; this class owns the device buffers, points the
+layers' selections at them and wraps the runtime.
+
 Policy (reference: HALORefetcher.predict_hot / schedule,
 halo/refetcher.py:38-114 -- predict the next hot set as the top
 (hot + lookahead) by the last score and fetch what is missing on a side
@@ -29,10 +34,12 @@ Ordering (no kernel observes a change while it runs):
     host memory.  A fill still in flight is committed later, except an urgent
     one (a chunk among its layer's current top-k, which the next launch would
     otherwise read over the link): the compute stream waits for its copy;
-  * an eviction stores -1 on the compute stream after the launches already
-    queued; the slot becomes free for a new fill only once an event
-    recorded after that store has completed, i.e. once every launch that
-    could have read the old entry has finished.
+  * evictions are decided only for layers whose feedback just came back:
+    every launch of such a layer has finished (its feedback copy ran behind
+    it) and its next launch is not enqueued yet.  So an eviction stores -1
+    on the compute stream and the slot can take a fill at once: the store
+    runs before any later launch of the layer, and the new chunk's entry is
+    committed only after it.
 A step may run as consecutive segments of layers (one graph each): a
 segment's scores are planned while the later segments execute, so the
 scores of step t can decide that segment's residency from step t + 1 on.
@@ -64,7 +71,8 @@ from . import _native as nat
 from .decode import ChunkRef, descs_to_device, pack_descs
 from .memory_tier import copy_stream
 
-_FREE, _FILLING, _READY, _RELEASING, _RESERVED = 0, 1, 2, 3, 4
+_FREE, _FILLING, _READY, _RESERVED = 0, 1, 2, 4
+_FILL_MODE = {"dma": 0, "kernel": 1}
 
 
 class ColdStaging:
@@ -75,16 +83,21 @@ class ColdStaging:
     same number of cold chunks each.  ``n_slots`` HBM slots per layer (each
     the size of the layer's widest cold chunk); ``keep`` best-scoring chunks
     per layer are staged (default n_slots - 2); ``spare`` slots per layer are
-    kept free or releasing (staged chunks outside the kept set are released
-    worst rank first to keep them); ``max_inflight`` bounds the copies in
-    flight on the link; ``write_allocate`` reserves two slots per layer for
-    missed chunks the kernel writes while reading them (16-bit layers with
-    one selection per launch; ignored otherwise).  It pays when the
-    selection moves fast (fewer bytes over the link) and costs hits when it
-    moves slowly (the reserved slots are missing from the cache)."""
+    kept free (staged chunks outside the kept set are evicted worst rank
+    first to keep them); ``max_inflight`` bounds the copies in flight on the
+    link; ``write_allocate`` reserves two slots per layer for missed chunks
+    the kernel writes while reading them (16-bit layers with one selection
+    per launch; ignored otherwise).  It pays when the selection moves fast
+    (fewer bytes over the link) and costs hits when it moves slowly (the
+    reserved slots are missing from the cache).  ``fill_mode`` "dma" copies
+    with hipMemcpyAsync, "kernel" with copy kernels that read the pinned
+    chunk in place; ``urgent_stream`` gives fills the next launch waits for
+    a copy stream of their own; ``track_busy`` counts operations issued
+    while the compute stream still had work queued (a test aid)."""
 
     def __init__(self, layers: Sequence, *, n_slots: int = 12, keep: Optional[int] = None,
-                 max_inflight: int = 8, spare: int = 0, ring: int = 16, write_allocate: bool = False) -> None:
+                 max_inflight: int = 8, spare: int = 0, ring: int = 16, write_allocate: bool = False,
+                 fill_mode: str = "dma", urgent_stream: bool = True, track_busy: bool = False) -> None:
         if not layers:
             raise AssertionError("no layers")
         self.layers = list(layers)
@@ -98,8 +111,11 @@ class ColdStaging:
         self.keep = int(keep if keep is not None else max(self.top_k, n_slots - 2))
         if not self.top_k <= self.keep <= self.n_slots:
             raise AssertionError(f"keep={self.keep} must be in [top_k={self.top_k}, n_slots={self.n_slots}]")
-        self.max_inflight = int(max_inflight)
+        if fill_mode not in _FILL_MODE:
+            raise AssertionError("fill_mode must be 'kernel' or 'dma'")
+        self.fill_mode = fill_mode
         self.spare = int(spare)
+        self._max_inflight = int(max_inflight)
         L, n, k = len(self.layers), self.n_cold, self.top_k
         for li, lay in enumerate(self.layers):
             if not lay.fused or lay.select_cfg is None:
@@ -119,36 +135,25 @@ class ColdStaging:
         self.write_allocate = bool(write_allocate) and self.n_slots >= self.top_k + 2 and all(
             lay.dtype != torch.float32 and not lay.select_cfg.per_row for lay in self.layers)
         # one feedback row per layer: scores (fp32) | picks (int32) | residency used (int32)
-        self._W = n + 2 * k
-        self.feedback = torch.zeros((L, self._W), dtype=torch.float32, device=dev)
+        W = n + 2 * k
+        self.feedback = torch.zeros((L, W), dtype=torch.float32, device=dev)
         self.scores = self.feedback[:, :n]
         self.idx = self.feedback[:, n:n + k].view(torch.int32)
         self.res_out = self.feedback[:, n + k:].view(torch.int32)
         self.idx.fill_(-1)
         self.res_out.fill_(-1)
-        self._ring = [torch.empty((L, self._W), dtype=torch.float32, pin_memory=True) for _ in range(max(2, ring))]
-        self._ring_ev = [torch.cuda.Event() for _ in self._ring]
-        self._ring_rows = [(0, L)] * len(self._ring)
-        self._queued = 0           # segments whose feedback was queued for the host
-        self._seen = 0             # segments the host has processed
-        # host mirror of the cache
-        self.slot_of = np.full((L, n), -1, dtype=np.int64)        # FILLING / READY slot of a chunk
-        self.state = np.full((L, self.n_slots), _FREE, dtype=np.int8)
-        self.holds = np.full((L, self.n_slots), -1, dtype=np.int64)
-        self._pending: list = []   # (layer, chunk, slot, event, urgent): fills not committed yet
-        self._last_rank = np.full((L, n), n, dtype=np.int64)     # rank at the last planning pass
-        self._releasing: list = []
-        self._release_ev: Optional[torch.cuda.Event] = None
         self.chunk_bytes = np.zeros((L, n), dtype=np.int64)
         self._slot_k, self._slot_v, self._slot_cat = [], [], []
-        # addresses for the batched copies: slot (layer, s) K/V, cold chunk (layer, c) K/V, bytes per tensor
-        self._dst = np.zeros((L, self.n_slots, 2), dtype=np.uint64)
-        self._src = np.zeros((L, n, 2), dtype=np.uint64)
-        self._nbytes = np.zeros((L, n), dtype=np.int64)
+        # slot (layer, s) K/V addresses, cold chunk (layer, c) K/V addresses, bytes per tensor
+        dst = np.zeros((L, self.n_slots, 2), dtype=np.uint64)
+        src = np.zeros((L, n, 2), dtype=np.uint64)
+        nbytes = np.zeros((L, n), dtype=np.int64)
         for li, lay in enumerate(self.layers):
             shape = max((tuple(c.k.shape) for c in lay.cold), key=lambda s: s[-2])
-            sk = torch.empty((self.n_slots,) + shape, dtype=lay.dtype, device=dev)
-            sv = torch.empty_like(sk)
+            # a slot's K rows and V rows are adjacent, so a cold chunk laid out
+            # the same way on the host is filled by one copy
+            skv = torch.empty((self.n_slots, 2) + shape, dtype=lay.dtype, device=dev)
+            sk, sv = skv[:, 0], skv[:, 1]
             # slot descriptors never change: they give the addresses and strides
             # a staged chunk is read through; its rows, start and flags come
             # from the chunk's own catalog entry
@@ -158,14 +163,17 @@ class ColdStaging:
             self._slot_v.append(sv)
             self._slot_cat.append(descs_to_device(sdesc, dev))
             for j in range(self.n_slots):
-                self._dst[li, j] = (sk[j].data_ptr(), sv[j].data_ptr())
+                dst[li, j] = (sk[j].data_ptr(), sv[j].data_ptr())
             for j, c in enumerate(lay.cold):
                 if tuple(c.k.shape) != tuple(sk.shape[1:]):
                     raise AssertionError(f"layer {li} cold chunk {j}: shape {tuple(c.k.shape)} differs from the "
                                          f"layer's other cold chunks {tuple(sk.shape[1:])}")
-                self._src[li, j] = (c.k.data_ptr(), c.v.data_ptr())
-                self._nbytes[li, j] = c.k.numel() * c.k.element_size()
-            self.chunk_bytes[li] = 2 * self._nbytes[li]
+                if fill_mode == "kernel":   # the copy kernel reads the pinned chunk in place
+                    src[li, j] = (nat.host_device_pointer(c.k.data_ptr()), nat.host_device_pointer(c.v.data_ptr()))
+                else:
+                    src[li, j] = (c.k.data_ptr(), c.v.data_ptr())
+                nbytes[li, j] = c.k.numel() * c.k.element_size()
+            self.chunk_bytes[li] = 2 * nbytes[li]
             cfg = lay.select_cfg
             cfg.n_slots = self.n_slots
             cfg.slot_catalog = self._slot_cat[li].data_ptr()
@@ -174,13 +182,31 @@ class ColdStaging:
             cfg.score_out = self.scores[li].data_ptr()
             cfg.idx_out = self.idx[li].data_ptr()
             cfg.alloc_slot = self.alloc[li].data_ptr() if self.write_allocate else None
-        # write-allocate reservations (two per layer), launches queued and
-        # feedback rows processed per layer
-        self.wa = np.full((L, 2), -1, dtype=np.int64)
-        self._launches = np.zeros(L, dtype=np.int64)
-        self._processed = np.zeros(L, dtype=np.int64)
-        self._reserve_wa()
-        self.reset_counters()
+        # the copy streams outlive the runtime (it holds their handles)
+        self._copy = copy_stream(dev)
+        # urgent fills (chunks the next launch of their layer selects) go on a
+        # stream of their own, so they share the link with the prefetches
+        # queued before them instead of waiting behind them
+        self._urgent = torch.cuda.Stream(device=dev) if urgent_stream else None
+        self._addr = (dst, src, nbytes)    # read at creation; kept for inspection
+        d = nat.StagingDesc(n_layers=L, n_cold=n, n_slots=self.n_slots, top_k=k, keep=self.keep,
+                            max_inflight=self._max_inflight, spare=self.spare, ring=max(2, int(ring)),
+                            write_allocate=int(self.write_allocate), fill_mode=_FILL_MODE[fill_mode],
+                            track_busy=int(track_busy), residency=self._dev_i32.data_ptr(),
+                            feedback=self.feedback.data_ptr(), slot_addr=dst.ctypes.data,
+                            chunk_addr=src.ctypes.data, chunk_nbytes=nbytes.ctypes.data,
+                            copy_stream=self._copy.cuda_stream,
+                            urgent_stream=self._urgent.cuda_stream if self._urgent is not None else None)
+        self._L = nat.lib()
+        h = ctypes.c_void_p()
+        nat.check(self._L.halo_staging_create(ctypes.byref(d), ctypes.byref(h)), "halo_staging_create")
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._L.halo_staging_destroy(h)
+            self._h = None
 
     # ----------------------------------------------------------------- per step
     # ``lo``/``hi`` name a segment of layers [lo, hi) run as one graph; the
@@ -192,46 +218,16 @@ class ColdStaging:
         for their copy, with one batched store of residency entries on the
         compute stream.  Call before enqueueing those layers' launches."""
         hi = len(self.layers) if hi is None else hi
-        compute = torch.cuda.current_stream(self.device)
-        done, rest, waited = [], [], set()
-        for p in self._pending:
-            li, c, s, ev, urgent = p
-            if lo <= li < hi and (urgent or ev.query()):
-                if urgent and id(ev) not in waited:
-                    compute.wait_event(ev)
-                    waited.add(id(ev))
-                done.append(p)
-            else:
-                rest.append(p)
-        self._pending = rest
-        idx = [li * self.n_cold + c for li, c, _, _, _ in done]
-        val = [s for _, _, s, _, _ in done]
-        for li, c, s, _, _ in done:
-            self.state[li, s] = _READY
-        if self.write_allocate:
-            base = len(self.layers) * self.n_cold
-            for li in range(lo, hi):
-                # a reservation is named again only after the feedback of the
-                # launch that last named it (two launches back) was processed
-                par = int(self._launches[li] & 1)
-                ok = self._launches[li] - self._processed[li] < 2
-                idx.append(base + li)
-                val.append(int(self.wa[li, par]) if ok else -1)
-        self._launches[lo:hi] += 1
-        if idx:
-            self._store(idx, val)
+        nat.check(self._L.halo_staging_before(self._h, lo, hi, nat.stream_ptr()), "halo_staging_before")
 
     def after_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
         """Queue the feedback rows of layers [lo, hi) (scores, picks,
         residency used) for the host: one copy after those layers' launches."""
         hi = len(self.layers) if hi is None else hi
-        if self._queued - self._seen >= len(self._ring):
+        rc = self._L.halo_staging_after(self._h, lo, hi, nat.stream_ptr())
+        if rc == nat.HALO_E_INVALID and b"overrun" in self._L.halo_last_error():
             raise RuntimeError("feedback ring overrun: call service() after every after_step()")
-        r = self._queued % len(self._ring)
-        self._ring[r][lo:hi].copy_(self.feedback[lo:hi], non_blocking=True)
-        self._ring_ev[r].record(torch.cuda.current_stream(self.device))
-        self._ring_rows[r] = (lo, hi)
-        self._queued += 1
+        nat.check(rc, "halo_staging_after")
 
     def drain(self) -> None:
         """Process every queued segment's feedback now (waits for it)."""
@@ -240,200 +236,76 @@ class ColdStaging:
     def service(self, *, lag: int = 1) -> None:
         """Process returned feedback -- waiting for every queued segment but
         the ``lag`` newest, and taking those too when they are done -- count
-        hits and misses, free released slots, and plan evictions and fills
-        for the processed segments' layers."""
-        target = self._queued - lag
-        rows, scores = [], []
-        while self._seen < self._queued:
-            r = self._seen % len(self._ring)
-            if self._seen < target:
-                self._ring_ev[r].synchronize()
-            elif not self._ring_ev[r].query():
-                break
-            lo, hi = self._ring_rows[r]
-            fb = self._ring[r].numpy()[lo:hi]
-            self._account(fb, lo)
-            rows.append(np.arange(lo, hi))
-            scores.append(fb[:, :self.n_cold].copy())
-            self._seen += 1
-        if self._release_ev is not None and self._release_ev.query():
-            for li, s in self._releasing:
-                self.state[li, s] = _FREE
-                self.holds[li, s] = -1
-            self._releasing = []
-            self._release_ev = None
-            self._reserve_wa()
-        if rows:
-            self._plan(np.concatenate(rows), np.concatenate(scores))
-
-    # ----------------------------------------------------------------- internals
-    def _store(self, flat_idx: list, values: list) -> None:
-        """residency.view(-1)[flat_idx] = values on the compute stream (the
-        pairs travel in the kernel arguments)."""
-        idx = np.ascontiguousarray(flat_idx, dtype=np.int64)
-        val = np.ascontiguousarray(values, dtype=np.int32)
-        nat.check(nat.lib().halo_store_i32(self._dev_i32.data_ptr(), self._dev_i32.numel(), idx.ctypes.data,
-                                           val.ctypes.data, len(idx), nat.stream_ptr()), "halo_store_i32")
-
-    def _account(self, fb: np.ndarray, lo: int) -> None:
-        n, k = self.n_cold, self.top_k
-        idx = np.ascontiguousarray(fb[:, n:n + k]).view(np.int32)
-        res = np.ascontiguousarray(fb[:, n + k:]).view(np.int32)
-        valid = idx >= 0
-        miss = valid & (res < 0)
-        self.hits += int((valid & (res >= 0)).sum())
-        self.misses += int(miss.sum())
-        self._processed[lo:lo + fb.shape[0]] += 1
-        if self.write_allocate:
-            wr, wj = np.nonzero(valid & (res <= -2))
-            commits_i, commits_v = [], []
-            for r, j in zip(wr.tolist(), wj.tolist()):
-                li, c, w = lo + r, int(idx[r, j]), -2 - int(res[r, j])
-                q = np.flatnonzero(self.wa[li] == w)
-                if q.size == 0:
-                    continue  # not a current reservation: nothing to commit
-                if self.slot_of[li, c] >= 0:
-                    self.wa_dups += 1  # staged or filling elsewhere meanwhile: keep the reservation
-                    continue
-                self.state[li, w] = _READY
-                self.holds[li, w] = c
-                self.slot_of[li, c] = w
-                commits_i.append(li * self.n_cold + c)
-                commits_v.append(w)
-                self.wa[li, q[0]] = -1
-                self.wa_commits += 1
-            if commits_i:
-                self._store(commits_i, commits_v)
-                self._reserve_wa()
-        if miss.any():
-            r, j = np.nonzero(miss)
-            self.miss_bytes += int(self.chunk_bytes[lo + r, idx[r, j]].sum())
-            # a miss the policy had predicted (in the kept set at the last plan:
-            # its fill had not landed or been committed) or one it had not
-            predicted = self._last_rank[lo + r, idx[r, j]] < self.keep
-            self.misses_predicted += int(predicted.sum())
-
-    def _plan(self, layers: np.ndarray, scores: np.ndarray) -> None:
-        sc = np.where(np.isnan(scores), -np.inf, scores)
-        order = np.argsort(-sc, axis=1, kind="stable")      # score desc, index asc
-        rank = np.empty_like(order)
-        np.put_along_axis(rank, order, np.arange(sc.shape[1])[None, :], axis=1)
-        self._last_rank[layers] = rank
-        missing = (rank < self.keep) & (self.slot_of[layers] < 0)
-        evicted, fills = [], []
-        # keep `spare` slots per layer free or on their way to free, releasing
-        # the worst-ranked staged chunks outside the kept set, so a newly
-        # predicted chunk finds a slot without waiting for a release
-        for i, li in enumerate(layers):
-            st = self.state[li]
-            short = self.spare - int(((st == _FREE) | (st == _RELEASING)).sum())
-            if short <= 0:
-                continue
-            ready = np.flatnonzero(st == _READY)
-            if ready.size == 0:
-                continue
-            rk = rank[i][self.holds[li, ready]]
-            for j in np.argsort(-rk, kind="stable")[:short]:
-                if rk[j] < self.keep:
-                    break
-                s = int(ready[j])
-                evicted.append((int(li), int(self.holds[li, s]), s))
-                self.slot_of[li, self.holds[li, s]] = -1
-                self.state[li, s] = _RELEASING
-        r, c = np.nonzero(missing)
-        pri = np.lexsort((layers[r], rank[r, c]))           # best ranks first, then layer order
-        budget = self.max_inflight - len(self._pending)
-        for i in pri:
-            if budget <= 0:
-                break
-            li, ch, rk = int(layers[r[i]]), int(c[i]), rank[r[i]]
-            free = np.flatnonzero(self.state[li] == _FREE)
-            if free.size == 0:
-                ready = np.flatnonzero(self.state[li] == _READY)
-                if ready.size:
-                    worst = ready[np.argmax(rk[self.holds[li, ready]])]
-                    if rk[self.holds[li, worst]] >= self.keep:
-                        evicted.append((li, int(self.holds[li, worst]), int(worst)))
-                        self.slot_of[li, self.holds[li, worst]] = -1
-                        self.state[li, worst] = _RELEASING
-                continue
-            fills.append(self._reserve(li, ch, int(free[0]), bool(rk[ch] < self.top_k)))
-            budget -= 1
-        if fills:
-            self._issue(fills)
-        if evicted:
-            self._store([li * self.n_cold + ch for li, ch, _ in evicted], [-1] * len(evicted))
-            self._releasing += [(li, s) for li, _, s in evicted]
-            ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.device))
-            self._release_ev = ev
-
-    def _reserve_wa(self) -> None:
-        """Give every empty write-allocate reservation a free slot (highest
-        index first, away from the fills, which take the lowest)."""
-        if not self.write_allocate:
-            return
-        for li, q in zip(*np.nonzero(self.wa < 0)):
-            free = np.flatnonzero(self.state[li] == _FREE)
-            if free.size:
-                s = int(free[-1])
-                self.state[li, s] = _RESERVED
-                self.wa[li, q] = s
-
-    def _reserve(self, li: int, c: int, s: int, urgent: bool) -> tuple:
-        self.state[li, s] = _FILLING
-        self.holds[li, s] = c
-        self.slot_of[li, c] = s
-        self.fills += 1
-        self.fill_bytes += int(self.chunk_bytes[li, c])
-        return li, c, s, urgent
-
-    def _issue(self, fills: list) -> None:
-        """hipMemcpyAsync copies on the copy stream in the given order (best
-        ranks first), each fill followed by its own event so it commits as
-        soon as it lands."""
-        cs = copy_stream(self.device)
-        L = nat.lib()
-        arr = nat.Fill()
-        for li, c, s, urgent in fills:
-            arr.dst_k, arr.dst_v = int(self._dst[li, s, 0]), int(self._dst[li, s, 1])
-            arr.src_k, arr.src_v = int(self._src[li, c, 0]), int(self._src[li, c, 1])
-            arr.bytes = int(self._nbytes[li, c])
-            nat.check(L.halo_stage_fills(ctypes.byref(arr), 1, nat.stream_ptr(cs)), "halo_stage_fills")
-            ev = torch.cuda.Event()
-            ev.record(cs)
-            self._pending.append((li, c, s, ev, urgent))
+        hits and misses, and plan evictions and fills for the processed
+        segments' layers."""
+        nat.check(self._L.halo_staging_service(self._h, int(lag), nat.stream_ptr()), "halo_staging_service")
 
     # ----------------------------------------------------------------- control
     def clear(self) -> None:
         """Empty every slot (synchronises the device first)."""
         torch.cuda.synchronize(self.device)
-        self._pending, self._releasing, self._release_ev = [], [], None
-        self._seen = self._queued
+        nat.check(self._L.halo_staging_reset(self._h), "halo_staging_reset")
         self._dev_i32.fill_(-1)
-        self.slot_of.fill(-1)
-        self._last_rank.fill(self.n_cold)
-        self.state.fill(_FREE)
-        self.holds.fill(-1)
-        self.wa.fill(-1)
-        self._launches.fill(0)
-        self._processed.fill(0)
-        self._reserve_wa()
         torch.cuda.synchronize(self.device)
-        self.reset_counters()
+
+    @property
+    def max_inflight(self) -> int:
+        return self._max_inflight
+
+    @max_inflight.setter
+    def max_inflight(self, v: int) -> None:
+        self._max_inflight = int(v)
+        nat.check(self._L.halo_staging_set(self._h, self._max_inflight, 0), "halo_staging_set")
+
+    def reset_counters(self) -> None:
+        nat.check(self._L.halo_staging_set(self._h, self._max_inflight, 1), "halo_staging_set")
+
+    def _snapshot(self):
+        L = len(self.layers)
+        stats = nat.StagingStats()
+        state = np.empty((L, self.n_slots), dtype=np.int8)
+        holds = np.empty((L, self.n_slots), dtype=np.int64)
+        wa = np.empty((L, 2), dtype=np.int64)
+        nat.check(self._L.halo_staging_get(self._h, ctypes.byref(stats), state.ctypes.data, holds.ctypes.data,
+                                           wa.ctypes.data), "halo_staging_get")
+        return stats, state, holds, wa
+
+    @property
+    def stats(self) -> dict:
+        s = self._snapshot()[0]
+        return {name: int(getattr(s, name)) for name, _ in nat.StagingStats._fields_}
+
+    def __getattr__(self, name):
+        # counters of the native runtime: hits, misses, misses_predicted,
+        # fills, fill_bytes, miss_bytes, wa_commits, wa_dups, *_while_busy
+        if name in {f for f, _ in nat.StagingStats._fields_}:
+            return int(getattr(self._snapshot()[0], name))
+        raise AttributeError(name)
+
+    @property
+    def state(self) -> np.ndarray:
+        """Slot states (layers, n_slots): 0 free, 1 filling, 2 ready, 4 reserved."""
+        return self._snapshot()[1]
+
+    @property
+    def holds(self) -> np.ndarray:
+        """Chunk each slot holds (layers, n_slots), -1 for none."""
+        return self._snapshot()[2]
+
+    @property
+    def wa(self) -> np.ndarray:
+        """Write-allocate slots (layers, 2), -1 for none."""
+        return self._snapshot()[3]
 
     def resident(self, layer: int) -> list:
         """Chunks of ``layer`` whose residency entry has been committed."""
-        return sorted(int(self.holds[layer, s]) for s in np.flatnonzero(self.state[layer] == _READY))
-
-    def reset_counters(self) -> None:
-        self.hits = self.misses = self.fills = self.fill_bytes = self.miss_bytes = 0
-        self.wa_commits = self.wa_dups = 0
-        self.misses_predicted = 0
+        _, state, holds, _ = self._snapshot()
+        return sorted(int(holds[layer, s]) for s in np.flatnonzero(state[layer] == _READY))
 
     def hit_rate(self) -> float:
-        n = self.hits + self.misses
-        return self.hits / n if n else 0.0
+        s = self._snapshot()[0]
+        n = s.hits + s.misses
+        return s.hits / n if n else 0.0
 
     @property
     def slot_bytes(self) -> int:

@@ -481,6 +481,17 @@ typedef struct halo_fill {
 int halo_stage_fills(const halo_fill* fills, int n, void* stream);
 
 /*
+ * The same fills as copy kernels on `stream` (one launch per 16 fills) that
+ * read the sources in place over the host link: src_k / src_v must be
+ * device-visible addresses of pinned host memory (halo_host_device_pointer);
+ * all addresses 16-byte aligned, bytes % 16 == 0.  Kernel reads of pinned
+ * memory sustain a higher host-link rate than hipMemcpyAsync of 2-4 MiB
+ * pieces.  Replaces move_block's copies in HALORefetcher._issue
+ * (halo/refetcher.py:102-114) for the staging cache.
+ */
+int halo_stage_fills_read(const halo_fill* fills, int n, void* stream);
+
+/*
  * base[idx[i]] = vals[i] for i < n (entries with idx outside [0, n_elems)
  * are skipped), as kernels on `stream` whose pairs travel in the kernel
  * arguments: the host arrays are read during the call only.  The staging
@@ -489,6 +500,83 @@ int halo_stage_fills(const halo_fill* fills, int n, void* stream);
  * halo/memory_tier.py:133).
  */
 int halo_store_i32(int32_t* base, int64_t n_elems, const int64_t* idx, const int32_t* vals, int n, void* stream);
+
+/* ---- HBM staging cache: host runtime ------------------------------------ */
+
+/*
+ * Description of a staging cache over n_layers decode layers whose fused
+ * selections (halo_select_cfg) already point at `residency`, the slot
+ * catalogs and `feedback`.  All arrays are copied at creation.
+ *   residency:   device int32[n_layers * n_cold + n_layers]: the residency
+ *                entries (slot or -1) then each layer's write-allocate slot;
+ *   feedback:    device fp32 rows (n_layers, n_cold + 2 * top_k): scores |
+ *                picks (int32) | residency used (int32), written by the kernel;
+ *   slot_addr:   (n_layers, n_slots, 2) device addresses of each slot's K, V;
+ *   chunk_addr:  (n_layers, n_cold, 2) addresses of each cold chunk's K, V:
+ *                host pointers of pinned memory (fill_mode 0, hipMemcpyAsync)
+ *                or device-visible ones (fill_mode 1, copy kernels); a chunk
+ *                whose V follows its K, staged into a slot laid out the same
+ *                way, is filled by one copy;
+ *   chunk_nbytes:(n_layers, n_cold) bytes of one chunk's K (= its V);
+ *   copy_stream / urgent_stream: where fills run (urgent: fills the next
+ *                launch of their layer waits for; NULL = copy_stream).
+ * keep in [top_k, n_slots] best-scoring chunks per layer are staged; at most
+ * max_inflight fills in flight; `spare` slots per layer kept free;
+ * `ring` feedback entries in flight (>= segments per step + 1);
+ * track_busy counts operations issued while the compute stream still had
+ * work queued (a test aid; costs one stream query each).
+ */
+typedef struct halo_staging_desc {
+  int32_t n_layers, n_cold, n_slots, top_k, keep, max_inflight, spare, ring;
+  int32_t write_allocate, fill_mode, track_busy, pad;
+  int32_t* residency;
+  const float* feedback;
+  const uint64_t* slot_addr;
+  const uint64_t* chunk_addr;
+  const int64_t* chunk_nbytes;
+  void* copy_stream;
+  void* urgent_stream;
+} halo_staging_desc;
+
+typedef struct halo_staging_stats {
+  int64_t hits, misses, misses_predicted, fills, fill_bytes, miss_bytes, wa_commits, wa_dups;
+  int64_t fills_while_busy, commits_while_busy, evictions_while_busy;
+} halo_staging_stats;
+
+typedef struct halo_staging halo_staging;
+
+/*
+ * The cache's host side, one call per segment of layers [lo, hi) run as
+ * one graph (or launches) on the compute `stream`:
+ *   halo_staging_before  -- commit the landed (and, after a compute-stream
+ *                           wait, the urgent) fills of the segment's layers
+ *                           and name their write-allocate slots: one store
+ *                           kernel; call before the segment's launches;
+ *   halo_staging_after   -- queue the segment's feedback rows for the host
+ *                           (one device-to-host copy + event); call after;
+ *   halo_staging_service -- process returned feedback (waiting for all but
+ *                           the `lag` newest segments, taking those too when
+ *                           done): count hits and misses, evict, and issue
+ *                           the fills of the best-ranked missing chunks.
+ * The reference's HALORefetcher.predict_hot / schedule / _issue / wait
+ * (halo/refetcher.py:38-114) with the scores written by the selection.
+ * Calls on one cache are not thread-safe.  halo_staging_reset waits for the
+ * cache's copies and forgets every slot (the caller clears `residency`);
+ * halo_staging_set changes max_inflight and can zero the counters;
+ * halo_staging_get copies the counters and the host mirror: slot state
+ * (n_layers, n_slots) int8 (0 free, 1 filling, 2 ready, 4 reserved), the
+ * chunk each slot holds (int64, -1 none) and the write-allocate slots
+ * (n_layers, 2) int64; any output may be NULL.
+ */
+int halo_staging_create(const halo_staging_desc* desc, halo_staging** out);
+int halo_staging_destroy(halo_staging* cache);
+int halo_staging_before(halo_staging* cache, int lo, int hi, void* stream);
+int halo_staging_after(halo_staging* cache, int lo, int hi, void* stream);
+int halo_staging_service(halo_staging* cache, int lag, void* stream);
+int halo_staging_reset(halo_staging* cache);
+int halo_staging_set(halo_staging* cache, int max_inflight, int reset_counters);
+int halo_staging_get(const halo_staging* cache, halo_staging_stats* stats, int8_t* state, int64_t* holds,
+                     int64_t* wa_slot);
 
 /* ---- build metadata ---------------------------------------------------- */
 /*

@@ -249,6 +249,51 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     }
 
 
+def kernel_level_c2(torch, layers, qs, *, scale, reps, with_scorer=True):
+    """The C2 layers with every cold chunk in HBM, one HIP graph of all
+    layers (attention with in-kernel selection + merge per layer), timed
+    with events on the capture stream over ``reps`` replays.  Returns ms per
+    layer of the attention launch and of the standalone scorer."""
+    L = len(layers)
+    H, D = layers[0].H, layers[0].D
+    dev = qs[0].device
+    outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    lses = [torch.empty((1, H), device=dev, dtype=torch.float32) for _ in range(L)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def capture(fn):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr, stream=s):
+                fn()
+        torch.cuda.synchronize()
+        return gr
+
+    def time_graph(gr, reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            gr.replay()
+            e0.record(s)
+            for _ in range(reps):
+                gr.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * L)
+
+    g_attn = capture(lambda: [layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li]) for li in range(L)])
+    attn_avg = time_graph(g_attn, reps)          # ms per layer: attention kernel + merge kernel
+    del g_attn
+    score_avg = None
+    if with_scorer:
+        g_score = capture(lambda: [layers[li].select(qs[li]) for li in range(L)])
+        score_avg = time_graph(g_score, reps)
+        del g_score
+    return attn_avg, score_avg
+
+
 def bench_prefill_c3(torch, dev, *, reps: int):
     """Chunked causal prefill, Llama-3-8B GQA shape: a 4096-token query block
     attends 28 prior chunks of 1024 rows plus itself (causal), bf16 MFMA.
@@ -483,8 +528,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c3", "c4", "c5", "dropin"], default=None,
-                    help="run one secondary leg alone (chunked prefill, ragged batch, KIVI) and print its reading")
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "dropin"], default=None,
+                    help="run one leg alone (C2 kernel level, chunked prefill, ragged batch, KIVI, drop-in) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
     args = ap.parse_args()
@@ -507,7 +552,16 @@ def main() -> int:
             lays, q_, _ = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
                                       n_planted=4, sigma=8.0, dev=dev, seed=1)
             return bench_dropin_c2(torch, dev, lays, q_, top_k=top_k, steps=max(1, args.steps))
-        leg = {"c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
+        def c2():
+            lays, q_, _ = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
+                                      n_planted=4, sigma=8.0, dev=dev, seed=1, split=args.split,
+                                      fused=not args.unfused)
+            a, _ = kernel_level_c2(torch, lays, q_, scale=1.0 / math.sqrt(D), reps=max(1, args.steps),
+                                   with_scorer=False)
+            return {"workload": "C2 kernel level: 32 layers, all chunks in HBM, attention with in-kernel "
+                                "selection + merge per layer, one graph", "us_per_layer": a * 1e3}
+        leg = {"c2": c2,
+               "c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
                "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
                "dropin": dropin}[args.only]
@@ -541,41 +595,10 @@ def main() -> int:
     dt = head["ms_per_step"] * 1e-3
 
     # ------------------------------------------------- kernel-level (all HBM)
-    outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
-    lses = [torch.empty((1, H), device=dev, dtype=torch.float32) for _ in range(L)]
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-
-    def capture(fn):
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            fn()
-            torch.cuda.synchronize()
-            with torch.cuda.graph(gr, stream=s):
-                fn()
-        torch.cuda.synchronize()
-        return gr
-
-    def time_graph(gr, reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(s):
-            gr.replay()
-            e0.record(s)
-            for _ in range(reps):
-                gr.replay()
-            e1.record(s)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / (reps * L)
-
-    g_attn = capture(lambda: [layers[li].step(qs[li], scale=scale, out=outs[li], lse=lses[li]) for li in range(L)])
-    g_score = capture(lambda: [layers[li].select(qs[li]) for li in range(L)])
-    reps = 50
-    attn_avg = time_graph(g_attn, reps)          # ms per layer: attention kernel + merge kernel
-    score_avg = time_graph(g_score, reps)
+    attn_avg, score_avg = kernel_level_c2(torch, layers, qs, scale=scale, reps=50)
     achieved = attn_bytes / (attn_avg * 1e-3) / 1e9
     log(f"kernel-level (all HBM): attention launch avg {attn_avg * 1e3:.2f} us ({achieved:.0f} GB/s), "
         f"{1.0 / (attn_avg * 1e-3 * L):.0f} tokens/s; standalone scorer {score_avg * 1e3:.2f} us")
-    del g_attn, g_score
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "decode_attn_c2_traffic.json")

@@ -107,19 +107,66 @@ struct KiviQuantParams {
   int H_kv, n_blk;
   uint8_t* blocks;
   int64_t bsb, bsh;  // bytes
+  int vec16;         // K and V rows 16-byte aligned: tiles loaded with 16-byte loads
 };
 
-// One workgroup per block: stage the 32 x D K and V tiles in LDS as fp32,
-// per-group min/max, codes, then packed bytes with coalesced stores.
+// Code of x for a group with precomputed inv = 1/scale (correctly rounded):
+// clamp(rint(dtype(dtype(x - zero) / scale)), 0, qmax).  The fp32 quotient
+// is formed without a division: q = d * inv, r = fma(-q, scale, d),
+// q' = fma(r, inv, q) equals the correctly rounded d / scale whenever d
+// (a dtype value >= 0) is 0 or in [2^-63, 2^63] and scale is in [2^-63,
+// 2^63] -- checked exhaustively for every pair of fp16 and bf16 values.
+// Outside that range (a zero scale, extreme bf16 values) the division runs.
+__device__ __forceinline__ float kivi_scale_ok(float scale) {
+  return scale >= 0x1p-63f && scale <= 0x1p63f ? 1.f : 0.f;
+}
+// p = (scale, 1/scale, zero, kivi_scale_ok(scale))
+template <int DT, int BITS>
+__device__ __forceinline__ uint32_t kivi_code_fma(float x, float4 p) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const float scale = p.x, inv = p.y, zero = p.z;
+  const float d = round_dt<DT>(opaque(x - zero));
+  const bool s_ok = p.w != 0.f;
+  const bool ok = DT == HALO_F16 ? s_ok : (s_ok && (d == 0.f || (d >= 0x1p-63f && d <= 0x1p63f)));
+  float q;
+  if (ok) {
+    const float q0 = opaque(d * inv);
+    const float r = __builtin_fmaf(-q0, scale, d);
+    q = __builtin_fmaf(r, inv, q0);
+  } else {
+    q = opaque(d / scale);
+  }
+  if constexpr (DT == HALO_F16) {
+    // ratio in fp16; NaN -> 0 through the IEEE max, codes in [0, qmax]
+    const _Float16 r16 = (_Float16)q;
+    _Float16 c16 = __builtin_rintf16(r16);
+    c16 = __builtin_fminf16(__builtin_fmaxf16(c16, (_Float16)0.f), (_Float16)qmax);
+    return (uint32_t)(unsigned short)c16;
+  } else {
+    const float ratio = round_dt<DT>(q);
+    return (uint32_t)fminf(fmaxf(rintf(ratio), 0.f), qmax);
+  }
+}
+
+// One workgroup per block, 256 threads.  The 32 x D K and V tiles are staged
+// in LDS in their storage dtype (16-byte loads; rows padded by 16 bytes so
+// column and row-run reads spread over the banks); pairs of threads reduce
+// each K channel and each V (token, 32-channel group) to its min / max;
+// then each thread codes a run of consecutive elements of one output row
+// and stores its packed bytes in one store (K rows token-major, V rows
+// channel-major in slot order), so every global access is a vector access.
 template <int DT, int D, int BITS>
 __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
   constexpr int G = kKiviG;
   constexpr int C = kivi_code_bytes(D, BITS);
-  constexpr int CPB = 8 / BITS;  // codes per byte
-  constexpr int NG = D / G;      // V groups per token
-  __shared__ float s_k[G][D + 1], s_v[G][D + 1];
-  __shared__ uint8_t s_ck[G * D], s_cv[G * D];
-  __shared__ uint16_t s_ks[D], s_kz[D], s_vs[G * NG], s_vz[G * NG];
+  constexpr int NG = D / G;                  // V groups per token
+  constexpr int RS = D + 8;                  // LDS row stride (elements)
+  constexpr int KR = G * D / 256;            // elements per thread per code run: 8, 16 or 32
+  constexpr int KP = D + D / KR;             // padded params (one float4 per channel, a pad per run)
+  __shared__ __align__(16) uint16_t s_k[G * RS], s_v[G * RS];
+  __shared__ float s_kmn[2][D], s_kmx[2][D], s_vmn[2][G * NG], s_vmx[2][G * NG];
+  __shared__ __align__(16) float4 s_kp[KP];  // (scale, 1/scale, zero, scale in range) per channel
+  __shared__ __align__(16) float4 s_vp[G * NG];
   const int tid = threadIdx.x;
   const int j = blockIdx.x % P.n_blk;
   const int bh = blockIdx.x / P.n_blk;
@@ -128,65 +175,132 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
                        (int64_t)j * G * P.kst;
   const uint16_t* vb = reinterpret_cast<const uint16_t*>(P.v) + (int64_t)b * P.vsb + (int64_t)h * P.vsh +
                        (int64_t)j * G * P.vst;
-  for (int e = tid; e < G * D; e += 256) {
-    const int t = e / D, d = e % D;
-    s_k[t][d] = from_bits<DT>(kb[(int64_t)t * P.kst + d]);
-    s_v[t][d] = from_bits<DT>(vb[(int64_t)t * P.vst + d]);
+  if (P.vec16) {
+    constexpr int PR = D / 8;  // 16-byte pieces per row
+    uint4 kk[G * PR / 256], vv[G * PR / 256];
+#pragma unroll
+    for (int i = 0; i < G * PR / 256; ++i) {
+      const int e = tid + 256 * i, t = e / PR, c = e % PR;
+      kk[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)t * P.kst + 8 * c);
+      vv[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)t * P.vst + 8 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < G * PR / 256; ++i) {
+      const int e = tid + 256 * i, t = e / PR, c = e % PR;
+      *reinterpret_cast<uint4*>(&s_k[t * RS + 8 * c]) = kk[i];
+      *reinterpret_cast<uint4*>(&s_v[t * RS + 8 * c]) = vv[i];
+    }
+  } else {
+    for (int e = tid; e < G * D; e += 256) {
+      const int t = e / D, d = e % D;
+      s_k[t * RS + d] = kb[(int64_t)t * P.kst + d];
+      s_v[t * RS + d] = vb[(int64_t)t * P.vst + d];
+    }
   }
   __syncthreads();
-  // K: per channel over the 32 tokens
-  for (int d = tid; d < D; d += 256) {
-    float mn = s_k[0][d], mx = s_k[0][d];
-    for (int t = 1; t < G; ++t) {
-      mn = fminf(mn, s_k[t][d]);
-      mx = fmaxf(mx, s_k[t][d]);
+  // min / max: K per (channel, half of the tokens), V per (token, group, half of the channels)
+  for (int i = tid; i < 2 * D; i += 256) {
+    const int d = i % D, hf = i / D;
+    float mn = from_bits<DT>(s_k[(16 * hf) * RS + d]), mx = mn;
+#pragma unroll
+    for (int t = 1; t < 16; ++t) {
+      const float x = from_bits<DT>(s_k[(16 * hf + t) * RS + d]);
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
     }
-    float sc, z;
-    kivi_params<DT, BITS>(mn, mx, sc, z);
-    s_ks[d] = bits_dt<DT>(sc);
-    s_kz[d] = bits_dt<DT>(z);
-    for (int t = 0; t < G; ++t) s_ck[t * D + d] = (uint8_t)kivi_code<DT, BITS>(s_k[t][d], sc, z);
+    s_kmn[hf][d] = mn;
+    s_kmx[hf][d] = mx;
   }
-  // V: per token over groups of 32 channels
-  for (int i = tid; i < G * NG; i += 256) {
-    const int t = i / NG, g = i % NG;
-    float mn = s_v[t][g * G], mx = mn;
-    for (int c = 1; c < G; ++c) {
-      mn = fminf(mn, s_v[t][g * G + c]);
-      mx = fmaxf(mx, s_v[t][g * G + c]);
+  for (int i = tid; i < 2 * G * NG; i += 256) {
+    const int tg = i >> 1, hf = i & 1;
+    const int t = tg / NG, g = tg % NG;
+    const uint4* row = reinterpret_cast<const uint4*>(&s_v[t * RS + g * G + 16 * hf]);
+    const uint4 r0 = row[0], r1 = row[1];
+    const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    float mn = from_bits<DT>((uint16_t)w[0]), mx = mn;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float lo = from_bits<DT>((uint16_t)w[c]), hi = from_bits<DT>((uint16_t)(w[c] >> 16));
+      mn = fminf(mn, fminf(lo, hi));
+      mx = fmaxf(mx, fmaxf(lo, hi));
     }
-    float sc, z;
-    kivi_params<DT, BITS>(mn, mx, sc, z);
-    s_vs[g * G + t] = bits_dt<DT>(sc);
-    s_vz[g * G + t] = bits_dt<DT>(z);
-    for (int c = 0; c < G; ++c) s_cv[t * D + g * G + c] = (uint8_t)kivi_code<DT, BITS>(s_v[t][g * G + c], sc, z);
+    s_vmn[hf][tg] = mn;
+    s_vmx[hf][tg] = mx;
   }
   __syncthreads();
   uint8_t* out = P.blocks + (int64_t)b * P.bsb + (int64_t)h * P.bsh + (int64_t)j * kivi_block_bytes(D, BITS);
-  constexpr int VRB = G * BITS / 8;  // V code bytes per channel row
-  constexpr int RKB = D * BITS / 8;  // K code bytes per token row
-  for (int q = tid; q < C; q += 256) {
-    uint32_t wk = 0, wv = 0;
-    const int d = q / VRB, qv = q % VRB;
-#pragma unroll
-    for (int c = 0; c < CPB; ++c) {
-      // K rows and V rows are whole 16-bit words: positions use the row's byte
-      wk |= (uint32_t)s_ck[(q / RKB) * D + kivi_elem<BITS>(q % RKB, c)] << (c * BITS);
-      wv |= (uint32_t)s_cv[kivi_vtok(kivi_elem<BITS>(qv, c)) * D + d] << (c * BITS);
-    }
-    out[q] = (uint8_t)wk;
-    out[C + 4 * D + q] = (uint8_t)wv;
-  }
   uint16_t* meta_k = reinterpret_cast<uint16_t*>(out + C);
   uint16_t* meta_v = reinterpret_cast<uint16_t*>(out + 2 * C + 4 * D);
   for (int d = tid; d < D; d += 256) {
-    meta_k[d] = s_ks[d];
-    meta_k[D + d] = s_kz[d];
+    float sc, z;
+    kivi_params<DT, BITS>(fminf(s_kmn[0][d], s_kmn[1][d]), fmaxf(s_kmx[0][d], s_kmx[1][d]), sc, z);
+    s_kp[d + d / KR] = make_float4(sc, 1.0f / sc, z, kivi_scale_ok(sc));
+    meta_k[d] = bits_dt<DT>(sc);
+    meta_k[D + d] = bits_dt<DT>(z);
   }
-  for (int i = tid; i < G * NG; i += 256) {
-    const int src = (i / G) * G + kivi_vtok(i % G);  // group-major, slot order
-    meta_v[i] = s_vs[src];
-    meta_v[G * NG + i] = s_vz[src];
+  for (int tg = tid; tg < G * NG; tg += 256) {
+    float sc, z;
+    kivi_params<DT, BITS>(fminf(s_vmn[0][tg], s_vmn[1][tg]), fmaxf(s_vmx[0][tg], s_vmx[1][tg]), sc, z);
+    s_vp[tg] = make_float4(sc, 1.0f / sc, z, kivi_scale_ok(sc));
+    const int t = tg / NG, g = tg % NG;
+    meta_v[g * G + kivi_vslot(t)] = bits_dt<DT>(sc);            // group-major, slot order
+    meta_v[G * NG + g * G + kivi_vslot(t)] = bits_dt<DT>(z);
+  }
+  __syncthreads();
+  // K codes: 32 rows x D elements; thread = (token, run of KR consecutive
+  // channels starting at a multiple of 8), KR * BITS bits stored at once
+  constexpr int RKB = D * BITS / 8;          // K code bytes per token row
+  {
+    const int t = tid / (D / KR), e0 = (tid % (D / KR)) * KR;
+    uint64_t acc0 = 0, acc1 = 0;             // up to 128 bits (32 elements x 4 bits)
+    const uint4* row = reinterpret_cast<const uint4*>(&s_k[t * RS + e0]);
+#pragma unroll
+    for (int v8 = 0; v8 < KR / 8; ++v8) {
+      const uint4 r = row[v8];
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int e = e0 + 8 * v8 + i;
+        const float4 pk = s_kp[e + e / KR];
+        const uint16_t xb = (uint16_t)(i & 1 ? w[i >> 1] >> 16 : w[i >> 1]);
+        const uint32_t c = kivi_code_fma<DT, BITS>(from_bits<DT>(xb), pk);
+        const int bit = kivi_bit<BITS>(8 * v8 + i);          // e0 is a multiple of 8
+        if (bit < 64) acc0 |= (uint64_t)c << bit;
+        else acc1 |= (uint64_t)c << (bit - 64);
+      }
+    }
+    uint8_t* dst = out + t * RKB + kivi_bit<BITS>(e0) / 8;
+    constexpr int NB = KR * BITS / 8;        // bytes this thread stores
+    if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)acc0;
+    else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)acc0;
+    else if constexpr (NB == 8) *reinterpret_cast<uint64_t*>(dst) = acc0;
+    else *reinterpret_cast<uint4*>(dst) = make_uint4((uint32_t)acc0, (uint32_t)(acc0 >> 32), (uint32_t)acc1,
+                                                     (uint32_t)(acc1 >> 32));
+  }
+  // V codes: D rows (channels) x 32 slots; thread = (channel, run of VR
+  // consecutive slots starting at a multiple of 8)
+  constexpr int VR = G * D / 256;
+  constexpr int VRB = G * BITS / 8;          // V code bytes per channel row
+  {
+    const int d = tid / (G / VR), s0 = (tid % (G / VR)) * VR;
+    const int g = d / G;
+    uint64_t acc0 = 0, acc1 = 0;
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const int s = s0 + i, t = kivi_vtok(s);
+      const float4 pv = s_vp[t * NG + g];
+      const uint32_t c = kivi_code_fma<DT, BITS>(from_bits<DT>(s_v[t * RS + d]), pv);
+      const int bit = kivi_bit<BITS>(s) - kivi_bit<BITS>(s0);
+      if (bit < 64) acc0 |= (uint64_t)c << bit;
+      else acc1 |= (uint64_t)c << (bit - 64);
+    }
+    uint8_t* dst = out + C + 4 * D + d * VRB + kivi_bit<BITS>(s0) / 8;
+    constexpr int NB = VR * BITS / 8;
+    if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)acc0;
+    else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)acc0;
+    else if constexpr (NB == 8) *reinterpret_cast<uint64_t*>(dst) = acc0;
+    else *reinterpret_cast<uint4*>(dst) = make_uint4((uint32_t)acc0, (uint32_t)(acc0 >> 32), (uint32_t)acc1,
+                                                     (uint32_t)(acc1 >> 32));
   }
 }
 
@@ -273,8 +387,15 @@ extern "C" int halo_kivi_quantize(const void* k, int64_t k_stride_b, int64_t k_s
   const int64_t n = (int64_t)B * H_kv * n_blk;
   if (n == 0) return HALO_OK;
   HALO_CHECK_ARG(n < (1ll << 31), "too many blocks");
+  auto a16 = [](const void* p, int64_t stride_elems) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (stride_elems * 2) % 16 == 0;
+  };
+  const int vec16 = a16(k, k_stride_t) && a16(v, v_stride_t) && (k_stride_b * 2) % 16 == 0 &&
+                    (k_stride_h * 2) % 16 == 0 && (v_stride_b * 2) % 16 == 0 && (v_stride_h * 2) % 16 == 0;
+  HALO_CHECK_ARG((reinterpret_cast<uintptr_t>(blocks) & 15) == 0 && blk_stride_b % 16 == 0 && blk_stride_h % 16 == 0,
+                 "block buffer must be 16-byte aligned");
   KiviQuantParams p{k, k_stride_b, k_stride_h, k_stride_t, v, v_stride_b, v_stride_h, v_stride_t,
-                    H_kv, n_blk, reinterpret_cast<uint8_t*>(blocks), blk_stride_b, blk_stride_h};
+                    H_kv, n_blk, reinterpret_cast<uint8_t*>(blocks), blk_stride_b, blk_stride_h, vec16};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dtype == HALO_F16) {
     if (D == 64) return quant_bits<HALO_F16, 64>(p, bits, (int)n, st);

@@ -157,22 +157,22 @@ def host_tier(torch, layers):
     return tiers
 
 
-def query_trajectory(torch, dev, *, steps, L, H, D, rho, seed):
-    """Per-layer AR(1) query drift in fp32, rounded to bf16:
-    q_0 ~ N(0, 1), q_t = rho q_{t-1} + sqrt(1 - rho^2) e_t.  (steps, L, 1, H, D)."""
+def query_trajectory(torch, dev, *, steps, L, H, D, rho, seed, B=1):
+    """Per-layer (and per-row) AR(1) query drift in fp32, rounded to bf16:
+    q_0 ~ N(0, 1), q_t = rho q_{t-1} + sqrt(1 - rho^2) e_t.  (steps, L, B, H, D)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    q = torch.randn((L, 1, H, D), generator=gen, device=dev)
-    out = torch.empty((steps, L, 1, H, D), device=dev, dtype=torch.bfloat16)
+    q = torch.randn((L, B, H, D), generator=gen, device=dev)
+    out = torch.empty((steps, L, B, H, D), device=dev, dtype=torch.bfloat16)
     c = math.sqrt(max(0.0, 1.0 - rho * rho))
     for t in range(steps):
-        q = rho * q + c * torch.randn((L, 1, H, D), generator=gen, device=dev)
+        q = rho * q + c * torch.randn((L, B, H, D), generator=gen, device=dev)
         out[t] = q.to(torch.bfloat16)
     return out
 
 
 def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, warm_fills=None, segments=4,
-                record=None, lses=None):
+                record=None, lses=None, q_pos=None):
     """Timed decode steps over the staged layers.  A step writes the next
     queries, then runs the layers as ``segments`` consecutive HIP graphs;
     before each segment the fills that landed for its layers are committed,
@@ -183,12 +183,14 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     ``record(t, lo, hi, outs)``, if given, is called right after segment
     [lo, hi) of step t is replayed, on the replay stream (to enqueue copies
     of that step's outputs: the loop itself never synchronises); ``lses``
-    (one (1, H) fp32 tensor per layer) makes the graphs write the LSEs too."""
+    (one (B, H) fp32 tensor per layer) makes the graphs write the LSEs too.
+    ``qtraj`` is (steps, L, B, H, D) for layers of batch B; ``q_pos`` (B,)
+    int64, if given, is every launch's decode position."""
     dev = qtraj.device
     L = len(staged)
-    H, D = staged[0].H, staged[0].D
-    qbuf = torch.empty((L, 1, H, D), device=dev, dtype=torch.bfloat16)
-    outs = [torch.empty((1, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
+    B, H, D = staged[0].B, staged[0].H, staged[0].D
+    qbuf = torch.empty((L, B, H, D), device=dev, dtype=torch.bfloat16)
+    outs = [torch.empty((B, H, D), device=dev, dtype=torch.bfloat16) for _ in range(L)]
     lse_of = (lambda li: lses[li]) if lses is not None else (lambda li: None)
     bounds = [(g * L // segments, (g + 1) * L // segments) for g in range(segments)]
     s = torch.cuda.Stream()
@@ -198,13 +200,13 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     with torch.cuda.stream(s):
         qbuf.copy_(qtraj[0])
         for li in range(L):
-            staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li))
+            staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li), q_pos=q_pos)
         torch.cuda.synchronize()
         for lo, hi in bounds:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
                 for li in range(lo, hi):
-                    staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li))
+                    staged[li].step(qbuf[li], scale=scale, out=outs[li], lse=lse_of(li), q_pos=q_pos)
             graphs.append(g)
         torch.cuda.synchronize()
         t0 = 0.0

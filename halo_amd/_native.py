@@ -67,9 +67,10 @@ class StagingDesc(ctypes.Structure):
     _fields_ = [
         ("n_layers", _i32), ("n_cold", _i32), ("n_slots", _i32), ("top_k", _i32), ("keep", _i32),
         ("max_inflight", _i32), ("spare", _i32), ("ring", _i32),
-        ("write_allocate", _i32), ("fill_mode", _i32), ("track_busy", _i32), ("pad", _i32),
+        ("write_allocate", _i32), ("fill_mode", _i32), ("track_busy", _i32), ("sels_per_layer", _i32),
         ("residency", _c_void_p), ("feedback", _c_void_p), ("slot_addr", _c_void_p), ("chunk_addr", _c_void_p),
-        ("chunk_nbytes", _c_void_p), ("copy_stream", _c_void_p), ("urgent_stream", _c_void_p),
+        ("chunk_nbytes", _c_void_p), ("n_cold_per_unit", _c_void_p), ("copy_stream", _c_void_p),
+        ("urgent_stream", _c_void_p),
     ]
 
 

@@ -7,6 +7,10 @@
 // this file only enqueues work on HIP streams (hipMemcpyAsync, events, the
 // int32 store kernel) and keeps the host mirror of the cache.
 //
+// The unit of the cache is a selection: one per layer, or one per batch row
+// of a layer with per-row selection (B selections per layer, each over its
+// own row's cold chunks with its own slots).  Unit u = layer * B + row.
+//
 // Reference policy: HALORefetcher.predict_hot / schedule / _issue / wait
 // (halo/refetcher.py:38-114): the next hot set is the top (hot + lookahead)
 // by the last score, and what is missing is fetched on a side stream.  Here
@@ -38,7 +42,7 @@ namespace {
 enum : int8_t { kFree = 0, kFilling = 1, kReady = 2, kReserved = 4 };
 
 struct Pending {
-  int layer, chunk, slot;
+  int unit, chunk, slot;
   bool urgent;
 };
 
@@ -46,30 +50,39 @@ struct Pending {
 }  // namespace halo
 
 struct halo_staging {
-  int L = 0, n = 0, S = 0, k = 0, keep = 0, max_inflight = 0, spare = 0, ring_n = 0, W = 0;
+  int L = 0, B = 1, U = 0, n = 0, S = 0, k = 0, keep = 0, max_inflight = 0, spare = 0, ring_n = 0, W = 0;
   bool wa = false, kernel_fills = false, track_busy = false;
-  int32_t* dev_i32 = nullptr;  // residency (L * n) then the write-allocate slot per layer (L)
+  int32_t* dev_i32 = nullptr;  // residency (U * n) then the write-allocate slot per layer (L)
   const float* feedback = nullptr;
   hipStream_t copy = nullptr, urgent = nullptr;
-  std::vector<uint64_t> dst, src;       // (L, S, 2) slot K/V, (L, n, 2) chunk K/V addresses
-  std::vector<int64_t> nbytes;          // (L, n) bytes per K (or V) tensor
+  std::vector<uint64_t> dst, src;       // (U, S, 2) slot K/V, (U, n, 2) chunk K/V addresses
+  std::vector<int64_t> nbytes;          // (U, n) bytes per K (or V) tensor
+  std::vector<int32_t> ncold;           // (U) cold chunks of each unit (<= n)
   std::vector<float*> ring;             // pinned (L, W) rows per ring entry
   std::vector<hipEvent_t> ring_ev;
   std::vector<std::pair<int, int>> ring_rows;
   int64_t queued = 0, seen = 0;
   std::vector<int64_t> slot_of, holds, last_rank, wa_slot, launches, processed;
   std::vector<int8_t> state;
-  std::vector<hipEvent_t> fill_ev;      // (L, S): the event of the slot's fill in flight
+  std::vector<hipEvent_t> fill_ev;      // (U, S): the event of the slot's fill in flight
   std::vector<halo::Pending> pending;
   halo_staging_stats st{};
   // scratch reused across calls
   std::vector<int64_t> idx_buf;
   std::vector<int32_t> val_buf;
 
-  int64_t& slot_of_at(int li, int c) { return slot_of[(size_t)li * n + c]; }
-  int8_t& state_at(int li, int s) { return state[(size_t)li * S + s]; }
-  int64_t& holds_at(int li, int s) { return holds[(size_t)li * S + s]; }
-  int64_t chunk_bytes(int li, int c) const { return 2 * nbytes[(size_t)li * n + c]; }
+  int64_t& slot_of_at(int u, int c) { return slot_of[(size_t)u * n + c]; }
+  int8_t& state_at(int u, int s) { return state[(size_t)u * S + s]; }
+  int64_t& holds_at(int u, int s) { return holds[(size_t)u * S + s]; }
+  int64_t chunk_bytes(int u, int c) const { return 2 * nbytes[(size_t)u * n + c]; }
+  // feedback of layer li within a row block: scores (B, n) | picks (B, k) | residency used (B, k)
+  const float* fb_scores(const float* layer_row, int r) const { return layer_row + (size_t)r * n; }
+  const int32_t* fb_idx(const float* layer_row, int r) const {
+    return reinterpret_cast<const int32_t*>(layer_row + (size_t)B * n + (size_t)r * k);
+  }
+  const int32_t* fb_res(const float* layer_row, int r) const {
+    return reinterpret_cast<const int32_t*>(layer_row + (size_t)B * n + (size_t)B * k + (size_t)r * k);
+  }
 };
 
 namespace halo {
@@ -86,7 +99,7 @@ bool stream_busy(hipStream_t s) {
 
 int store(halo_staging* h, hipStream_t compute) {
   if (h->idx_buf.empty()) return HALO_OK;
-  const int rc = halo_store_i32(h->dev_i32, (int64_t)h->L * h->n + h->L, h->idx_buf.data(), h->val_buf.data(),
+  const int rc = halo_store_i32(h->dev_i32, (int64_t)h->U * h->n + h->L, h->idx_buf.data(), h->val_buf.data(),
                                 (int)h->idx_buf.size(), compute);
   h->idx_buf.clear();
   h->val_buf.clear();
@@ -94,7 +107,8 @@ int store(halo_staging* h, hipStream_t compute) {
 }
 
 // Give every empty write-allocate reservation a free slot (highest index
-// first, away from the fills, which take the lowest).
+// first, away from the fills, which take the lowest).  One selection per
+// layer only (B == 1: unit == layer).
 void reserve_wa(halo_staging* h) {
   if (!h->wa) return;
   for (int li = 0; li < h->L; ++li) {
@@ -111,45 +125,49 @@ void reserve_wa(halo_staging* h) {
   }
 }
 
-// Hit/miss accounting of the feedback rows of layers [lo, hi) and the
-// commits of slots the kernel wrote (write-allocate).
+// Hit/miss accounting of the feedback rows of layers [lo, hi) (`fb` points
+// at layer lo's row) and the commits of slots the kernel wrote
+// (write-allocate).
 int account(halo_staging* h, const float* fb, int lo, int hi, hipStream_t compute) {
   const int n = h->n, k = h->k;
   for (int li = lo; li < hi; ++li) h->processed[li] += 1;
   bool committed = false;
   for (int li = lo; li < hi; ++li) {
     const float* row = fb + (size_t)(li - lo) * h->W;
-    const int32_t* idx = reinterpret_cast<const int32_t*>(row + n);
-    const int32_t* res = reinterpret_cast<const int32_t*>(row + n + k);
-    for (int j = 0; j < k; ++j) {
-      const int c = idx[j];
-      if (c < 0 || c >= n) continue;
-      const int r = res[j];
-      if (r >= 0) {
-        h->st.hits += 1;
-        continue;
-      }
-      h->st.misses += 1;
-      h->st.miss_bytes += h->chunk_bytes(li, c);
-      if (h->last_rank[(size_t)li * n + c] < h->keep) h->st.misses_predicted += 1;
-      if (h->wa && r <= -2) {
-        const int w = -2 - r;
-        int q = -1;
-        for (int t = 0; t < 2; ++t)
-          if (h->wa_slot[(size_t)li * 2 + t] == w) q = t;
-        if (q < 0) continue;  // not a current reservation: nothing to commit
-        if (h->slot_of_at(li, c) >= 0) {
-          h->st.wa_dups += 1;  // staged or filling elsewhere meanwhile: keep the reservation
+    for (int r = 0; r < h->B; ++r) {
+      const int u = li * h->B + r;
+      const int32_t* idx = h->fb_idx(row, r);
+      const int32_t* res = h->fb_res(row, r);
+      for (int j = 0; j < k; ++j) {
+        const int c = idx[j];
+        if (c < 0 || c >= h->ncold[u]) continue;
+        const int rr = res[j];
+        if (rr >= 0) {
+          h->st.hits += 1;
           continue;
         }
-        h->state_at(li, w) = kReady;
-        h->holds_at(li, w) = c;
-        h->slot_of_at(li, c) = w;
-        h->idx_buf.push_back((int64_t)li * n + c);
-        h->val_buf.push_back(w);
-        h->wa_slot[(size_t)li * 2 + q] = -1;
-        h->st.wa_commits += 1;
-        committed = true;
+        h->st.misses += 1;
+        h->st.miss_bytes += h->chunk_bytes(u, c);
+        if (h->last_rank[(size_t)u * n + c] < h->keep) h->st.misses_predicted += 1;
+        if (h->wa && rr <= -2) {
+          const int w = -2 - rr;
+          int q = -1;
+          for (int t = 0; t < 2; ++t)
+            if (h->wa_slot[(size_t)li * 2 + t] == w) q = t;
+          if (q < 0) continue;  // not a current reservation: nothing to commit
+          if (h->slot_of_at(u, c) >= 0) {
+            h->st.wa_dups += 1;  // staged or filling elsewhere meanwhile: keep the reservation
+            continue;
+          }
+          h->state_at(u, w) = kReady;
+          h->holds_at(u, w) = c;
+          h->slot_of_at(u, c) = w;
+          h->idx_buf.push_back((int64_t)u * n + c);
+          h->val_buf.push_back(w);
+          h->wa_slot[(size_t)li * 2 + q] = -1;
+          h->st.wa_commits += 1;
+          committed = true;
+        }
       }
     }
   }
@@ -164,8 +182,8 @@ int account(halo_staging* h, const float* fb, int lo, int hi, hipStream_t comput
 
 int issue(halo_staging* h, const Pending& p) {
   hipStream_t s = (p.urgent && h->urgent != nullptr) ? h->urgent : h->copy;
-  const size_t sk = ((size_t)p.layer * h->S + p.slot) * 2, ck = ((size_t)p.layer * h->n + p.chunk) * 2;
-  const int64_t nb = h->nbytes[(size_t)p.layer * h->n + p.chunk];
+  const size_t sk = ((size_t)p.unit * h->S + p.slot) * 2, ck = ((size_t)p.unit * h->n + p.chunk) * 2;
+  const int64_t nb = h->nbytes[(size_t)p.unit * h->n + p.chunk];
   halo_fill f;
   f.dst_k = reinterpret_cast<void*>(h->dst[sk]);
   f.dst_v = reinterpret_cast<void*>(h->dst[sk + 1]);
@@ -179,95 +197,99 @@ int issue(halo_staging* h, const Pending& p) {
   }
   const int rc = h->kernel_fills ? halo_stage_fills_read(&f, 1, s) : halo_stage_fills(&f, 1, s);
   if (rc != HALO_OK) return rc;
-  HALO_CHECK_HIP(hipEventRecord(h->fill_ev[(size_t)p.layer * h->S + p.slot], s));
+  HALO_CHECK_HIP(hipEventRecord(h->fill_ev[(size_t)p.unit * h->S + p.slot], s));
   h->pending.push_back(p);
   return HALO_OK;
 }
 
-// Plan evictions and fills for the layers whose feedback was just processed
-// (scores rows in `sc`, one per layer of `layers`).
-int plan(halo_staging* h, const std::vector<int>& layers, const std::vector<float>& sc, hipStream_t compute) {
+// Plan evictions and fills for the units whose feedback was just processed
+// (one score row of n per unit in `sc`, in the order of `units`).
+int plan(halo_staging* h, const std::vector<int>& units, const std::vector<float>& sc, hipStream_t compute) {
   const int n = h->n, S = h->S;
   std::vector<int> order(n);
-  std::vector<int64_t> rank((size_t)layers.size() * n);
+  std::vector<int64_t> rank((size_t)units.size() * n);
   struct Miss {
     int64_t rank;
-    int layer, chunk, row;
+    int unit, chunk, row;
   };
   std::vector<Miss> missing;
-  for (size_t i = 0; i < layers.size(); ++i) {
+  for (size_t i = 0; i < units.size(); ++i) {
+    const int u = units[i], nu = h->ncold[u];
     const float* s = sc.data() + i * n;
-    auto key = [&](int c) { return std::isnan(s[c]) ? -INFINITY : s[c]; };
+    auto key = [&](int c) { return (c >= nu || std::isnan(s[c])) ? -INFINITY : s[c]; };
     std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) > key(b); });
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      const float ka = key(a), kb = key(b);
+      return ka != kb ? ka > kb : (a < nu) > (b < nu);   // chunks past the unit's count rank last
+    });
     int64_t* rk = rank.data() + i * n;
     for (int r = 0; r < n; ++r) rk[order[r]] = r;
-    const int li = layers[i];
-    std::copy(rk, rk + n, h->last_rank.begin() + (size_t)li * n);
-    for (int c = 0; c < n; ++c)
-      if (rk[c] < h->keep && h->slot_of_at(li, c) < 0) missing.push_back({rk[c], li, c, (int)i});
+    for (int c = nu; c < n; ++c) rk[c] = n;                 // never kept
+    std::copy(rk, rk + n, h->last_rank.begin() + (size_t)u * n);
+    for (int c = 0; c < nu; ++c)
+      if (rk[c] < h->keep && h->slot_of_at(u, c) < 0) missing.push_back({rk[c], u, c, (int)i});
   }
   bool evicted = false;
-  auto evict = [&](int li, int s) {
-    const int64_t c = h->holds_at(li, s);
-    h->idx_buf.push_back((int64_t)li * n + c);
+  auto evict = [&](int u, int s) {
+    const int64_t c = h->holds_at(u, s);
+    h->idx_buf.push_back((int64_t)u * n + c);
     h->val_buf.push_back(-1);
-    h->slot_of_at(li, (int)c) = -1;
-    h->state_at(li, s) = kFree;
-    h->holds_at(li, s) = -1;
+    h->slot_of_at(u, (int)c) = -1;
+    h->state_at(u, s) = kFree;
+    h->holds_at(u, s) = -1;
     evicted = true;
   };
-  // keep `spare` slots per layer free, evicting the worst-ranked staged
+  // keep `spare` slots per unit free, evicting the worst-ranked staged
   // chunks outside the kept set
   if (h->spare > 0) {
-    for (size_t i = 0; i < layers.size(); ++i) {
-      const int li = layers[i];
+    for (size_t i = 0; i < units.size(); ++i) {
+      const int u = units[i];
       const int64_t* rk = rank.data() + i * n;
       int free_n = 0;
       std::vector<int> ready;
       for (int s = 0; s < S; ++s) {
-        if (h->state_at(li, s) == kFree) ++free_n;
-        if (h->state_at(li, s) == kReady) ready.push_back(s);
+        if (h->state_at(u, s) == kFree) ++free_n;
+        if (h->state_at(u, s) == kReady) ready.push_back(s);
       }
       int short_n = h->spare - free_n;
       std::stable_sort(ready.begin(), ready.end(),
-                       [&](int a, int b) { return rk[h->holds_at(li, a)] > rk[h->holds_at(li, b)]; });
+                       [&](int a, int b) { return rk[h->holds_at(u, a)] > rk[h->holds_at(u, b)]; });
       for (size_t j = 0; j < ready.size() && short_n > 0; ++j, --short_n) {
-        if (rk[h->holds_at(li, ready[j])] < h->keep) break;
-        evict(li, ready[j]);
+        if (rk[h->holds_at(u, ready[j])] < h->keep) break;
+        evict(u, ready[j]);
       }
     }
   }
-  // best ranks first, then layer order
+  // best ranks first, then unit order
   std::stable_sort(missing.begin(), missing.end(), [](const Miss& a, const Miss& b) {
-    return a.rank != b.rank ? a.rank < b.rank : a.layer < b.layer;
+    return a.rank != b.rank ? a.rank < b.rank : a.unit < b.unit;
   });
   int budget = h->max_inflight - (int)h->pending.size();
   std::vector<Pending> fills;
   for (const Miss& m : missing) {
     if (budget <= 0) break;
-    const int li = m.layer;
+    const int u = m.unit;
     const int64_t* rk = rank.data() + (size_t)m.row * n;
     int slot = -1;
     for (int s = 0; s < S && slot < 0; ++s)
-      if (h->state_at(li, s) == kFree) slot = s;
+      if (h->state_at(u, s) == kFree) slot = s;
     if (slot < 0) {
       // no free slot: take the one of the worst-ranked staged chunk outside
       // the kept set, if there is one
       int worst = -1;
       for (int s = 0; s < S; ++s)
-        if (h->state_at(li, s) == kReady && (worst < 0 || rk[h->holds_at(li, s)] > rk[h->holds_at(li, worst)]))
+        if (h->state_at(u, s) == kReady && (worst < 0 || rk[h->holds_at(u, s)] > rk[h->holds_at(u, worst)]))
           worst = s;
-      if (worst < 0 || rk[h->holds_at(li, worst)] < h->keep) continue;
-      evict(li, worst);
+      if (worst < 0 || rk[h->holds_at(u, worst)] < h->keep) continue;
+      evict(u, worst);
       slot = worst;
     }
-    h->state_at(li, slot) = kFilling;
-    h->holds_at(li, slot) = m.chunk;
-    h->slot_of_at(li, m.chunk) = slot;
+    h->state_at(u, slot) = kFilling;
+    h->holds_at(u, slot) = m.chunk;
+    h->slot_of_at(u, m.chunk) = slot;
     h->st.fills += 1;
-    h->st.fill_bytes += h->chunk_bytes(li, m.chunk);
-    fills.push_back({li, m.chunk, slot, m.rank < h->k});
+    h->st.fill_bytes += h->chunk_bytes(u, m.chunk);
+    fills.push_back({u, m.chunk, slot, m.rank < h->k});
     --budget;
   }
   if (evicted) {
@@ -293,13 +315,17 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
   HALO_CHECK_ARG(d != nullptr && out != nullptr, "null pointer argument");
   *out = nullptr;
   HALO_CHECK_ARG(d->n_layers > 0 && d->n_cold > 0 && d->top_k > 0, "empty staging cache");
+  HALO_CHECK_ARG(d->sels_per_layer >= 1, "sels_per_layer must be >= 1");
   HALO_CHECK_ARG(d->n_slots >= 1 && d->n_slots <= 64, "n_slots must be in [1, 64]");
   HALO_CHECK_ARG(d->top_k <= d->keep && d->keep <= d->n_slots, "keep must be in [top_k, n_slots]");
   HALO_CHECK_ARG(d->ring >= 2 && d->max_inflight >= 0 && d->spare >= 0, "bad ring / max_inflight / spare");
   HALO_CHECK_ARG(d->residency && d->feedback && d->slot_addr && d->chunk_addr && d->chunk_nbytes && d->copy_stream,
                  "null pointer in the staging description");
+  HALO_CHECK_ARG(!(d->write_allocate && d->sels_per_layer > 1), "write-allocate needs one selection per layer");
   auto h = new halo_staging();
   h->L = d->n_layers;
+  h->B = d->sels_per_layer;
+  h->U = h->L * h->B;
   h->n = d->n_cold;
   h->S = d->n_slots;
   h->k = d->top_k;
@@ -307,7 +333,7 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
   h->max_inflight = d->max_inflight;
   h->spare = d->spare;
   h->ring_n = d->ring;
-  h->W = d->n_cold + 2 * d->top_k;
+  h->W = h->B * (d->n_cold + 2 * d->top_k);
   h->wa = d->write_allocate != 0;
   h->kernel_fills = d->fill_mode == 1;
   h->track_busy = d->track_busy != 0;
@@ -315,18 +341,24 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
   h->feedback = d->feedback;
   h->copy = static_cast<hipStream_t>(d->copy_stream);
   h->urgent = static_cast<hipStream_t>(d->urgent_stream);
-  const size_t L = h->L, n = h->n, S = h->S;
-  h->dst.assign(d->slot_addr, d->slot_addr + L * S * 2);
-  h->src.assign(d->chunk_addr, d->chunk_addr + L * n * 2);
-  h->nbytes.assign(d->chunk_nbytes, d->chunk_nbytes + L * n);
-  h->slot_of.assign(L * n, -1);
-  h->last_rank.assign(L * n, (int64_t)n);
-  h->holds.assign(L * S, -1);
-  h->state.assign(L * S, kFree);
+  const size_t L = h->L, U = h->U, n = h->n, S = h->S;
+  h->dst.assign(d->slot_addr, d->slot_addr + U * S * 2);
+  h->src.assign(d->chunk_addr, d->chunk_addr + U * n * 2);
+  h->nbytes.assign(d->chunk_nbytes, d->chunk_nbytes + U * n);
+  if (d->n_cold_per_unit != nullptr) {
+    h->ncold.assign(d->n_cold_per_unit, d->n_cold_per_unit + U);
+    for (auto& c : h->ncold) c = std::max(0, std::min(c, h->n));
+  } else {
+    h->ncold.assign(U, h->n);
+  }
+  h->slot_of.assign(U * n, -1);
+  h->last_rank.assign(U * n, (int64_t)n);
+  h->holds.assign(U * S, -1);
+  h->state.assign(U * S, kFree);
   h->wa_slot.assign(L * 2, -1);
   h->launches.assign(L, 0);
   h->processed.assign(L, 0);
-  h->fill_ev.assign(L * S, nullptr);
+  h->fill_ev.assign(U * S, nullptr);
   h->ring.assign(h->ring_n, nullptr);
   h->ring_ev.assign(h->ring_n, nullptr);
   h->ring_rows.assign(h->ring_n, {0, 0});
@@ -371,13 +403,14 @@ extern "C" int halo_staging_destroy(halo_staging* h) {
 extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream) {
   HALO_CHECK_ARG(h != nullptr && 0 <= lo && lo <= hi && hi <= h->L, "bad staging segment");
   hipStream_t compute = static_cast<hipStream_t>(stream);
+  const int ulo = lo * h->B, uhi = hi * h->B;
   std::vector<Pending> rest;
   rest.reserve(h->pending.size());
   bool any = false;
   for (const Pending& p : h->pending) {
     bool take = false;
-    if (lo <= p.layer && p.layer < hi) {
-      hipEvent_t ev = h->fill_ev[(size_t)p.layer * h->S + p.slot];
+    if (ulo <= p.unit && p.unit < uhi) {
+      hipEvent_t ev = h->fill_ev[(size_t)p.unit * h->S + p.slot];
       if (p.urgent) {
         HALO_CHECK_HIP(hipStreamWaitEvent(compute, ev, 0));
         take = true;
@@ -393,8 +426,8 @@ extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream
       }
     }
     if (take) {
-      h->state_at(p.layer, p.slot) = kReady;
-      h->idx_buf.push_back((int64_t)p.layer * h->n + p.chunk);
+      h->state_at(p.unit, p.slot) = kReady;
+      h->idx_buf.push_back((int64_t)p.unit * h->n + p.chunk);
       h->val_buf.push_back(p.slot);
       any = true;
     } else {
@@ -403,7 +436,7 @@ extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream
   }
   h->pending.swap(rest);
   if (h->wa) {
-    const int64_t base = (int64_t)h->L * h->n;
+    const int64_t base = (int64_t)h->U * h->n;
     for (int li = lo; li < hi; ++li) {
       // a reservation is named again only after the feedback of the launch
       // that last named it (two launches back) was processed
@@ -438,7 +471,7 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
   HALO_CHECK_ARG(h != nullptr && lag >= 0, "bad staging service call");
   hipStream_t compute = static_cast<hipStream_t>(stream);
   const int64_t target = h->queued - lag;
-  std::vector<int> layers;
+  std::vector<int> units;
   std::vector<float> scores;
   while (h->seen < h->queued) {
     const int r = (int)(h->seen % h->ring_n);
@@ -457,14 +490,17 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
     const int rc = account(h, fb, lo, hi, compute);
     if (rc != HALO_OK) return rc;
     for (int li = lo; li < hi; ++li) {
-      layers.push_back(li);
       const float* row = fb + (size_t)(li - lo) * h->W;
-      scores.insert(scores.end(), row, row + h->n);
+      for (int r = 0; r < h->B; ++r) {
+        units.push_back(li * h->B + r);
+        const float* sr = h->fb_scores(row, r);
+        scores.insert(scores.end(), sr, sr + h->n);
+      }
     }
     h->seen += 1;
   }
-  if (layers.empty()) return HALO_OK;
-  return plan(h, layers, scores, compute);
+  if (units.empty()) return HALO_OK;
+  return plan(h, units, scores, compute);
 }
 
 extern "C" int halo_staging_reset(halo_staging* h) {

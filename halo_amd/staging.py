@@ -80,11 +80,13 @@ class ColdStaging:
 
     ``layers``: ``TieredDecodeLayer`` objects with the fused in-kernel
     selection over cold chunks held as contiguous pinned host tensors, the
-    same number of cold chunks each.  ``n_slots`` HBM slots per layer (each
-    the size of the layer's widest cold chunk); ``keep`` best-scoring chunks
-    per layer are staged (default n_slots - 2); ``spare`` slots per layer are
-    kept free (staged chunks outside the kept set are evicted worst rank
-    first to keep them); ``max_inflight`` bounds the copies in flight on the
+    same number of cold chunks each -- or ``RaggedTieredDecodeLayer``
+    objects (per-row selection), where every batch row is a unit of its own:
+    its own cold chunks (ragged counts), slots and policy.  ``n_slots`` HBM
+    slots per unit (each the size of the unit's widest cold chunk); ``keep``
+    best-scoring chunks per unit are staged (default n_slots - 2); ``spare``
+    slots per unit are kept free (staged chunks outside the kept set are
+    evicted worst rank first to keep them); ``max_inflight`` bounds the copies in flight on the
     link; ``write_allocate`` reserves two slots per layer for missed chunks
     the kernel writes while reading them (16-bit layers with one selection
     per launch; ignored otherwise).  It pays when the selection moves fast
@@ -103,8 +105,25 @@ class ColdStaging:
         self.layers = list(layers)
         lay0 = self.layers[0]
         self.device = lay0.plan.descs.device
-        self.n_cold = len(lay0.cold)
         self.top_k = lay0.top_k
+        for li, lay in enumerate(self.layers):
+            if getattr(lay, "select_cfg", None) is None or not getattr(lay, "fused", True):
+                raise AssertionError(f"layer {li}: staging needs the fused in-kernel selection")
+        # the cache's unit is a selection: the layer's one selection, or one
+        # per batch row of a layer with per-row selection (ragged batches)
+        self.per_row = bool(lay0.select_cfg.per_row)
+        self.sels = lay0.B if self.per_row else 1
+        units = []                          # cold chunks of each unit, unit = layer * sels + row
+        for li, lay in enumerate(self.layers):
+            if bool(lay.select_cfg.per_row) != self.per_row or (lay.B if self.per_row else 1) != self.sels \
+                    or lay.top_k != self.top_k:
+                raise AssertionError("every layer must have the same selections per layer and top_k")
+            units += [list(cold) for _, cold in lay.rows] if self.per_row else [list(lay.cold)]
+        self.n_cold = int(lay0.select_cfg.catalog_stride) if self.per_row else len(lay0.cold)
+        if any(len(u) > self.n_cold for u in units) or any(
+                int(lay.select_cfg.catalog_stride if self.per_row else len(lay.cold)) != self.n_cold
+                for lay in self.layers):
+            raise AssertionError("every layer must have the same number of cold chunks (catalog stride)")
         if not 1 <= n_slots <= 64:
             raise AssertionError("n_slots must be in [1, 64]")
         self.n_slots = int(n_slots)
@@ -116,71 +135,86 @@ class ColdStaging:
         self.fill_mode = fill_mode
         self.spare = int(spare)
         self._max_inflight = int(max_inflight)
-        L, n, k = len(self.layers), self.n_cold, self.top_k
-        for li, lay in enumerate(self.layers):
-            if not lay.fused or lay.select_cfg is None:
-                raise AssertionError(f"layer {li}: staging needs the fused in-kernel selection")
-            if len(lay.cold) != n or lay.top_k != k:
-                raise AssertionError("every layer must have the same number of cold chunks and top_k")
-            for c in lay.cold:
+        for ui, cold in enumerate(units):
+            for c in cold:
                 if c.k.device.type != "cpu" or not c.k.is_pinned() or not c.k.is_contiguous() \
                         or not c.v.is_contiguous():
-                    raise AssertionError(f"layer {li}: cold chunks must be contiguous pinned host tensors")
+                    raise AssertionError(f"layer {ui // self.sels}: cold chunks must be contiguous pinned host "
+                                         f"tensors")
+        L, n, k, Bs = len(self.layers), self.n_cold, self.top_k, self.sels
+        U = L * Bs
         dev = self.device
-        # residency (L, n) and the per-layer write-allocate slot (L) in one
+        # residency (U, n) and the per-layer write-allocate slot (L) in one
         # device buffer, so one store kernel updates both
-        self._dev_i32 = torch.full((L * n + L,), -1, dtype=torch.int32, device=dev)
-        self.residency = self._dev_i32[:L * n].view(L, n)
-        self.alloc = self._dev_i32[L * n:]
-        self.write_allocate = bool(write_allocate) and self.n_slots >= self.top_k + 2 and all(
-            lay.dtype != torch.float32 and not lay.select_cfg.per_row for lay in self.layers)
-        # one feedback row per layer: scores (fp32) | picks (int32) | residency used (int32)
-        W = n + 2 * k
+        self._dev_i32 = torch.full((U * n + L,), -1, dtype=torch.int32, device=dev)
+        self.residency = self._dev_i32[:U * n].view(L, Bs * n)
+        self.alloc = self._dev_i32[U * n:]
+        self.write_allocate = bool(write_allocate) and not self.per_row and self.n_slots >= self.top_k + 2 and all(
+            lay.dtype != torch.float32 for lay in self.layers)
+        # one feedback row per layer, as the selection writes it:
+        # scores (sels, n) fp32 | picks (sels, k) int32 | residency used (sels, k) int32
+        W = Bs * (n + 2 * k)
         self.feedback = torch.zeros((L, W), dtype=torch.float32, device=dev)
-        self.scores = self.feedback[:, :n]
-        self.idx = self.feedback[:, n:n + k].view(torch.int32)
-        self.res_out = self.feedback[:, n + k:].view(torch.int32)
-        self.idx.fill_(-1)
-        self.res_out.fill_(-1)
-        self.chunk_bytes = np.zeros((L, n), dtype=np.int64)
+        scores = self.feedback[:, :Bs * n]
+        idx = self.feedback[:, Bs * n:Bs * (n + k)].view(torch.int32)
+        res = self.feedback[:, Bs * (n + k):].view(torch.int32)
+        idx.fill_(-1)
+        res.fill_(-1)
+        if self.per_row:
+            self.scores, self.idx, self.res_out = scores.view(L, Bs, n), idx.view(L, Bs, k), res.view(L, Bs, k)
+        else:
+            self.scores, self.idx, self.res_out = scores, idx, res
+        self.chunk_bytes = np.zeros((U, n), dtype=np.int64)
         self._slot_k, self._slot_v, self._slot_cat = [], [], []
-        # slot (layer, s) K/V addresses, cold chunk (layer, c) K/V addresses, bytes per tensor
-        dst = np.zeros((L, self.n_slots, 2), dtype=np.uint64)
-        src = np.zeros((L, n, 2), dtype=np.uint64)
-        nbytes = np.zeros((L, n), dtype=np.int64)
+        # slot (unit, s) K/V addresses, cold chunk (unit, c) K/V addresses, bytes per tensor
+        dst = np.zeros((U, self.n_slots, 2), dtype=np.uint64)
+        src = np.zeros((U, n, 2), dtype=np.uint64)
+        nbytes = np.zeros((U, n), dtype=np.int64)
+        ncold = np.asarray([len(u) for u in units], dtype=np.int32)
         for li, lay in enumerate(self.layers):
-            shape = max((tuple(c.k.shape) for c in lay.cold), key=lambda s: s[-2])
-            # a slot's K rows and V rows are adjacent, so a cold chunk laid out
-            # the same way on the host is filled by one copy
-            skv = torch.empty((self.n_slots, 2) + shape, dtype=lay.dtype, device=dev)
-            sk, sv = skv[:, 0], skv[:, 1]
-            # slot descriptors never change: they give the addresses and strides
-            # a staged chunk is read through; its rows, start and flags come
-            # from the chunk's own catalog entry
-            sdesc, _ = pack_descs([ChunkRef(sk[s], sv[s], 0, False) for s in range(self.n_slots)],
-                                  B=lay.B, H_kv=lay.H_kv, D=lay.D, dtype=lay.dtype)
-            self._slot_k.append(sk)
-            self._slot_v.append(sv)
-            self._slot_cat.append(descs_to_device(sdesc, dev))
-            for j in range(self.n_slots):
-                dst[li, j] = (sk[j].data_ptr(), sv[j].data_ptr())
-            for j, c in enumerate(lay.cold):
-                if tuple(c.k.shape) != tuple(sk.shape[1:]):
-                    raise AssertionError(f"layer {li} cold chunk {j}: shape {tuple(c.k.shape)} differs from the "
-                                         f"layer's other cold chunks {tuple(sk.shape[1:])}")
-                if fill_mode == "kernel":   # the copy kernel reads the pinned chunk in place
-                    src[li, j] = (nat.host_device_pointer(c.k.data_ptr()), nat.host_device_pointer(c.v.data_ptr()))
+            sdescs = []
+            for r in range(Bs):
+                ui = li * Bs + r
+                cold = units[ui]
+                if cold:
+                    shape = max((tuple(c.k.shape) for c in cold), key=lambda sh: sh[-2])
+                elif self.per_row:
+                    shape = (lay.H_kv, 1, lay.D)
                 else:
-                    src[li, j] = (c.k.data_ptr(), c.v.data_ptr())
-                nbytes[li, j] = c.k.numel() * c.k.element_size()
-            self.chunk_bytes[li] = 2 * nbytes[li]
+                    raise AssertionError(f"layer {li} has no cold chunks")
+                # a slot's K rows and V rows are adjacent, so a cold chunk laid
+                # out the same way on the host is filled by one copy
+                skv = torch.empty((self.n_slots, 2) + shape, dtype=lay.dtype, device=dev)
+                sk, sv = skv[:, 0], skv[:, 1]
+                # slot descriptors never change: they give the addresses and
+                # strides a staged chunk is read through; its rows, start, flags
+                # and batch come from the chunk's own catalog entry
+                d, _ = pack_descs([ChunkRef(sk[s], sv[s], 0, False, r if self.per_row else -1)
+                                   for s in range(self.n_slots)], B=lay.B, H_kv=lay.H_kv, D=lay.D, dtype=lay.dtype)
+                sdescs.append(d)
+                self._slot_k.append(sk)
+                self._slot_v.append(sv)
+                for j in range(self.n_slots):
+                    dst[ui, j] = (sk[j].data_ptr(), sv[j].data_ptr())
+                for j, c in enumerate(cold):
+                    if tuple(c.k.shape) != tuple(sk.shape[1:]):
+                        raise AssertionError(f"layer {li} cold chunk {j}: shape {tuple(c.k.shape)} differs from the "
+                                             f"unit's other cold chunks {tuple(sk.shape[1:])}")
+                    if fill_mode == "kernel":   # the copy kernel reads the pinned chunk in place
+                        src[ui, j] = (nat.host_device_pointer(c.k.data_ptr()),
+                                      nat.host_device_pointer(c.v.data_ptr()))
+                    else:
+                        src[ui, j] = (c.k.data_ptr(), c.v.data_ptr())
+                    nbytes[ui, j] = c.k.numel() * c.k.element_size()
+                self.chunk_bytes[ui] = 2 * nbytes[ui]
+            self._slot_cat.append(descs_to_device(np.concatenate(sdescs), dev))
             cfg = lay.select_cfg
             cfg.n_slots = self.n_slots
             cfg.slot_catalog = self._slot_cat[li].data_ptr()
             cfg.residency = self.residency[li].data_ptr()
-            cfg.res_out = self.res_out[li].data_ptr()
-            cfg.score_out = self.scores[li].data_ptr()
-            cfg.idx_out = self.idx[li].data_ptr()
+            cfg.res_out = res[li].data_ptr()
+            cfg.score_out = scores[li].data_ptr()
+            cfg.idx_out = idx[li].data_ptr()
             cfg.alloc_slot = self.alloc[li].data_ptr() if self.write_allocate else None
         # the copy streams outlive the runtime (it holds their handles)
         self._copy = copy_stream(dev)
@@ -188,14 +222,14 @@ class ColdStaging:
         # stream of their own, so they share the link with the prefetches
         # queued before them instead of waiting behind them
         self._urgent = torch.cuda.Stream(device=dev) if urgent_stream else None
-        self._addr = (dst, src, nbytes)    # read at creation; kept for inspection
+        self._addr = (dst, src, nbytes, ncold)    # read at creation; kept for inspection
         d = nat.StagingDesc(n_layers=L, n_cold=n, n_slots=self.n_slots, top_k=k, keep=self.keep,
                             max_inflight=self._max_inflight, spare=self.spare, ring=max(2, int(ring)),
                             write_allocate=int(self.write_allocate), fill_mode=_FILL_MODE[fill_mode],
-                            track_busy=int(track_busy), residency=self._dev_i32.data_ptr(),
+                            track_busy=int(track_busy), sels_per_layer=Bs, residency=self._dev_i32.data_ptr(),
                             feedback=self.feedback.data_ptr(), slot_addr=dst.ctypes.data,
                             chunk_addr=src.ctypes.data, chunk_nbytes=nbytes.ctypes.data,
-                            copy_stream=self._copy.cuda_stream,
+                            n_cold_per_unit=ncold.ctypes.data, copy_stream=self._copy.cuda_stream,
                             urgent_stream=self._urgent.cuda_stream if self._urgent is not None else None)
         self._L = nat.lib()
         h = ctypes.c_void_p()
@@ -262,9 +296,10 @@ class ColdStaging:
 
     def _snapshot(self):
         L = len(self.layers)
+        U = L * self.sels
         stats = nat.StagingStats()
-        state = np.empty((L, self.n_slots), dtype=np.int8)
-        holds = np.empty((L, self.n_slots), dtype=np.int64)
+        state = np.empty((U, self.n_slots), dtype=np.int8)
+        holds = np.empty((U, self.n_slots), dtype=np.int64)
         wa = np.empty((L, 2), dtype=np.int64)
         nat.check(self._L.halo_staging_get(self._h, ctypes.byref(stats), state.ctypes.data, holds.ctypes.data,
                                            wa.ctypes.data), "halo_staging_get")
@@ -284,12 +319,13 @@ class ColdStaging:
 
     @property
     def state(self) -> np.ndarray:
-        """Slot states (layers, n_slots): 0 free, 1 filling, 2 ready, 4 reserved."""
+        """Slot states (units, n_slots): 0 free, 1 filling, 2 ready, 4
+        reserved; unit = layer * selections per layer + row."""
         return self._snapshot()[1]
 
     @property
     def holds(self) -> np.ndarray:
-        """Chunk each slot holds (layers, n_slots), -1 for none."""
+        """Chunk each slot holds (units, n_slots), -1 for none."""
         return self._snapshot()[2]
 
     @property
@@ -297,10 +333,12 @@ class ColdStaging:
         """Write-allocate slots (layers, 2), -1 for none."""
         return self._snapshot()[3]
 
-    def resident(self, layer: int) -> list:
-        """Chunks of ``layer`` whose residency entry has been committed."""
+    def resident(self, layer: int, row: int = 0) -> list:
+        """Chunks of ``layer`` (batch ``row`` of a per-row layer) whose
+        residency entry has been committed."""
         _, state, holds, _ = self._snapshot()
-        return sorted(int(holds[layer, s]) for s in np.flatnonzero(state[layer] == _READY))
+        u = layer * self.sels + row
+        return sorted(int(holds[u, s]) for s in np.flatnonzero(state[u] == _READY))
 
     def hit_rate(self) -> float:
         s = self._snapshot()[0]

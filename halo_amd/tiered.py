@@ -145,7 +145,10 @@ class RaggedTieredDecodeLayer:
     """
 
     def __init__(self, *, H: int, H_kv: int, D: int, dtype: torch.dtype, rows, top_k: int, device,
-                 split: Optional[int] = None) -> None:
+                 split: Optional[int] = None, cold_kmean: Optional[torch.Tensor] = None) -> None:
+        """``cold_kmean`` (B, H_kv, max_cold, D): the cold chunks' page means,
+        computed from the chunks when not given (needed when the chunks live
+        in pinned host memory)."""
         from .decode import SlotRef
         B = len(rows)
         n_cold = [len(cold) for _, cold in rows]
@@ -177,10 +180,17 @@ class RaggedTieredDecodeLayer:
                 cat[b * max_cold: b * max_cold + len(cold)] = d
                 self.plan.keep += keep
         self.catalog = descs_to_device(cat, device)
-        self.kmean = torch.zeros((B, H_kv, max(max_cold, 1), D), device=device, dtype=dtype)
-        for b, (_, cold) in enumerate(rows):
-            for j, c in enumerate(cold):
-                chunk_means(c.k.unsqueeze(0), c.T, row0=0, n_pages=1, out=self.kmean[b:b + 1], page_offset=j)
+        if cold_kmean is None:
+            if any(c.k.device.type == "cpu" for _, cold in rows for c in cold):
+                raise AssertionError("cold chunks in pinned host memory need cold_kmean (their page means on the GPU)")
+            cold_kmean = torch.zeros((B, H_kv, max(max_cold, 1), D), device=device, dtype=dtype)
+            for b, (_, cold) in enumerate(rows):
+                for j, c in enumerate(cold):
+                    chunk_means(c.k.unsqueeze(0), c.T, row0=0, n_pages=1, out=cold_kmean[b:b + 1], page_offset=j)
+        if tuple(cold_kmean.shape) != (B, H_kv, max(max_cold, 1), D) or cold_kmean.dtype != dtype \
+                or cold_kmean.stride(-1) != 1:
+            raise AssertionError(f"cold_kmean must be ({B}, {H_kv}, {max(max_cold, 1)}, {D}) {dtype}")
+        self.kmean = cold_kmean
         self.n_cold = torch.tensor(n_cold, dtype=torch.int32, device=device)
         self.idx = torch.empty((B, top_k), device=device, dtype=torch.int32)
         self.scores = torch.empty((B, max(max_cold, 1)), device=device, dtype=torch.float32)

@@ -506,34 +506,45 @@ int halo_store_i32(int32_t* base, int64_t n_elems, const int64_t* idx, const int
 /*
  * Description of a staging cache over n_layers decode layers whose fused
  * selections (halo_select_cfg) already point at `residency`, the slot
- * catalogs and `feedback`.  All arrays are copied at creation.
- *   residency:   device int32[n_layers * n_cold + n_layers]: the residency
- *                entries (slot or -1) then each layer's write-allocate slot;
- *   feedback:    device fp32 rows (n_layers, n_cold + 2 * top_k): scores |
- *                picks (int32) | residency used (int32), written by the kernel;
- *   slot_addr:   (n_layers, n_slots, 2) device addresses of each slot's K, V;
- *   chunk_addr:  (n_layers, n_cold, 2) addresses of each cold chunk's K, V:
+ * catalogs and `feedback`.  The cache's unit is one selection:
+ * sels_per_layer = 1 for a layer with one selection, B for a layer with
+ * per-row selection (per_row = 1: each batch row selects among its own cold
+ * chunks, with its own n_slots slots); unit u = layer * sels_per_layer + row.
+ * All arrays are copied at creation.
+ *   residency:   device int32[U * n_cold + n_layers] (U = n_layers *
+ *                sels_per_layer): the residency entries of each unit (slot or
+ *                -1; n_cold = the selection's catalog_stride) then each
+ *                layer's write-allocate slot;
+ *   feedback:    device fp32, per layer sels_per_layer * (n_cold + 2 * top_k)
+ *                words: scores (sels, n_cold) | picks (sels, top_k) int32 |
+ *                residency used (sels, top_k) int32, as the selection writes
+ *                them (score_out, idx_out, res_out);
+ *   slot_addr:   (U, n_slots, 2) device addresses of each slot's K, V;
+ *   chunk_addr:  (U, n_cold, 2) addresses of each cold chunk's K, V:
  *                host pointers of pinned memory (fill_mode 0, hipMemcpyAsync)
  *                or device-visible ones (fill_mode 1, copy kernels); a chunk
  *                whose V follows its K, staged into a slot laid out the same
  *                way, is filled by one copy;
- *   chunk_nbytes:(n_layers, n_cold) bytes of one chunk's K (= its V);
+ *   chunk_nbytes:(U, n_cold) bytes of one chunk's K (= its V);
+ *   n_cold_per_unit: (U) cold chunks of each unit (NULL: n_cold each);
  *   copy_stream / urgent_stream: where fills run (urgent: fills the next
  *                launch of their layer waits for; NULL = copy_stream).
- * keep in [top_k, n_slots] best-scoring chunks per layer are staged; at most
- * max_inflight fills in flight; `spare` slots per layer kept free;
+ * keep in [top_k, n_slots] best-scoring chunks per unit are staged; at most
+ * max_inflight fills in flight; `spare` slots per unit kept free;
  * `ring` feedback entries in flight (>= segments per step + 1);
- * track_busy counts operations issued while the compute stream still had
- * work queued (a test aid; costs one stream query each).
+ * write_allocate needs sels_per_layer == 1; track_busy counts operations
+ * issued while the compute stream still had work queued (a test aid; costs
+ * one stream query each).
  */
 typedef struct halo_staging_desc {
   int32_t n_layers, n_cold, n_slots, top_k, keep, max_inflight, spare, ring;
-  int32_t write_allocate, fill_mode, track_busy, pad;
+  int32_t write_allocate, fill_mode, track_busy, sels_per_layer;
   int32_t* residency;
   const float* feedback;
   const uint64_t* slot_addr;
   const uint64_t* chunk_addr;
   const int64_t* chunk_nbytes;
+  const int32_t* n_cold_per_unit;
   void* copy_stream;
   void* urgent_stream;
 } halo_staging_desc;
@@ -564,8 +575,8 @@ typedef struct halo_staging halo_staging;
  * cache's copies and forgets every slot (the caller clears `residency`);
  * halo_staging_set changes max_inflight and can zero the counters;
  * halo_staging_get copies the counters and the host mirror: slot state
- * (n_layers, n_slots) int8 (0 free, 1 filling, 2 ready, 4 reserved), the
- * chunk each slot holds (int64, -1 none) and the write-allocate slots
+ * (U, n_slots) int8 (0 free, 1 filling, 2 ready, 4 reserved), the chunk
+ * each slot holds (int64, -1 none) and the write-allocate slots
  * (n_layers, 2) int64; any output may be NULL.
  */
 int halo_staging_create(const halo_staging_desc* desc, halo_staging** out);

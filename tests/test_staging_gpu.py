@@ -238,3 +238,93 @@ def test_benchmark_loop_matches_all_hbm_every_step(dev):
             assert torch.equal(out_hist[t, li], o_ref), (t, li)
             assert torch.equal(lse_hist[t, li], l_ref), (t, li)
             assert torch.equal(idx_hist[t, li], hbm[li].idx[0].to(torch.int32)), (t, li)
+
+
+def _ragged_setup(dev, *, L=2, ctx=(1536, 3072, 768, 4096), chunk=256, top_k=2, seed=21):
+    """All-HBM and staged ragged layers over the same K/V: per row, the last
+    quarter of its chunks hot in HBM and the rest cold (staged: K and V of a
+    chunk adjacent in one pinned buffer per row)."""
+    from halo_amd.decode import ChunkRef
+    from halo_amd.tiered import RaggedTieredDecodeLayer
+    H, H_kv, D = 16, 4, 128
+    g = torch.Generator(device=dev).manual_seed(seed)
+    hbm, staged = [], []
+    for _ in range(L):
+        rows_h, rows_s = [], []
+        for b, T in enumerate(ctx):
+            k = torch.randn((H_kv, T, D), generator=g, device=dev)
+            k[..., :3] *= 6
+            k = k.to(torch.bfloat16)
+            v = torch.randn((H_kv, T, D), generator=g, device=dev).to(torch.bfloat16)
+            n = T // chunk
+            n_hot = max(1, n // 4)
+            refs = [ChunkRef(k[:, i * chunk:(i + 1) * chunk], v[:, i * chunk:(i + 1) * chunk], i * chunk, True,
+                             batch=b) for i in range(n)]
+            buf = torch.empty((n - n_hot, 2, H_kv, chunk, D), dtype=torch.bfloat16, pin_memory=True)
+            host = []
+            for j, c in enumerate(refs[:n - n_hot]):
+                buf[j, 0].copy_(c.k)
+                buf[j, 1].copy_(c.v)
+                host.append(ChunkRef(buf[j, 0], buf[j, 1], c.chunk_start, True, batch=b))
+            rows_h.append((refs[n - n_hot:], refs[:n - n_hot]))
+            rows_s.append((refs[n - n_hot:], host))
+        a = RaggedTieredDecodeLayer(H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, rows=rows_h, top_k=top_k, device=dev)
+        s = RaggedTieredDecodeLayer(H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, rows=rows_s, top_k=top_k, device=dev,
+                                    cold_kmean=a.kmean)
+        hbm.append(a)
+        staged.append(s)
+    return hbm, staged, (len(ctx), H, D)
+
+
+def test_staged_ragged_batch_matches_all_hbm(dev):
+    """Per-row staging of a ragged batch (each row its own cold chunks,
+    slots and policy; rows with 3 to 12 cold chunks and 4 slots) through the
+    benchmark's loop: every step's outputs, LSEs and per-row picks equal the
+    all-HBM ragged layers' bit for bit, and rows are served both from their
+    slots and in place."""
+    import bench
+    from halo_amd.staging import ColdStaging
+    hbm, staged, (B, H, D) = _ragged_setup(dev)
+    L, steps, k = len(hbm), 20, 2
+    scale = 1 / math.sqrt(D)
+    st = ColdStaging(staged, n_slots=4, keep=3, max_inflight=6)
+    assert st.sels == B and st.per_row
+    qtraj = bench.query_trajectory(torch, dev, steps=steps, L=L, H=H, D=D, rho=0.8, seed=22, B=B)
+    q_pos = torch.tensor([T - 1 for T in (1536, 3072, 768, 4096)], device=dev, dtype=torch.int64)
+    out_hist = torch.zeros((steps, L, B, H, D), device=dev, dtype=torch.bfloat16)
+    lse_hist = torch.zeros((steps, L, B, H), device=dev)
+    idx_hist = torch.full((steps, L, B, k), -7, device=dev, dtype=torch.int32)
+    res_hist = torch.full((steps, L, B, k), -7, device=dev, dtype=torch.int32)
+    lses = [torch.zeros((B, H), device=dev) for _ in range(L)]
+
+    def record(t, lo, hi, outs):
+        for li in range(lo, hi):
+            out_hist[t, li].copy_(outs[li])
+            lse_hist[t, li].copy_(lses[li])
+        idx_hist[t, lo:hi].copy_(st.idx[lo:hi])
+        res_hist[t, lo:hi].copy_(st.res_out[lo:hi])
+
+    bench.refetch_run(torch, staged, st, qtraj, warmup=0, steps=steps, scale=scale, label="ragged test",
+                      segments=2, record=record, lses=lses, q_pos=q_pos)
+    torch.cuda.synchronize()
+    assert st.hits > 0 and st.misses > 0 and st.fills > 0
+    res = res_hist.cpu().numpy()
+    assert (res >= 0).any() and (res == -1).any()
+    o_ref = torch.empty((B, H, D), device=dev, dtype=torch.bfloat16)
+    l_ref = torch.empty((B, H), device=dev)
+    for t in range(steps):
+        for li in range(L):
+            hbm[li].step(qtraj[t, li], scale=scale, out=o_ref, lse=l_ref, q_pos=q_pos)
+            assert torch.equal(out_hist[t, li], o_ref), (t, li)
+            assert torch.equal(lse_hist[t, li], l_ref), (t, li)
+            assert torch.equal(idx_hist[t, li], hbm[li].idx), (t, li)
+    # every ready slot of every row holds its chunk bit for bit
+    state, holds = st.state, st.holds
+    for li, lay in enumerate(staged):
+        for b, (_, cold) in enumerate(lay.rows):
+            u = li * B + b
+            for s in range(st.n_slots):
+                if state[u, s] == 2:
+                    c = int(holds[u, s])
+                    assert torch.equal(st._slot_k[u][s].cpu(), cold[c].k), (li, b, s, c)
+                    assert torch.equal(st._slot_v[u][s].cpu(), cold[c].v), (li, b, s, c)

@@ -509,6 +509,85 @@ def bench_ragged_c4(torch, dev, *, steps: int):
     }
 
 
+def bench_ragged_c4_host(torch, dev, *, steps: int, warmup: int = 10, layers: int = 4, slots: int = 12,
+                         keep: int = 10, rho: float = 0.98):
+    """The ragged batch with its cold tier in pinned host memory: ``layers``
+    distinct layers of the C4 batch (16 sequences of 8K-128K tokens, seed 3,
+    2048-row chunks, hot = last 25 % of each sequence's chunks in HBM), every
+    row selecting its top-8 cold chunks per step inside the launch, served by
+    a per-row HBM staging cache (``slots`` slots per row, the ``keep`` best
+    by the last scores staged) or read in place over the host link.  Each
+    row's query drifts as an AR(1) trajectory (``rho``); one step = the L
+    layers as L graph segments plus the cache's commits, feedback and fills;
+    tokens/s = 16 / step time."""
+    import numpy as np
+
+    from halo_amd.decode import ChunkRef
+    from halo_amd.staging import ColdStaging
+    from halo_amd.tiered import RaggedTieredDecodeLayer
+
+    B, H, H_kv, D, chunk, top_k = 16, 32, 8, 128, 2048, 8
+    rng = np.random.default_rng(3)
+    ctx = [int(x) // chunk * chunk for x in rng.uniform(8192, 131072, size=B)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    staged = []
+    hot_rows = cold_rows = 0
+    for _ in range(layers):
+        rows, rows_hbm = [], []
+        for b, T in enumerate(ctx):
+            k = torch.randn((H_kv, T, D), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((H_kv, T, D), generator=gen, device=dev).to(torch.bfloat16)
+            n = T // chunk
+            n_hot = max(1, n // 4)
+            refs = [ChunkRef(k[:, i * chunk:(i + 1) * chunk], v[:, i * chunk:(i + 1) * chunk], i * chunk, True,
+                             batch=b) for i in range(n)]
+            rows_hbm.append((refs[n - n_hot:], refs[:n - n_hot]))
+            hot_rows += n_hot * chunk
+            cold_rows += (n - n_hot) * chunk
+        means = RaggedTieredDecodeLayer(H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, rows=rows_hbm, top_k=top_k,
+                                        device=dev).kmean
+        for b, (hot, cold) in enumerate(rows_hbm):
+            # hot chunks into HBM tensors of their own (the cold rows' HBM
+            # copies are dropped), cold chunks K|V into one pinned buffer
+            hk = torch.stack([c.k for c in hot], 0).contiguous()
+            hv = torch.stack([c.v for c in hot], 0).contiguous()
+            hot_own = [ChunkRef(hk[i], hv[i], c.chunk_start, True, batch=b) for i, c in enumerate(hot)]
+            buf = torch.empty((len(cold), 2, H_kv, chunk, D), dtype=torch.bfloat16, pin_memory=True)
+            host = []
+            for j, c in enumerate(cold):
+                buf[j, 0].copy_(c.k)
+                buf[j, 1].copy_(c.v)
+                host.append(ChunkRef(buf[j, 0], buf[j, 1], c.chunk_start, True, batch=b))
+            rows.append((hot_own, host))
+        del rows_hbm, k, v, refs
+        staged.append(RaggedTieredDecodeLayer(H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, rows=rows, top_k=top_k,
+                                              device=dev, cold_kmean=means))
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    staging = ColdStaging(staged, n_slots=slots, keep=keep, max_inflight=16)
+    qtraj = query_trajectory(torch, dev, steps=warmup + steps, L=layers, H=H, D=D, rho=rho, seed=13, B=B)
+    q_pos = torch.tensor([T - 1 for T in ctx], device=dev, dtype=torch.int64)
+    rd = refetch_run(torch, staged, staging, qtraj, warmup=warmup, steps=steps, scale=1.0 / math.sqrt(D),
+                     label=f"ragged batch, host tier, {layers} layers, rho {rho}", warm_fills=10 ** 6,
+                     segments=layers, q_pos=q_pos)
+    staged_rows = sum(min(slots, len(c)) for lay in staged for _, c in lay.rows) * chunk
+    rd["tokens_per_s"] = B / (rd["ms_per_step"] * 1e-3)
+    out = {
+        "workload": f"ragged batched GQA decode, bf16, 16 sequences of 8K-128K tokens (seed 3) in 2048-row "
+                    f"chunks, 32/8 heads, d128, {layers} layers, hot 25% per sequence in HBM, cold chunks in "
+                    f"pinned host memory, per-row top-8 refetched through a per-row HBM staging cache "
+                    f"({slots} slots, keep {keep}), AR(1) query drift rho {rho}",
+        "context_lengths": ctx, "layers": layers, "staging_slots_per_row": slots, "staging_keep": keep,
+        "hbm_resident_fraction": (hot_rows + staged_rows) / (hot_rows + cold_rows),
+        "staging_bytes": staging.slot_bytes,
+        **rd,
+    }
+    del staging, staged
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -530,7 +609,7 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "dropin"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin"], default=None,
                     help="run one leg alone (C2 kernel level, chunked prefill, ragged batch, KIVI, drop-in) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
@@ -563,6 +642,7 @@ def main() -> int:
             return {"workload": "C2 kernel level: 32 layers, all chunks in HBM, attention with in-kernel "
                                 "selection + merge per layer, one graph", "us_per_layer": a * 1e3}
         leg = {"c2": c2,
+               "c4host": lambda: bench_ragged_c4_host(torch, dev, steps=max(1, args.steps)),
                "c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
                "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
@@ -711,6 +791,8 @@ def main() -> int:
         del staging, staged
         torch.cuda.empty_cache()
         extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=20)
+        log("ragged host-tier leg")
+        extra["ragged_c4_host_tier"] = bench_ragged_c4_host(torch, dev, steps=40)
         result["extra"] = extra
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -588,6 +588,77 @@ def bench_ragged_c4_host(torch, dev, *, steps: int, warmup: int = 10, layers: in
     return out
 
 
+def bench_model_decode(torch, dev, *, new_tokens: int = 32, prompt: int = 8192):
+    """Decode through a transformers model wrapped with
+    ``wrap_with_halo(HALOConfig(chunked=True))``: a randomly initialised
+    Qwen2-architecture model with Llama-3-8B attention shapes (hidden 4096,
+    32/8 heads, head dim 128; 4 layers, MLP width 1024, bf16) prefilled with
+    an 8192-token prompt in 2048-token slices, then ``new_tokens`` greedy
+    steps; the cold tier (chunks of 1024 rows beyond the 512-row recent
+    window) lives in pinned host memory and every decode step attends all
+    of it (the lossless Path-D cache).  Beside it: the same weights
+    unwrapped, decoding with SDPA over a DynamicCache in HBM."""
+    from transformers import AutoModelForCausalLM
+    from transformers.models.qwen2 import Qwen2Config
+
+    from halo_amd import HALOConfig, prefill_then_generate, wrap_with_halo
+
+    def cfg():
+        return Qwen2Config(vocab_size=1024, hidden_size=4096, intermediate_size=1024, num_hidden_layers=4,
+                           num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=16384,
+                           rope_theta=500000.0, tie_word_embeddings=False, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    ref = AutoModelForCausalLM.from_config(cfg()).to(dev, torch.bfloat16).eval()
+    halo = AutoModelForCausalLM.from_config(cfg()).to(dev, torch.bfloat16).eval()
+    halo.load_state_dict(ref.state_dict())
+    wrap_with_halo(halo, HALOConfig(chunked=True, chunk_size=1024, recent_window=512))
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(10, 1000, (1, prompt), generator=g).to(dev)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        r = fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, r
+
+    with torch.no_grad():
+        prefill_then_generate(halo, ids[:, :2048], prefill_chunk_tokens=1024, max_new_tokens=2)   # warm-up
+        t_pre, _ = timed(lambda: prefill_then_generate(halo, ids, prefill_chunk_tokens=2048, max_new_tokens=0))
+        t_all, res = timed(lambda: prefill_then_generate(halo, ids, prefill_chunk_tokens=2048,
+                                                         max_new_tokens=new_tokens))
+        tele = res["cache_telemetry"]
+        halo_ms = (t_all - t_pre) / new_tokens * 1e3
+        # the same weights, SDPA over a DynamicCache held in HBM
+        out = ref(ids, use_cache=True, return_dict=True)
+        cache, nxt = out.past_key_values, out.logits[:, -1:].argmax(-1)
+        for _ in range(2):
+            o = ref(nxt, past_key_values=cache, use_cache=True, return_dict=True)
+            nxt = o.logits[:, -1:].argmax(-1)
+
+        def sdpa_steps():
+            nonlocal nxt
+            for _ in range(new_tokens):
+                o = ref(nxt, past_key_values=cache, use_cache=True, return_dict=True)
+                nxt = o.logits[:, -1:].argmax(-1)
+        t_ref, _ = timed(sdpa_steps)
+    ref_ms = t_ref / new_tokens * 1e3
+    cold_bytes = int(tele.get("cold_positions_per_layer_max", 0)) * 8 * 128 * 2 * 2 * 4   # K+V, 4 layers
+    out = {
+        "workload": "transformers Qwen2-architecture model (random init), Llama-3-8B attention shapes (32/8 heads, "
+                    "d128), 4 layers, bf16, 8192-token prompt prefilled in 2048-token slices, then greedy decode "
+                    "through wrap_with_halo(chunked=True): chunk 1024, recent window 512, cold chunks in pinned host "
+                    "memory attended every step",
+        "decode_ms_per_token": halo_ms, "decode_tokens_per_s": 1e3 / halo_ms,
+        "prefill_ms": t_pre * 1e3, "sdpa_dynamic_cache_ms_per_token": ref_ms,
+        "cold_bytes_per_token_over_link": cold_bytes,
+        "telemetry": {k: (v if isinstance(v, (int, float, bool, str)) else str(v)) for k, v in tele.items()},
+    }
+    del ref, halo, cache
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -609,7 +680,7 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin", "model"], default=None,
                     help="run one leg alone (C2 kernel level, chunked prefill, ragged batch, KIVI, drop-in) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
@@ -643,6 +714,7 @@ def main() -> int:
                                 "selection + merge per layer, one graph", "us_per_layer": a * 1e3}
         leg = {"c2": c2,
                "c4host": lambda: bench_ragged_c4_host(torch, dev, steps=max(1, args.steps)),
+               "model": lambda: bench_model_decode(torch, dev),
                "c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
                "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
@@ -793,6 +865,8 @@ def main() -> int:
         extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=20)
         log("ragged host-tier leg")
         extra["ragged_c4_host_tier"] = bench_ragged_c4_host(torch, dev, steps=40)
+        log("model decode leg")
+        extra["model_decode"] = bench_model_decode(torch, dev)
         result["extra"] = extra
     if not args.no_cpu_baseline:
         log("cpu baseline")

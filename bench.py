@@ -235,6 +235,9 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
     del graphs
     sel = staging.hits + staging.misses
     link = (staging.fill_bytes + staging.miss_bytes) / steps
+    ns = staging.stats
+    log(f"{label}: host per step: plan {ns['ns_plan'] / steps / 1e3:.0f} us (fill issue {ns['ns_issue'] / steps / 1e3:.0f} "
+        f"us), feedback wait {ns['ns_wait'] / steps / 1e3:.0f} us")
     log(f"{label}: {dt * 1e3:.3f} ms/step, hit rate {staging.hit_rate():.4f} over {sel} selections "
         f"({staging.misses_predicted} of {staging.misses} misses predicted), "
         f"{staging.fills / steps:.2f} fills/step, {staging.wa_commits / steps:.2f} write-allocated/step, "

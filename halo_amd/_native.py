@@ -78,7 +78,7 @@ class StagingStats(ctypes.Structure):
     """halo_staging_stats (include/halo_hip.h)."""
     _fields_ = [(name, _i64) for name in (
         "hits", "misses", "misses_predicted", "fills", "fill_bytes", "miss_bytes", "wa_commits", "wa_dups",
-        "fills_while_busy", "commits_while_busy", "evictions_while_busy")]
+        "fills_while_busy", "commits_while_busy", "evictions_while_busy", "ns_plan", "ns_issue", "ns_wait")]
 
 
 _DECODE_ARGS = [

@@ -31,6 +31,7 @@
 //    the compute stream precedes every later read and the slot can take a
 //    fill at once.
 #include <algorithm>
+#include <chrono>
 #include <numeric>
 #include <vector>
 
@@ -87,6 +88,11 @@ struct halo_staging {
 
 namespace halo {
 namespace {
+
+int64_t now_ns() {
+  return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
 
 bool stream_busy(hipStream_t s) {
   const hipError_t e = hipStreamQuery(s);
@@ -195,7 +201,9 @@ int issue(halo_staging* h, const Pending& p) {
     f.dst_v = nullptr;
     f.src_v = nullptr;
   }
+  const int64_t t0 = now_ns();
   const int rc = h->kernel_fills ? halo_stage_fills_read(&f, 1, s) : halo_stage_fills(&f, 1, s);
+  h->st.ns_issue += now_ns() - t0;
   if (rc != HALO_OK) return rc;
   HALO_CHECK_HIP(hipEventRecord(h->fill_ev[(size_t)p.unit * h->S + p.slot], s));
   h->pending.push_back(p);
@@ -476,7 +484,9 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
   while (h->seen < h->queued) {
     const int r = (int)(h->seen % h->ring_n);
     if (h->seen < target) {
+      const int64_t t0 = now_ns();
       HALO_CHECK_HIP(hipEventSynchronize(h->ring_ev[r]));
+      h->st.ns_wait += now_ns() - t0;
     } else {
       const hipError_t e = hipEventQuery(h->ring_ev[r]);
       if (e == hipErrorNotReady) {
@@ -500,7 +510,10 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
     h->seen += 1;
   }
   if (units.empty()) return HALO_OK;
-  return plan(h, units, scores, compute);
+  const int64_t t0 = now_ns();
+  const int rc = plan(h, units, scores, compute);
+  h->st.ns_plan += now_ns() - t0;
+  return rc;
 }
 
 extern "C" int halo_staging_reset(halo_staging* h) {

@@ -549,9 +549,12 @@ typedef struct halo_staging_desc {
   void* urgent_stream;
 } halo_staging_desc;
 
+/* Counters of a staging cache; ns_* are host nanoseconds spent planning
+ * (including fill issue), issuing fills, and waiting for feedback. */
 typedef struct halo_staging_stats {
   int64_t hits, misses, misses_predicted, fills, fill_bytes, miss_bytes, wa_commits, wa_dups;
   int64_t fills_while_busy, commits_while_busy, evictions_while_busy;
+  int64_t ns_plan, ns_issue, ns_wait;
 } halo_staging_stats;
 
 typedef struct halo_staging halo_staging;

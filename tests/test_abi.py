@@ -54,11 +54,11 @@ def test_select_cfg_layout_matches_header():
 
 def test_staging_structs_match_header():
     """halo_staging_desc: 12 int32 then 8 pointers (112 bytes);
-    halo_staging_stats: 11 int64."""
+    halo_staging_stats: 14 int64."""
     from halo_amd import _native as nat
     assert ctypes.sizeof(nat.StagingDesc) == 112
     assert nat.StagingDesc.residency.offset == 48 and nat.StagingDesc.urgent_stream.offset == 104
-    assert ctypes.sizeof(nat.StagingStats) == 88 and nat.StagingStats.evictions_while_busy.offset == 80
+    assert ctypes.sizeof(nat.StagingStats) == 112 and nat.StagingStats.evictions_while_busy.offset == 80
 
 
 def test_descriptor_record_size():

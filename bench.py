@@ -591,6 +591,46 @@ def bench_ragged_c4_host(torch, dev, *, steps: int, warmup: int = 10, layers: in
     return out
 
 
+def bench_long_context(torch, dev, *, steps: int = 60, warmup: int = 10, L: int = 16, slots: int = 12,
+                       keep: int = 6, rho: float = 0.98):
+    """C2's layer shape at a 131072-token context: 128 chunks of 1024 rows,
+    32 hot (25 %) in HBM, 96 cold in pinned host memory, top-4 per layer per
+    step -- beyond the fused selection's 64 cold chunks, so each layer is the
+    two-launch path (the staged scorer, then the attention launch and its
+    merge) -- served by the HBM staging cache; L distinct layers, AR(1)
+    query drift.  Beside it the same layers with every chunk in HBM."""
+    H, H_kv, D, T, chunk, n_hot, top_k = 32, 8, 128, 131072, 1024, 32, 4
+    from halo_amd.staging import ColdStaging
+    from halo_amd.tiered import TieredDecodeLayer
+    layers, qs, _ = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
+                                n_planted=4, sigma=8.0, dev=dev, seed=7)
+    assert not layers[0].fused
+    scale = 1.0 / math.sqrt(D)
+    attn_avg, _ = kernel_level_c2(torch, layers, qs, scale=scale, reps=20, with_scorer=False)
+    tiers = host_tier(torch, layers)
+    staged = [TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=lay.hot, cold=tiers[li],
+                                top_k=top_k, device=dev, cold_kmean=lay.kmean) for li, lay in enumerate(layers)]
+    staging = ColdStaging(staged, n_slots=slots, keep=keep, max_inflight=16)
+    qtraj = query_trajectory(torch, dev, steps=warmup + steps, L=L, H=H, D=D, rho=rho, seed=17)
+    rd = refetch_run(torch, staged, staging, qtraj, warmup=warmup, steps=steps, scale=scale,
+                     label=f"131072-token context, 96 cold chunks, rho {rho}", warm_fills=10 ** 6, segments=4)
+    rows = staged[0].attended_rows
+    layer_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4 + (T // chunk - n_hot) * H_kv * D * 2
+    out = {
+        "workload": f"Llama-3-8B-shaped GQA decode at 131072 tokens: {L} layers, 128 chunks of 1024 rows, 32 hot in "
+                    f"HBM + top-4 of 96 cold chunks in pinned host memory per layer per step (staged scorer + "
+                    f"attention launch), HBM staging cache of {slots} slots (keep {keep}), AR(1) drift rho {rho}",
+        "layers": L, "hbm_resident_fraction": (n_hot + slots) / (T // chunk),
+        "all_hbm_us_per_layer": attn_avg * 1e3,
+        "all_hbm_gbps": layer_bytes / (attn_avg * 1e-3) / 1e9,
+        "staged_us_per_layer": rd["ms_per_step"] * 1e3 / L,
+        **{k: v for k, v in rd.items() if k != "tokens_per_s"},
+    }
+    del staging, staged, layers, tiers
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_model_decode(torch, dev, *, new_tokens: int = 32, prompt: int = 8192):
     """Decode through a transformers model wrapped with
     ``wrap_with_halo(HALOConfig(chunked=True))``: a randomly initialised
@@ -683,7 +723,7 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin", "model"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin", "model", "long"], default=None,
                     help="run one leg alone (C2 kernel level, chunked prefill, ragged batch, KIVI, drop-in) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
@@ -718,6 +758,7 @@ def main() -> int:
         leg = {"c2": c2,
                "c4host": lambda: bench_ragged_c4_host(torch, dev, steps=max(1, args.steps)),
                "model": lambda: bench_model_decode(torch, dev),
+               "long": lambda: bench_long_context(torch, dev, steps=max(1, args.steps)),
                "c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
                "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
@@ -870,6 +911,8 @@ def main() -> int:
         extra["ragged_c4_host_tier"] = bench_ragged_c4_host(torch, dev, steps=40)
         log("model decode leg")
         extra["model_decode"] = bench_model_decode(torch, dev)
+        log("long-context leg")
+        extra["long_context_128k"] = bench_long_context(torch, dev)
         result["extra"] = extra
     if not args.no_cpu_baseline:
         log("cpu baseline")

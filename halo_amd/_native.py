@@ -126,6 +126,16 @@ _SIGNATURES = {
         _i32, _f32, _f32, _f32, _i32, _i32, _i32,  # normalize, alpha, beta, gamma, refresh, sink_pages, P_total
         _c_void_p,
     ]),
+    "halo_chunk_score_topk_staged": (_i32, [
+        _c_void_p, _i64, _i64, _i32,             # q, strides, dtype
+        _i32, _i32, _i32, _i32,                  # B, H, H_kv, D
+        _c_void_p, _i64, _i64, _i64,             # kmean + strides
+        _c_void_p, _i64, _c_void_p, _i32, _i32, _i32,  # eligible, stride, n_elig_per_sel, n_elig, k, per_row
+        _c_void_p, _c_void_p,                    # idx_out, score_out
+        _c_void_p, _i64, _c_void_p, _i64, _i32,  # catalog, stride, table, stride, slot0
+        _c_void_p, _c_void_p, _i32, _c_void_p,   # residency, slot_catalog, n_slots, res_out
+        _c_void_p,
+    ]),
     "halo_page_minmax": (_i32, [_c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i32, _i32,
                                 _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "halo_quest_score_topk": (_i32, [

@@ -53,14 +53,19 @@ def score_topk(q: torch.Tensor, kmean: torch.Tensor, eligible: torch.Tensor, k: 
                P_total: Optional[int] = None,
                catalog: Optional[torch.Tensor] = None, table: Optional[torch.Tensor] = None,
                table_stride: int = 0, table_slot0: int = 0, catalog_stride: int = 0,
-               idx_out: Optional[torch.Tensor] = None, score_out: Optional[torch.Tensor] = None):
+               idx_out: Optional[torch.Tensor] = None, score_out: Optional[torch.Tensor] = None,
+               staging: Optional[tuple] = None):
     """Score eligible chunks and pick the top ``k``.
 
     q (B, H, D) or (B, H, 1, D); kmean (B, H_kv, P, D) in q's dtype;
     eligible int32 (n_sel, n_elig) or (n_elig,).  Returns (idx int32
     (n_sel, k) ascending with -1 padding, scores fp32 (n_sel, n_elig)).
     With ``table``/``catalog`` (uint8 views of halo_chunk_desc arrays) the
-    chosen descriptors are copied into the table on the device."""
+    chosen descriptors are copied into the table on the device.
+    ``staging`` = (residency int32 tensor, slot catalog uint8 tensor,
+    n_slots, res_out int32 tensor): chosen chunks held by an HBM staging
+    slot are written to the table with the slot's addresses
+    (``halo_chunk_score_topk_staged``; raw scores only)."""
     L = nat.lib()
     q3 = q.squeeze(2) if q.dim() == 4 else q
     B, H, D = q3.shape
@@ -84,6 +89,20 @@ def score_topk(q: torch.Tensor, kmean: torch.Tensor, eligible: torch.Tensor, k: 
         score_out = torch.empty((n_sel, max(n_elig, 1)), device=q3.device, dtype=torch.float32)
     if catalog is not None and catalog_stride == 0 and per_row:
         catalog_stride = catalog.numel() // 88 // n_sel
+    if staging is not None:
+        if normalize or table is None:
+            raise AssertionError("the staged selection writes a table and uses raw scores")
+        res, scat, n_slots, res_out = staging
+        nat.check(L.halo_chunk_score_topk_staged(
+            q3.data_ptr(), q3.stride(0), q3.stride(1), nat.dtype_code(q3.dtype),
+            B, H, H_kv, D,
+            kmean.data_ptr(), kmean.stride(0), kmean.stride(1), kmean.stride(2),
+            eligible.data_ptr(), elig_stride, nat.ptr(n_elig_per_sel), n_elig, int(k), int(per_row),
+            idx_out.data_ptr(), score_out.data_ptr(),
+            nat.ptr(catalog), catalog_stride or n_elig, nat.ptr(table), table_stride, table_slot0,
+            res.data_ptr(), scat.data_ptr(), int(n_slots), res_out.data_ptr(), nat.stream_ptr()),
+            "halo_chunk_score_topk_staged")
+        return idx_out, score_out
     nat.check(L.halo_chunk_score_topk(
         q3.data_ptr(), q3.stride(0), q3.stride(1), nat.dtype_code(q3.dtype),
         B, H, H_kv, D,

@@ -108,6 +108,13 @@ struct ScoreParams {
   int normalize;
   float alpha, beta, gamma;
   int refresh, sink_pages, P_total;
+  // HBM staging (residency == NULL: off): a chosen chunk whose residency
+  // entry names a slot is written to the table with that slot's addresses
+  // and strides; res_out[sel * k + j] gets the entry used (-1: in place).
+  const int32_t* residency;
+  const halo_chunk_desc* slot_catalog;
+  int n_slots;
+  int32_t* res_out;
 };
 
 constexpr int kMaxElig = 1024;
@@ -120,12 +127,15 @@ __device__ __forceinline__ bool beats(float sa, int ea, float sb, int eb) {
   return sa > sb || (sa == sb && ea < eb);
 }
 
-template <int DT>
+// DC: the head dim when known at compile time (64, 128, 256: the dot-product
+// loops unroll and every load of a triple is issued before the first use),
+// 0 for any other multiple of 16 (runtime loops).
+template <int DT, int DC>
 __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
   __shared__ float s_qg[kMaxQg];
-  __shared__ float s_score[kMaxElig];
-  __shared__ int s_chunk[kMaxElig];
-  __shared__ int s_sel[kMaxElig];
+  __shared__ __align__(16) float s_score[kMaxElig];
+  __shared__ __align__(16) int s_chunk[kMaxElig];
+  __shared__ __align__(16) int s_sel[kMaxElig];
   __shared__ float s_dot[kMaxDots];
   const int sel = blockIdx.x;
   const int tid = threadIdx.x;
@@ -138,18 +148,28 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
 
   // GQA mean of the query heads of each KV head, rounded to the q dtype
   // (torch's .mean keeps the dtype); rep == 1 uses q as is.
-  const int QG = nrows * P.H_kv * P.D;
+  const int Dq = DC ? DC : P.D;
+  const int QG = nrows * P.H_kv * Dq;
   for (int i = tid; i < QG; i += nthr) {
-    const int d = i % P.D;
-    const int h = (i / P.D) % P.H_kv;
-    const int r = i / (P.D * P.H_kv);
+    const int d = i % Dq;
+    const int h = (i / Dq) % P.H_kv;
+    const int r = i / (Dq * P.H_kv);
     const int64_t qb = (int64_t)(b0 + r) * P.qsb;
     float v;
     if (P.rep == 1) {
       v = load_elem(P.q, qb + (int64_t)h * P.qsh + d, DT);
     } else {
+      // the rep loads are independent: issue them in batches of 4, then add in head order
       float acc = 0.f;
-      for (int j = 0; j < P.rep; ++j) acc += load_elem(P.q, qb + (int64_t)(h * P.rep + j) * P.qsh + d, DT);
+      for (int j0 = 0; j0 < P.rep; j0 += 4) {
+        float x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          x[j] = j0 + j < P.rep ? load_elem(P.q, qb + (int64_t)(h * P.rep + j0 + j) * P.qsh + d, DT) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j0 + j < P.rep) acc += x[j];
+      }
       acc = opaque(acc * P.inv_rep);  // fp32 product, then one rounding to the q dtype
       v = DT == HALO_F32 ? acc
           : (DT == HALO_BF16 ? __uint_as_float((uint32_t)f32_to_bf16_rne(acc) << 16)
@@ -179,18 +199,29 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
       const int r = rh / P.H_kv, h = rh % P.H_kv;
       const int64_t mb = (int64_t)(b0 + r) * P.msb + (int64_t)h * P.msh + (int64_t)s_chunk[i] * P.msp;
       const char* row = reinterpret_cast<const char*>(P.km) + mb * esz;
-      const float* qg = s_qg + (r * P.H_kv + h) * P.D;
+      const float* qg = s_qg + (r * P.H_kv + h) * Dq;
       // D is cut into G = D/16 slices; slice c holds elements
       // ep*(c + p*G) + e (p < 16/ep, e < ep), summed in (p, e) order; the G
       // slice sums are added as a balanced pairwise tree in slice order.  This
       // is the order of the fused selection in decode_attn.hip, whose slices
       // sit in G lanes and meet in an xor butterfly.
-      const int G = P.D / 16;
+      constexpr int GC = DC / 16;  // compile-time slice count (0: runtime)
+      const int G = DC ? GC : P.D / 16;
       float part[16];
-      for (int c = 0; c < G; ++c) {
+      // compile-time D: every piece of the row is loaded before the first use
+      uint4 rowv[DC ? (DC / 16) * (16 / ep) : 1];
+      if constexpr (DC != 0) {
+#pragma unroll
+        for (int x = 0; x < GC * (16 / ep); ++x) rowv[x] = *reinterpret_cast<const uint4*>(row + x * 16);
+      }
+#pragma unroll
+      for (int c = 0; c < (DC ? GC : 16); ++c) {
+        if (!DC && c >= G) break;
         float a = 0.f;
+#pragma unroll
         for (int p = 0; p < 16 / ep; ++p) {
-          const uint4 v = *reinterpret_cast<const uint4*>(row + (c + p * G) * 16);
+          const uint4 v = DC ? rowv[(c + p * G) % (DC ? GC * (16 / ep) : 1)]
+                             : *reinterpret_cast<const uint4*>(row + (c + p * G) * 16);
           float f[8];
           if constexpr (DT == HALO_F32) {
             f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
@@ -276,12 +307,33 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
     __syncthreads();
   }
 
-  // Rank by (score desc, chunk asc); selected = rank < kk.
+  // Rank by (score desc, chunk asc); selected = rank < kk.  Candidates are
+  // read four at a time (16-byte LDS reads, several in flight); entries past
+  // n are padding that never outranks (-inf, index past every chunk).
+  for (int i = n + tid; i < ((n + 15) & ~15); i += nthr) {
+    s_score[i] = -INFINITY;
+    s_chunk[i] = 0x7fffffff;
+    s_sel[i] = 0;
+  }
+  __syncthreads();
+  const int n16 = (n + 15) & ~15;
   for (int i = tid; i < n; i += nthr) {
     const float si = s_score[i];
     const int ei = s_chunk[i];
     int rank = 0;
-    for (int j = 0; j < n; ++j) rank += beats(s_score[j], s_chunk[j], si, ei) ? 1 : 0;
+    for (int j = 0; j < n16; j += 16) {
+      float4 sv[4];
+      int4 ev[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        sv[x] = *reinterpret_cast<const float4*>(&s_score[j + 4 * x]);
+        ev[x] = *reinterpret_cast<const int4*>(&s_chunk[j + 4 * x]);
+      }
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        rank += (beats(sv[x].x, ev[x].x, si, ei) ? 1 : 0) + (beats(sv[x].y, ev[x].y, si, ei) ? 1 : 0) +
+                (beats(sv[x].z, ev[x].z, si, ei) ? 1 : 0) + (beats(sv[x].w, ev[x].w, si, ei) ? 1 : 0);
+    }
     s_sel[i] = rank < kk;
   }
   __syncthreads();
@@ -291,14 +343,45 @@ __global__ void __launch_bounds__(512) score_topk_kernel(ScoreParams P) {
     if (!s_sel[i]) continue;
     const int ei = s_chunk[i];
     int pos = 0;
-    for (int j = 0; j < n; ++j) pos += (s_sel[j] && s_chunk[j] < ei) ? 1 : 0;
+    for (int j = 0; j < n16; j += 16) {
+      int4 sv[4], ev[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        sv[x] = *reinterpret_cast<const int4*>(&s_sel[j + 4 * x]);
+        ev[x] = *reinterpret_cast<const int4*>(&s_chunk[j + 4 * x]);
+      }
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        pos += (sv[x].x && ev[x].x < ei) + (sv[x].y && ev[x].y < ei) + (sv[x].z && ev[x].z < ei) +
+               (sv[x].w && ev[x].w < ei);
+    }
     if (P.idx_out) P.idx_out[(int64_t)sel * P.k + pos] = ei;
-    if (P.table) P.table[(int64_t)sel * P.table_stride + P.table_slot0 + pos] =
-        P.catalog[(int64_t)sel * P.catalog_stride + ei];
+    int rs = -1;
+    if (P.residency != nullptr) {
+      const int r = P.residency[(int64_t)sel * P.catalog_stride + ei];
+      rs = (r >= 0 && r < P.n_slots) ? r : -1;
+    }
+    if (P.res_out) P.res_out[(int64_t)sel * P.k + pos] = rs;
+    if (P.table) {
+      halo_chunk_desc d = P.catalog[(int64_t)sel * P.catalog_stride + ei];
+      if (rs >= 0) {  // rows, start, flags and batch stay the chunk's own
+        const halo_chunk_desc& sd = P.slot_catalog[(int64_t)sel * P.n_slots + rs];
+        d.k = sd.k;
+        d.v = sd.v;
+        d.k_stride_b = sd.k_stride_b;
+        d.k_stride_h = sd.k_stride_h;
+        d.k_stride_t = sd.k_stride_t;
+        d.v_stride_b = sd.v_stride_b;
+        d.v_stride_h = sd.v_stride_h;
+        d.v_stride_t = sd.v_stride_t;
+      }
+      P.table[(int64_t)sel * P.table_stride + P.table_slot0 + pos] = d;
+    }
   }
   // Unfilled slots: index -1 and an empty descriptor (T_c = 0, never read).
   for (int j = kk + tid; j < P.k; j += nthr) {
     if (P.idx_out) P.idx_out[(int64_t)sel * P.k + j] = -1;
+    if (P.res_out) P.res_out[(int64_t)sel * P.k + j] = -1;
     if (P.table) {
       halo_chunk_desc e = {};
       e.k = nullptr;
@@ -341,7 +424,7 @@ extern "C" int halo_chunk_means(const void* k, int64_t k_stride_b, int64_t k_str
   return HALO_OK;
 }
 
-extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+static int score_topk_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
                                      int B, int H, int H_kv, int D,
                                      const void* kmean, int64_t km_stride_b, int64_t km_stride_h,
                                      int64_t km_stride_p,
@@ -352,8 +435,11 @@ extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t 
                                      halo_chunk_desc* table, int64_t table_stride, int table_slot0,
                                      int normalize, float alpha, float beta, float gamma,
                                      int refresh, int sink_pages, int P_total,
-                                     void* stream) {
+                                     const int32_t* residency, const halo_chunk_desc* slot_catalog, int n_slots,
+                                     int32_t* res_out, void* stream) {
   HALO_CHECK_ARG(q && kmean && eligible, "null pointer");
+  HALO_CHECK_ARG(residency == nullptr || (slot_catalog != nullptr && n_slots >= 1 && table != nullptr),
+                 "staging needs slot_catalog, n_slots >= 1 and a table");
   HALO_CHECK_ARG(dtype == HALO_F32 || dtype == HALO_BF16 || dtype == HALO_F16, "bad dtype");
   HALO_CHECK_ARG(B > 0 && H > 0 && H_kv > 0 && H % H_kv == 0 && D > 0, "bad head sizes");
   HALO_CHECK_ARG(n_elig >= 0 && n_elig <= kMaxElig, "n_elig must be in [0, 1024]");
@@ -402,12 +488,60 @@ extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t 
   p.refresh = refresh;
   p.sink_pages = sink_pages;
   p.P_total = P_total;
+  p.residency = residency;
+  p.slot_catalog = slot_catalog;
+  p.n_slots = n_slots;
+  p.res_out = res_out;
   HALO_CHECK_ARG(!normalize || P_total > 0, "P_total must be positive when normalising");
   const int n_sel = per_row ? B : 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == HALO_F32) hipLaunchKernelGGL(score_topk_kernel<HALO_F32>, dim3(n_sel), dim3(512), 0, st, p);
-  else if (dtype == HALO_BF16) hipLaunchKernelGGL(score_topk_kernel<HALO_BF16>, dim3(n_sel), dim3(512), 0, st, p);
-  else hipLaunchKernelGGL(score_topk_kernel<HALO_F16>, dim3(n_sel), dim3(512), 0, st, p);
+#define HALO_SCORE(DTV)                                                                                    \
+  do {                                                                                                     \
+    if (D == 64) hipLaunchKernelGGL((score_topk_kernel<DTV, 64>), dim3(n_sel), dim3(512), 0, st, p);       \
+    else if (D == 128) hipLaunchKernelGGL((score_topk_kernel<DTV, 128>), dim3(n_sel), dim3(512), 0, st, p); \
+    else if (D == 256) hipLaunchKernelGGL((score_topk_kernel<DTV, 256>), dim3(n_sel), dim3(512), 0, st, p); \
+    else hipLaunchKernelGGL((score_topk_kernel<DTV, 0>), dim3(n_sel), dim3(512), 0, st, p);                \
+  } while (0)
+  if (dtype == HALO_F32) HALO_SCORE(HALO_F32);
+  else if (dtype == HALO_BF16) HALO_SCORE(HALO_BF16);
+  else HALO_SCORE(HALO_F16);
+#undef HALO_SCORE
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
+}
+
+extern "C" int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                     int B, int H, int H_kv, int D,
+                                     const void* kmean, int64_t km_stride_b, int64_t km_stride_h,
+                                     int64_t km_stride_p,
+                                     const int32_t* eligible, int64_t elig_stride,
+                                     const int32_t* n_elig_per_sel, int n_elig, int k, int per_row,
+                                     int32_t* idx_out, float* score_out,
+                                     const halo_chunk_desc* catalog, int64_t catalog_stride,
+                                     halo_chunk_desc* table, int64_t table_stride, int table_slot0,
+                                     int normalize, float alpha, float beta, float gamma,
+                                     int refresh, int sink_pages, int P_total,
+                                     void* stream) {
+  return score_topk_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, kmean, km_stride_b, km_stride_h,
+                         km_stride_p, eligible, elig_stride, n_elig_per_sel, n_elig, k, per_row, idx_out, score_out,
+                         catalog, catalog_stride, table, table_stride, table_slot0, normalize, alpha, beta, gamma,
+                         refresh, sink_pages, P_total, nullptr, nullptr, 0, nullptr, stream);
+}
+
+extern "C" int halo_chunk_score_topk_staged(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                            int B, int H, int H_kv, int D,
+                                            const void* kmean, int64_t km_stride_b, int64_t km_stride_h,
+                                            int64_t km_stride_p,
+                                            const int32_t* eligible, int64_t elig_stride,
+                                            const int32_t* n_elig_per_sel, int n_elig, int k, int per_row,
+                                            int32_t* idx_out, float* score_out,
+                                            const halo_chunk_desc* catalog, int64_t catalog_stride,
+                                            halo_chunk_desc* table, int64_t table_stride, int table_slot0,
+                                            const int32_t* residency, const halo_chunk_desc* slot_catalog,
+                                            int n_slots, int32_t* res_out, void* stream) {
+  HALO_CHECK_ARG(residency != nullptr, "residency is NULL: use halo_chunk_score_topk");
+  return score_topk_impl(q, q_stride_b, q_stride_h, dtype, B, H, H_kv, D, kmean, km_stride_b, km_stride_h,
+                         km_stride_p, eligible, elig_stride, n_elig_per_sel, n_elig, k, per_row, idx_out, score_out,
+                         catalog, catalog_stride, table, table_stride, table_slot0, 0, 1.f, 0.f, 0.f, 64, 0, 1,
+                         residency, slot_catalog, n_slots, res_out, stream);
 }

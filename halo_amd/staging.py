@@ -106,16 +106,23 @@ class ColdStaging:
         lay0 = self.layers[0]
         self.device = lay0.plan.descs.device
         self.top_k = lay0.top_k
+        # fused layers select in the attention launch (halo_select_cfg);
+        # unfused ones (beyond the fused selection's limits) run the staged
+        # scorer (halo_chunk_score_topk_staged) before the attention launch
         for li, lay in enumerate(self.layers):
-            if getattr(lay, "select_cfg", None) is None or not getattr(lay, "fused", True):
-                raise AssertionError(f"layer {li}: staging needs the fused in-kernel selection")
+            fused = getattr(lay, "select_cfg", None) is not None and getattr(lay, "fused", True)
+            if not fused and not hasattr(lay, "staging"):
+                raise AssertionError(f"layer {li}: no selection that staging can drive")
+        per_row_of = [bool(lay.select_cfg.per_row) if getattr(lay, "select_cfg", None) is not None else False
+                      for lay in self.layers]
+        self.all_fused = all(getattr(lay, "select_cfg", None) is not None for lay in self.layers)
         # the cache's unit is a selection: the layer's one selection, or one
         # per batch row of a layer with per-row selection (ragged batches)
-        self.per_row = bool(lay0.select_cfg.per_row)
+        self.per_row = per_row_of[0]
         self.sels = lay0.B if self.per_row else 1
         units = []                          # cold chunks of each unit, unit = layer * sels + row
         for li, lay in enumerate(self.layers):
-            if bool(lay.select_cfg.per_row) != self.per_row or (lay.B if self.per_row else 1) != self.sels \
+            if per_row_of[li] != self.per_row or (lay.B if self.per_row else 1) != self.sels \
                     or lay.top_k != self.top_k:
                 raise AssertionError("every layer must have the same selections per layer and top_k")
             units += [list(cold) for _, cold in lay.rows] if self.per_row else [list(lay.cold)]
@@ -149,8 +156,8 @@ class ColdStaging:
         self._dev_i32 = torch.full((U * n + L,), -1, dtype=torch.int32, device=dev)
         self.residency = self._dev_i32[:U * n].view(L, Bs * n)
         self.alloc = self._dev_i32[U * n:]
-        self.write_allocate = bool(write_allocate) and not self.per_row and self.n_slots >= self.top_k + 2 and all(
-            lay.dtype != torch.float32 for lay in self.layers)
+        self.write_allocate = bool(write_allocate) and self.all_fused and not self.per_row \
+            and self.n_slots >= self.top_k + 2 and all(lay.dtype != torch.float32 for lay in self.layers)
         # one feedback row per layer, as the selection writes it:
         # scores (sels, n) fp32 | picks (sels, k) int32 | residency used (sels, k) int32
         W = Bs * (n + 2 * k)
@@ -209,6 +216,11 @@ class ColdStaging:
                 self.chunk_bytes[ui] = 2 * nbytes[ui]
             self._slot_cat.append(descs_to_device(np.concatenate(sdescs), dev))
             cfg = lay.select_cfg
+            if cfg is None:
+                # the staged scorer writes the feedback row and the table
+                lay.idx, lay.scores = idx[li:li + 1], scores[li:li + 1]
+                lay.staging = (self.residency[li], self._slot_cat[li], self.n_slots, res[li])
+                continue
             cfg.n_slots = self.n_slots
             cfg.slot_catalog = self._slot_cat[li].data_ptr()
             cfg.residency = self.residency[li].data_ptr()

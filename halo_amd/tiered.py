@@ -75,6 +75,9 @@ class TieredDecodeLayer:
         self.idx = torch.empty((1, top_k), device=device, dtype=torch.int32)
         self.scores = torch.empty((1, max(len(cold), 1)), device=device, dtype=torch.float32)
         self.select_cfg = None
+        # (residency, slot catalog, n_slots, res_out) when an HBM staging cache
+        # serves the cold chunks of an unfused layer (set by ColdStaging)
+        self.staging = None
         if self.fused:
             km = self.kmean
             if km.shape != (B, H_kv, n_cold, D) or km.dtype != dtype or km.stride(-1) != 1:
@@ -113,7 +116,8 @@ class TieredDecodeLayer:
         """Standalone selection (``halo_chunk_score_topk``): fills idx/scores
         and the table's selection slots."""
         score_topk(q, self.kmean, self.eligible, self.top_k, catalog=self.catalog,
-                   table=self.plan.descs, table_slot0=self.slot0, idx_out=self.idx, score_out=self.scores)
+                   table=self.plan.descs, table_slot0=self.slot0, idx_out=self.idx, score_out=self.scores,
+                   staging=self.staging)
 
     def attend(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse: Optional[torch.Tensor] = None,
                q_pos: Optional[torch.Tensor] = None) -> None:

@@ -309,6 +309,32 @@ int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                           void* stream);
 
 /*
+ * halo_chunk_score_topk (raw attn scores, normalize = 0) for a layer whose
+ * cold chunks are served by an HBM staging cache: a chosen chunk p whose
+ * residency[s*catalog_stride + p] names a slot r in [0, n_slots) is written
+ * to the table with the addresses and strides of slot_catalog[s*n_slots + r]
+ * (its rows, start, flags and batch from its own catalog entry), and
+ * res_out[s*k + j] receives the entry used for the j-th chosen chunk (-1:
+ * read in place; unfilled slots -1).  The two-launch selection path (this,
+ * then halo_decode_attn over the table) of layers beyond the fused
+ * selection's limits (more than 64 cold chunks or 512 (chunk, row, KV head)
+ * triples); the same residency protocol as halo_select_cfg.  The reference
+ * selects on the host and refetches with HALORefetcher
+ * (baselines/scorer_ablations.py:218-268, halo/refetcher.py:59-114).
+ */
+int halo_chunk_score_topk_staged(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype,
+                                 int B, int H, int H_kv, int D,
+                                 const void* kmean, int64_t km_stride_b, int64_t km_stride_h,
+                                 int64_t km_stride_p,
+                                 const int32_t* eligible, int64_t elig_stride,
+                                 const int32_t* n_elig_per_sel, int n_elig, int k, int per_row,
+                                 int32_t* idx_out, float* score_out,
+                                 const halo_chunk_desc* catalog, int64_t catalog_stride,
+                                 halo_chunk_desc* table, int64_t table_stride, int table_slot0,
+                                 const int32_t* residency, const halo_chunk_desc* slot_catalog,
+                                 int n_slots, int32_t* res_out, void* stream);
+
+/*
  * Quest page metadata: channel-wise minima and maxima of `n_pages` pages of
  * `page` rows starting at row `row0`, kmin[b,h,j,:] / kmax[b,h,j,:] in the
  * key dtype (exact; a NaN in a channel propagates, as torch.amin / amax).

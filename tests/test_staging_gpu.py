@@ -328,3 +328,43 @@ def test_staged_ragged_batch_matches_all_hbm(dev):
                     c = int(holds[u, s])
                     assert torch.equal(st._slot_k[u][s].cpu(), cold[c].k), (li, b, s, c)
                     assert torch.equal(st._slot_v[u][s].cpu(), cold[c].v), (li, b, s, c)
+
+
+def test_staged_layers_beyond_the_fused_selection_limits(dev):
+    """Layers with 72 cold chunks (beyond the fused selection's 64) run the
+    two-launch path -- the staged scorer writes the chosen descriptors,
+    with a staged chunk's slot addresses, into the table, then the attention
+    launch -- and match the all-HBM layers bit for bit through the
+    benchmark's loop, with hits and misses both served."""
+    import bench
+    from halo_amd.staging import ColdStaging
+    hbm, staged, _, (H, D) = _setup(dev, L=4, n_chunks=96, chunk=64, n_hot=24, top_k=4, slots=10, keep=6,
+                                    seed=31, adjacent=True)
+    assert not staged[0].fused and not hbm[0].fused
+    L, steps, k = len(hbm), 20, 4
+    scale = 1 / math.sqrt(D)
+    st = ColdStaging(staged, n_slots=10, keep=6, max_inflight=8)
+    assert not st.all_fused and staged[0].staging is not None
+    qtraj = bench.query_trajectory(torch, dev, steps=steps, L=L, H=H, D=D, rho=0.8, seed=32)
+    out_hist = torch.zeros((steps, L, 1, H, D), device=dev, dtype=torch.bfloat16)
+    idx_hist = torch.full((steps, L, k), -7, device=dev, dtype=torch.int32)
+    res_hist = torch.full((steps, L, k), -7, device=dev, dtype=torch.int32)
+
+    def record(t, lo, hi, outs):
+        for li in range(lo, hi):
+            out_hist[t, li].copy_(outs[li])
+        idx_hist[t, lo:hi].copy_(st.idx[lo:hi])
+        res_hist[t, lo:hi].copy_(st.res_out[lo:hi])
+
+    bench.refetch_run(torch, staged, st, qtraj, warmup=0, steps=steps, scale=scale, label="unfused test",
+                      segments=2, record=record)
+    torch.cuda.synchronize()
+    assert st.hits > 0 and st.misses > 0 and st.fills > 0
+    res = res_hist.cpu().numpy()
+    assert (res >= 0).any() and (res == -1).any()
+    o_ref = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+    for t in range(steps):
+        for li in range(L):
+            hbm[li].step(qtraj[t, li], scale=scale, out=o_ref)
+            assert torch.equal(out_hist[t, li], o_ref), (t, li)
+            assert torch.equal(idx_hist[t, li], hbm[li].idx[0]), (t, li)

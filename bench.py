@@ -251,6 +251,8 @@ def refetch_run(torch, staged, staging, qtraj, *, warmup, steps, scale, label, w
         "prefetch_bytes_per_step": staging.fill_bytes / steps,
         "in_place_miss_bytes_per_step": staging.miss_bytes / steps,
         "link_bytes_per_step": link, "link_gbps": link / dt / 1e9, "segments": segments,
+        "host_us_per_step": {"plan": ns["ns_plan"] / steps / 1e3, "fill_issue": ns["ns_issue"] / steps / 1e3,
+                             "feedback_wait": ns["ns_wait"] / steps / 1e3},
     }
 
 

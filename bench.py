@@ -656,9 +656,16 @@ def bench_model_decode(torch, dev, *, new_tokens: int = 32, prompt: int = 8192):
     ref = AutoModelForCausalLM.from_config(cfg()).to(dev, torch.bfloat16).eval()
     halo = AutoModelForCausalLM.from_config(cfg()).to(dev, torch.bfloat16).eval()
     halo.load_state_dict(ref.state_dict())
-    wrap_with_halo(halo, HALOConfig(chunked=True, chunk_size=1024, recent_window=512))
+    wrap_with_halo(halo, HALOConfig(chunked=True, chunk_size=1024, recent_window=512, use_triton=True))
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(10, 1000, (1, prompt), generator=g).to(dev)
+    route_env = {"in_place": {}, "streamed": {"HALO_TRITON_STREAMED": "1"},
+                 "single_launch": {"HALO_TRITON_SINGLE_LAUNCH": "1"}}
+
+    def set_route(name):
+        for k in ("HALO_TRITON_STREAMED", "HALO_TRITON_SINGLE_LAUNCH"):
+            os.environ.pop(k, None)
+        os.environ.update(route_env[name])
 
     def timed(fn):
         torch.cuda.synchronize()
@@ -667,13 +674,20 @@ def bench_model_decode(torch, dev, *, new_tokens: int = 32, prompt: int = 8192):
         torch.cuda.synchronize()
         return time.perf_counter() - t0, r
 
+    routes = {}
     with torch.no_grad():
         prefill_then_generate(halo, ids[:, :2048], prefill_chunk_tokens=1024, max_new_tokens=2)   # warm-up
         t_pre, _ = timed(lambda: prefill_then_generate(halo, ids, prefill_chunk_tokens=2048, max_new_tokens=0))
-        t_all, res = timed(lambda: prefill_then_generate(halo, ids, prefill_chunk_tokens=2048,
-                                                         max_new_tokens=new_tokens))
+        for name in ("streamed", "single_launch", "in_place"):   # the cache's default route last
+            set_route(name)
+            prefill_then_generate(halo, ids[:, :4096], prefill_chunk_tokens=2048, max_new_tokens=2)
+            t_all, res = timed(lambda: prefill_then_generate(halo, ids, prefill_chunk_tokens=2048,
+                                                             max_new_tokens=new_tokens))
+            routes[name] = (t_all - t_pre) / new_tokens * 1e3
+            log(f"model decode, route {name}: {routes[name]:.2f} ms per token")
+        set_route("in_place")
         tele = res["cache_telemetry"]
-        halo_ms = (t_all - t_pre) / new_tokens * 1e3
+        halo_ms = routes["in_place"]
         # the same weights, SDPA over a DynamicCache held in HBM
         out = ref(ids, use_cache=True, return_dict=True)
         cache, nxt = out.past_key_values, out.logits[:, -1:].argmax(-1)
@@ -693,8 +707,10 @@ def bench_model_decode(torch, dev, *, new_tokens: int = 32, prompt: int = 8192):
         "workload": "transformers Qwen2-architecture model (random init), Llama-3-8B attention shapes (32/8 heads, "
                     "d128), 4 layers, bf16, 8192-token prompt prefilled in 2048-token slices, then greedy decode "
                     "through wrap_with_halo(chunked=True): chunk 1024, recent window 512, cold chunks in pinned host "
-                    "memory attended every step",
+                    "memory attended every step (read in place by the decode launch; the reference's streamed and "
+                    "single-launch routes beside it)",
         "decode_ms_per_token": halo_ms, "decode_tokens_per_s": 1e3 / halo_ms,
+        "decode_ms_per_token_by_route": routes,
         "prefill_ms": t_pre * 1e3, "sdpa_dynamic_cache_ms_per_token": ref_ms,
         "cold_bytes_per_token_over_link": cold_bytes,
         "telemetry": {k: (v if isinstance(v, (int, float, bool, str)) else str(v)) for k, v in tele.items()},

@@ -21,11 +21,16 @@ What changes on MI355X:
     async variant had to block the host, :86-100, :833-848);
   * pinned chunks are staged as whole byte spans (``span_to_device``), so the
     host never reads a pinned row;
-  * decode (T_q == 1) streams the cold chunks through HBM staging slots while
-    the GPU rows are attended (``halo_decode_attn`` with fp32
-    accumulators); T_q > 1 stages the cold chunks and runs one
-    ``halo_prefill_attn`` (bf16/fp16 MFMA; fp32 on the decode kernel's fp32
-    path) over them and the GPU rows;
+  * decode (T_q == 1) is one ``halo_decode_attn`` launch over the GPU rows
+    and the cold chunks read in place over the host link (no staging
+    memory, no copy); with ``use_triton`` the reference's route switches
+    pick the other two shapes of its fast path (:610-700):
+    ``HALO_TRITON_STREAMED=1`` streams the cold chunks through two HBM
+    staging buffers merged into fp32 accumulators, and
+    ``HALO_TRITON_SINGLE_LAUNCH=1`` stages the whole cold tier in HBM first
+    and attends it with the GPU rows in one launch.  T_q > 1 stages the cold
+    chunks and runs one ``halo_prefill_attn`` (bf16/fp16 MFMA; fp32 on the
+    decode kernel's fp32 path) over them and the GPU rows;
   * per-chunk fp32 key sums are accumulated at peel time, so every filled
     cold chunk has its mean key on the GPU (the page-mean metadata a chunk
     scorer reads) without touching host memory.
@@ -34,6 +39,7 @@ The cache is lossless: every cold row is attended (Path D).
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -96,8 +102,9 @@ class HALOCacheChunked(HALOCache):
         super().__init__(config=config, storage=storage, scorer=scorer, demoter=demoter, refetcher=refetcher)
         self.chunk_size = int(chunk_size)
         self.recent_window = int(recent_window)
-        # Every route of this cache runs the HIP kernels; the flag is kept
-        # because the reference reads it (halo/kv_cache_chunked.py:152-167).
+        # Every route of this cache runs the HIP kernels; as in the reference
+        # (halo/kv_cache_chunked.py:152-167, :610-660) the flag enables the
+        # route switches HALO_TRITON_SINGLE_LAUNCH / HALO_TRITON_STREAMED.
         self.use_triton = bool(use_triton)
         self._mode = "warmup"
         self._cold: dict = {}
@@ -158,6 +165,10 @@ class HALOCacheChunked(HALOCache):
         return (cold.rows if cold is not None else 0) + self._rows(k)
 
     def reset(self) -> None:
+        if self._cold and torch.cuda.is_available():
+            # decode launches read the pinned chunks in place: they must be
+            # done before the chunks go back to the host allocator
+            torch.cuda.synchronize()
         super().reset()
         self._cold.clear()
         self._gpu_pos.clear()
@@ -328,7 +339,8 @@ class HALOCacheChunked(HALOCache):
         stats = ChunkedAttentionStats(hot_positions=T_gpu, cold_positions=T_cold, chunk_size=self.chunk_size,
                                       n_chunks=len(chunks) + (1 if T_gpu else 0))
         stats.used_lse_merge = stats.n_chunks > 1
-        if T_q == 1:
+        route = self.decode_route(T_q) if chunks else "in_place"
+        if T_q == 1 and route == "streamed":
             q3 = q[:, :, 0, :]
             qp = torch.full((B,), q0, dtype=torch.int64).to(q.device, non_blocking=True)
             m, l, o = init_acc(B=B, H=H, D_v=D, device=q.device)
@@ -336,37 +348,47 @@ class HALOCacheChunked(HALOCache):
                 plan = build_plan(B=B, H=H, H_kv=hot[0].k.shape[1], D=D, dtype=hot[0].k.dtype, chunks=hot,
                                   device=q.device)
                 launch(plan, q3, scale=scale, q_pos=qp, m=m, l=l, o=o, acc_mode=2)
-            if chunks:
-                entries = [(c.k, c.v, self._cold_runs(c, q0, last_q)) for c in chunks]
-                stats.dma_bytes = stream_cold_chunks(q3, entries, scale=scale, q_pos=qp, m=m, l=l, o=o,
-                                                     after=cold.ready)
-                stats.peak_staging_bytes = 2 * max(2 * span_elems(c.k) * c.k.element_size() for c in chunks)
+            entries = [(c.k, c.v, self._cold_runs(c, q0, last_q)) for c in chunks]
+            stats.dma_bytes = stream_cold_chunks(q3, entries, scale=scale, q_pos=qp, m=m, l=l, o=o,
+                                                 after=cold.ready)
+            stats.peak_staging_bytes = 2 * max(2 * span_elems(c.k) * c.k.element_size() for c in chunks)
             res = finalize(m=m, l=l, o=o, out_dtype=q.dtype, return_lse=return_lse)
             res = (res[0].unsqueeze(2), res[1].unsqueeze(2)) if return_lse else res.unsqueeze(2)
-        else:
-            staged = []
-            if chunks:
-                cs = copy_stream(q.device)
-                if cold.ready is not None:
-                    cs.wait_event(cold.ready)
-                cs.wait_stream(torch.cuda.current_stream(q.device))
-                bufs = []
-                for c in chunks:  # allocated on the compute stream, which reads them
-                    kb = torch.empty(span_elems(c.k), dtype=c.k.dtype, device=q.device)
-                    vb = torch.empty(span_elems(c.v), dtype=c.v.dtype, device=q.device)
-                    bufs.append((c, kb, vb))
-                with torch.cuda.stream(cs):
-                    bufs = [(c, span_to_device(c.k, kb), span_to_device(c.v, vb), kb, vb) for c, kb, vb in bufs]
-                    ev = torch.cuda.Event()
-                    ev.record(cs)
-                torch.cuda.current_stream(q.device).wait_event(ev)
-                for c, kd, vd, kb, vb in bufs:
-                    kb.record_stream(cs)
-                    vb.record_stream(cs)
-                    for lo, hi, start, causal in self._cold_runs(c, q0, last_q):
-                        staged.append(ChunkRef(kd[..., lo:hi, :], vd[..., lo:hi, :], start, causal))
-                    stats.dma_bytes += 2 * kb.numel() * kb.element_size()
+        elif T_q == 1:
+            # one launch over the GPU rows and the cold chunks: read in place
+            # over the host link, or (single_launch) staged in HBM first
+            compute = torch.cuda.current_stream(q.device)
+            if route == "single_launch":
+                cold_refs = self._stage_cold(chunks, cold, q, q0, last_q, stats)
                 stats.peak_staging_bytes = stats.dma_bytes
+                stats.n_chunks = 1
+                stats.used_lse_merge = False
+            else:
+                if cold is not None and cold.ready is not None:
+                    compute.wait_event(cold.ready)   # the peel's copies into the pinned chunks
+                cold_refs = [ChunkRef(c.k[..., lo:hi, :], c.v[..., lo:hi, :], start, causal)
+                             for c in chunks for lo, hi, start, causal in self._cold_runs(c, q0, last_q)]
+                stats.dma_bytes = sum(2 * (hi - lo) * c.k.shape[0] * c.k.shape[1] * c.k.shape[-1] *
+                                      c.k.element_size()
+                                      for c in chunks for lo, hi, _, _ in self._cold_runs(c, q0, last_q))
+            q3 = q[:, :, 0, :]
+            qp = torch.full((B,), q0, dtype=torch.int64).to(q.device, non_blocking=True)
+            all_chunks = cold_refs + hot
+            out = torch.empty((B, H, D), dtype=q.dtype, device=q.device)
+            lse = torch.empty((B, H), dtype=torch.float32, device=q.device) if return_lse else None
+            if all_chunks:
+                ref = all_chunks[0]
+                plan = build_plan(B=B, H=H, H_kv=ref.k.shape[1], D=D, dtype=ref.k.dtype, chunks=all_chunks,
+                                  device=q.device)
+                launch(plan, q3, scale=scale, q_pos=qp, out=out, lse=lse)
+            else:
+                out.zero_()
+                if lse is not None:
+                    lse.fill_(float("-inf"))
+            res = (out.unsqueeze(2), lse.unsqueeze(2)) if return_lse else out.unsqueeze(2)
+        else:
+            staged = self._stage_cold(chunks, cold, q, q0, last_q, stats) if chunks else []
+            stats.peak_staging_bytes = stats.dma_bytes
             all_chunks = staged + hot
             if not all_chunks:
                 out = torch.zeros(B, H, T_q, D, dtype=q.dtype, device=q.device)
@@ -381,6 +403,51 @@ class HALOCacheChunked(HALOCache):
         if self.refetcher is not None and hasattr(self.refetcher, "count_hits"):
             self.refetcher.count_hits(blocks)
         return res
+
+    def decode_route(self, T_q: int = 1) -> str:
+        """Shape of a decode call's cold-tier traffic, read per call as the
+        reference reads its switches (halo/kv_cache_chunked.py:610-660,
+        851-862): "single_launch" (``use_triton`` and
+        HALO_TRITON_SINGLE_LAUNCH=1, checked first), "streamed"
+        (``use_triton`` and HALO_TRITON_STREAMED=1), else "in_place"."""
+        if T_q != 1 or not self.use_triton:
+            return "in_place"
+        if os.environ.get("HALO_TRITON_SINGLE_LAUNCH", "0") == "1":
+            return "single_launch"
+        if os.environ.get("HALO_TRITON_STREAMED", "0") == "1":
+            return "streamed"
+        return "in_place"
+
+    def _stage_cold(self, chunks, cold, q: torch.Tensor, q0: int, last_q: int, stats) -> list:
+        """Copy every cold chunk's byte span to HBM on the tier copy stream
+        (behind the peel's event) and make the compute stream wait for the
+        copies; returns the staged rows as chunk refs and adds the copied
+        bytes to ``stats.dma_bytes``."""
+        from .decode import ChunkRef
+
+        cs = copy_stream(q.device)
+        compute = torch.cuda.current_stream(q.device)
+        if cold.ready is not None:
+            cs.wait_event(cold.ready)
+        cs.wait_stream(compute)
+        bufs = []
+        for c in chunks:  # allocated on the compute stream, which reads them
+            kb = torch.empty(span_elems(c.k), dtype=c.k.dtype, device=q.device)
+            vb = torch.empty(span_elems(c.v), dtype=c.v.dtype, device=q.device)
+            bufs.append((c, kb, vb))
+        with torch.cuda.stream(cs):
+            bufs = [(c, span_to_device(c.k, kb), span_to_device(c.v, vb), kb, vb) for c, kb, vb in bufs]
+            ev = torch.cuda.Event()
+            ev.record(cs)
+        compute.wait_event(ev)
+        staged = []
+        for c, kd, vd, kb, vb in bufs:
+            kb.record_stream(cs)
+            vb.record_stream(cs)
+            for lo, hi, start, causal in self._cold_runs(c, q0, last_q):
+                staged.append(ChunkRef(kd[..., lo:hi, :], vd[..., lo:hi, :], start, causal))
+            stats.dma_bytes += 2 * kb.numel() * kb.element_size()
+        return staged
 
     @staticmethod
     def _cold_runs(c: _ColdChunk, q0: int, last_q: int):

@@ -151,3 +151,51 @@ def test_cold_chunk_means_on_device(dev):
     for j, a in enumerate(range(0, n, 128)):
         want = ks[:, :, a:min(a + 128, n)].astype(np.float64).mean(axis=-2)
         assert np.abs(got[:, :, j] - want).max() <= 2.0 ** -7 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("route", ["in_place", "streamed", "single_launch"])
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float32, 1e-5)])
+def test_decode_routes(dev, monkeypatch, route, dtype, tol):
+    """The three decode routes (halo/kv_cache_chunked.py:610-700): cold
+    chunks read in place by one launch (default), streamed through HBM
+    staging buffers (use_triton + HALO_TRITON_STREAMED=1), staged whole then
+    one launch (use_triton + HALO_TRITON_SINGLE_LAUNCH=1); each right after a
+    peel on a busy stream, against the float64 closed form, with the
+    route's telemetry."""
+    from halo_amd import HALOCacheChunked
+    monkeypatch.delenv("HALO_TRITON_STREAMED", raising=False)
+    monkeypatch.delenv("HALO_TRITON_SINGLE_LAUNCH", raising=False)
+    if route == "streamed":
+        monkeypatch.setenv("HALO_TRITON_STREAMED", "1")
+    if route == "single_launch":
+        monkeypatch.setenv("HALO_TRITON_SINGLE_LAUNCH", "1")
+        monkeypatch.setenv("HALO_TRITON_STREAMED", "1")   # single launch is checked first
+    rng = np.random.default_rng(17)
+    B, H, H_kv, D = 2, 8, 2, 128
+    T = 1400
+    ks, vs = _rows(rng, (B, H_kv, T, D), dtype), _rows(rng, (B, H_kv, T, D), dtype)
+    kg = torch.from_numpy(ks).to(dev).to(dtype)
+    vg = torch.from_numpy(vs).to(dev).to(dtype)
+    cache = HALOCacheChunked(chunk_size=256, recent_window=64, use_triton=True)
+    assert cache.decode_route() == route
+    cache.update(kg[:, :, :T - 2], vg[:, :, :T - 2], 0)
+    torch.cuda.synchronize()
+    _busy(dev)
+    esz = torch.tensor([], dtype=dtype).element_size()
+    for t in (T - 2, T - 1):       # the transition peel, then a plain decode step
+        cache.update(kg[:, :, t:t + 1], vg[:, :, t:t + 1], 0)
+        q1 = _rows(rng, (B, H, 1, D), dtype)
+        out, lse = cache.compute_attention(torch.from_numpy(q1).to(dev).to(dtype), layer_idx=0, return_lse=True)
+        w, wl = A.attention_f64(q1[:, :, 0], ks[:, :, :t + 1], vs[:, :, :t + 1], scale=1 / math.sqrt(D))
+        assert np.abs(out[:, :, 0].float().cpu().numpy() - w).max() <= tol, (route, t)
+        assert np.abs(lse[:, :, 0].cpu().numpy() - wl).max() <= (1e-5 if dtype == torch.float32 else 1e-2)
+        st = cache.last_stats
+        cold_rows = cache._cold[0].rows
+        assert st.cold_positions == cold_rows and st.hot_positions == t + 1 - cold_rows
+        if route == "in_place":
+            assert st.dma_bytes == 2 * cold_rows * B * H_kv * D * esz and st.peak_staging_bytes == 0
+        elif route == "single_launch":
+            assert st.n_chunks == 1 and not st.used_lse_merge
+            assert st.dma_bytes >= 2 * cold_rows * B * H_kv * D * esz and st.peak_staging_bytes == st.dma_bytes
+        else:
+            assert st.dma_bytes >= 2 * cold_rows * B * H_kv * D * esz and st.peak_staging_bytes > 0

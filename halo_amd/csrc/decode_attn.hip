@@ -1594,6 +1594,10 @@ __device__ __forceinline__ void write_partial_owners(const DecodeParams& P, int 
 }
 
 
+// Slack (log2 units) by which a block pair's max may exceed the running max
+// before the running max moves.
+constexpr float kKiviLazyMax = 8.0f;
+
 template <int DT, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kivi_kernel(DecodeParams P) {
@@ -1712,6 +1716,9 @@ decode_attn_kivi_kernel(DecodeParams P) {
   for (int gg = 0; gg < (DT == HALO_F16 ? NG : 1); ++gg) accz[gg] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_lane = -INFINITY;  // running max of head hl (equal on its 4 lanes)
   float l_lane = 0.f;        // this lane's share of head hl's denominator
+  // Lanes of heads past the group's live heads score -inf, so their
+  // probabilities are exact zeros without a select per P register.
+  const float zbias = hl < nvalid_h ? 0.f : -INFINITY;
   // One block pair staged at bkp, first token tokp: the score MFMAs of both
   // blocks are independent and issue together, one online-softmax step
   // covers their 64 tokens (one max, one rescale), and the P.V MFMAs of
@@ -1756,7 +1763,7 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) zs[pb][c] = sz[pb][c] * P.scale2;
+      for (int c = 0; c < 4; ++c) zs[pb][c] = __builtin_fmaf(sz[pb][c], P.scale2, zbias);
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
@@ -1779,9 +1786,13 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) bm = fmaxf(bm, sv[pb][nb][c]);
     bm = rows4_max(bm);
-    const float m_new = fmaxf(m_lane, bm);
+    // Lazy running max: it moves only when the pair's max exceeds it by more
+    // than kKiviLazyMax (probabilities stay below 2^8), so the accumulators
+    // are rescaled only then; out = o / l and lse = m + log2(l) use the same m.
+    const float m_old = m_lane;
+    const float m_new = (bm > m_old + kKiviLazyMax) ? bm : m_old;
     const float ms = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_lane - ms);
+    const float alpha = __builtin_amdgcn_exp2f(m_old - ms);
     m_lane = m_new;
     // P operand of block pb in registers: the block's V slots 8kg..8kg+7 are
     // tokens {4kg + c, 16 + 4kg + c} (c = 0..3), exactly this lane's scores
@@ -1797,13 +1808,13 @@ decode_attn_kivi_kernel(DecodeParams P) {
           p8[4 * nb + c] = __builtin_amdgcn_exp2f(sv[pb][nb][c] - ms);
           psum += p8[4 * nb + c];
         }
-      pa[pb] = hl < REP ? make_uint4(pack2<DT>(p8[0], p8[1]), pack2<DT>(p8[2], p8[3]), pack2<DT>(p8[4], p8[5]),
-                                     pack2<DT>(p8[6], p8[7]))
-                        : make_uint4(0, 0, 0, 0);
+      pa[pb] = make_uint4(pack2<DT>(p8[0], p8[1]), pack2<DT>(p8[2], p8[3]), pack2<DT>(p8[4], p8[5]),
+                          pack2<DT>(p8[6], p8[7]));
     }
     l_lane = l_lane * alpha + psum;
     // ---- P.V: per block and group, codes against p*s and the zeros against p
-    if (__builtin_amdgcn_read_exec() & __ballot(hl < REP && alpha != 1.f)) {  // some head's max moved
+    // (a head whose max was -inf holds zero accumulators: nothing to rescale)
+    if (__builtin_amdgcn_read_exec() & __ballot(m_new != m_old && m_old != -INFINITY)) {  // some head's max moved
       // the output rows of this lane are heads 4kg + e; head r's factor sits on lane r
       float ar[REP];
 #pragma unroll

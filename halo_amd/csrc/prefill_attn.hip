@@ -415,6 +415,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    // past the last tile the scores came from a stale (or never filled)
+    // stage: no max to take from them
+    if (!c1.valid) bm = -INFINITY;
     float m_old;
     const bool moved = take_max(bm, m_old);
     if (__builtin_amdgcn_read_exec() & __ballot(moved)) {

@@ -27,9 +27,11 @@
 //    would otherwise read it over the link);
 //  * evictions are decided only for layers whose feedback rows came back:
 //    every launch of such a layer has finished (the feedback copy ran
-//    behind it) and its next launch is not enqueued yet, so the -1 store on
-//    the compute stream precedes every later read and the slot can take a
-//    fill at once.
+//    behind it) and its next launch is not enqueued yet, so the slot can
+//    take a fill at once; the -1 store waits for the layer's next
+//    halo_staging_before and goes out in the same batched store as that
+//    call's commits (one small launch per segment instead of two), ahead of
+//    them, so it precedes every later read.
 #include <algorithm>
 #include <chrono>
 #include <numeric>
@@ -71,6 +73,10 @@ struct halo_staging {
   // scratch reused across calls
   std::vector<int64_t> idx_buf;
   std::vector<int32_t> val_buf;
+  // eviction stores held for the unit's next halo_staging_before
+  std::vector<int64_t> def_idx;
+  std::vector<int32_t> def_val;
+  std::vector<int> def_unit;
 
   int64_t& slot_of_at(int u, int c) { return slot_of[(size_t)u * n + c]; }
   int8_t& state_at(int u, int s) { return state[(size_t)u * S + s]; }
@@ -101,6 +107,26 @@ bool stream_busy(hipStream_t s) {
     return true;
   }
   return false;
+}
+
+// Move the held eviction stores of units [ulo, uhi) into the store batch
+// (ahead of any commit added after them).
+void take_deferred(halo_staging* h, int ulo, int uhi) {
+  size_t w = 0;
+  for (size_t i = 0; i < h->def_idx.size(); ++i) {
+    if (ulo <= h->def_unit[i] && h->def_unit[i] < uhi) {
+      h->idx_buf.push_back(h->def_idx[i]);
+      h->val_buf.push_back(h->def_val[i]);
+    } else {
+      h->def_idx[w] = h->def_idx[i];
+      h->def_val[w] = h->def_val[i];
+      h->def_unit[w] = h->def_unit[i];
+      ++w;
+    }
+  }
+  h->def_idx.resize(w);
+  h->def_val.resize(w);
+  h->def_unit.resize(w);
 }
 
 int store(halo_staging* h, hipStream_t compute) {
@@ -240,8 +266,9 @@ int plan(halo_staging* h, const std::vector<int>& units, const std::vector<float
   bool evicted = false;
   auto evict = [&](int u, int s) {
     const int64_t c = h->holds_at(u, s);
-    h->idx_buf.push_back((int64_t)u * n + c);
-    h->val_buf.push_back(-1);
+    h->def_idx.push_back((int64_t)u * n + c);
+    h->def_val.push_back(-1);
+    h->def_unit.push_back(u);
     h->slot_of_at(u, (int)c) = -1;
     h->state_at(u, s) = kFree;
     h->holds_at(u, s) = -1;
@@ -302,8 +329,6 @@ int plan(halo_staging* h, const std::vector<int>& units, const std::vector<float
   }
   if (evicted) {
     if (h->track_busy && stream_busy(compute)) h->st.evictions_while_busy += 1;
-    const int rc = store(h, compute);
-    if (rc != HALO_OK) return rc;
     reserve_wa(h);
   }
   if (!fills.empty() && h->track_busy && stream_busy(compute)) h->st.fills_while_busy += 1;
@@ -412,6 +437,7 @@ extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream
   HALO_CHECK_ARG(h != nullptr && 0 <= lo && lo <= hi && hi <= h->L, "bad staging segment");
   hipStream_t compute = static_cast<hipStream_t>(stream);
   const int ulo = lo * h->B, uhi = hi * h->B;
+  take_deferred(h, ulo, uhi);
   std::vector<Pending> rest;
   rest.reserve(h->pending.size());
   bool any = false;
@@ -509,10 +535,17 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
     }
     h->seen += 1;
   }
-  if (units.empty()) return HALO_OK;
-  const int64_t t0 = now_ns();
-  const int rc = plan(h, units, scores, compute);
-  h->st.ns_plan += now_ns() - t0;
+  int rc = HALO_OK;
+  if (!units.empty()) {
+    const int64_t t0 = now_ns();
+    rc = plan(h, units, scores, compute);
+    h->st.ns_plan += now_ns() - t0;
+  }
+  if (rc == HALO_OK && lag == 0) {
+    // a full drain leaves the device residency equal to the host's
+    take_deferred(h, 0, h->U);
+    rc = store(h, compute);
+  }
   return rc;
 }
 
@@ -521,6 +554,9 @@ extern "C" int halo_staging_reset(halo_staging* h) {
   for (auto e : h->ring_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
   for (auto e : h->fill_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
   h->pending.clear();
+  h->def_idx.clear();
+  h->def_val.clear();
+  h->def_unit.clear();
   h->seen = h->queued;
   std::fill(h->slot_of.begin(), h->slot_of.end(), -1);
   std::fill(h->last_rank.begin(), h->last_rank.end(), (int64_t)h->n);

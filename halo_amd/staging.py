@@ -36,10 +36,11 @@ Ordering (no kernel observes a change while it runs):
     otherwise read over the link): the compute stream waits for its copy;
   * evictions are decided only for layers whose feedback just came back:
     every launch of such a layer has finished (its feedback copy ran behind
-    it) and its next launch is not enqueued yet.  So an eviction stores -1
-    on the compute stream and the slot can take a fill at once: the store
-    runs before any later launch of the layer, and the new chunk's entry is
-    committed only after it.
+    it) and its next launch is not enqueued yet.  So the slot can take a
+    fill at once, and the eviction's -1 store goes out with the layer's next
+    ``before_step`` batch, ahead of that batch's commits: it runs before any
+    later launch of the layer, and the new chunk's entry is committed only
+    after it (``drain`` flushes the stores still held).
 A step may run as consecutive segments of layers (one graph each): a
 segment's scores are planned while the later segments execute, so the
 scores of step t can decide that segment's residency from step t + 1 on.

@@ -445,17 +445,16 @@ extern "C" int halo_staging_before(halo_staging* h, int lo, int hi, void* stream
     bool take = false;
     if (ulo <= p.unit && p.unit < uhi) {
       hipEvent_t ev = h->fill_ev[(size_t)p.unit * h->S + p.slot];
-      if (p.urgent) {
-        HALO_CHECK_HIP(hipStreamWaitEvent(compute, ev, 0));
-        take = true;
+      const hipError_t e = hipEventQuery(ev);
+      if (e == hipSuccess) {
+        take = true;  // landed: a plain commit
+      } else if (e != hipErrorNotReady) {
+        HALO_CHECK_HIP(e);
       } else {
-        const hipError_t e = hipEventQuery(ev);
-        if (e == hipSuccess) {
+        (void)hipGetLastError();
+        if (p.urgent) {  // still in flight: the compute stream waits for it
+          HALO_CHECK_HIP(hipStreamWaitEvent(compute, ev, 0));
           take = true;
-        } else if (e != hipErrorNotReady) {
-          HALO_CHECK_HIP(e);
-        } else {
-          (void)hipGetLastError();
         }
       }
     }

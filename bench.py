@@ -915,22 +915,27 @@ def main() -> int:
         result["refetch_sweep"] = sweep
     if not args.no_extra:
         extra = {}
-        log("prefill leg")
-        extra["prefill_c3"] = bench_prefill_c3(torch, dev, reps=10)
-        log("ragged leg")
-        extra["ragged_c4"] = bench_ragged_c4(torch, dev, steps=20)
-        log("drop-in API leg")
-        extra["dropin_c2"] = bench_dropin_c2(torch, dev, layers, qs, top_k=top_k, steps=20)
-        log("kivi leg")
+
+        def leg(key, label, fn):
+            # a leg that raises is recorded with its error; the line still prints
+            log(label)
+            try:
+                extra[key] = fn()
+            except Exception as e:  # noqa: BLE001 -- reported in the JSON line
+                log(f"{label} failed: {type(e).__name__}: {e}")
+                extra[key] = {"error": f"{type(e).__name__}: {e}"}
+                torch.cuda.synchronize()
+                torch.cuda.empty_cache()
+
+        leg("prefill_c3", "prefill leg", lambda: bench_prefill_c3(torch, dev, reps=10))
+        leg("ragged_c4", "ragged leg", lambda: bench_ragged_c4(torch, dev, steps=20))
+        leg("dropin_c2", "drop-in API leg", lambda: bench_dropin_c2(torch, dev, layers, qs, top_k=top_k, steps=20))
         del staging, staged
         torch.cuda.empty_cache()
-        extra["kivi_c5"] = bench_kivi_c5(torch, dev, steps=20)
-        log("ragged host-tier leg")
-        extra["ragged_c4_host_tier"] = bench_ragged_c4_host(torch, dev, steps=40)
-        log("model decode leg")
-        extra["model_decode"] = bench_model_decode(torch, dev)
-        log("long-context leg")
-        extra["long_context_128k"] = bench_long_context(torch, dev)
+        leg("kivi_c5", "kivi leg", lambda: bench_kivi_c5(torch, dev, steps=20))
+        leg("ragged_c4_host_tier", "ragged host-tier leg", lambda: bench_ragged_c4_host(torch, dev, steps=40))
+        leg("model_decode", "model decode leg", lambda: bench_model_decode(torch, dev))
+        leg("long_context_128k", "long-context leg", lambda: bench_long_context(torch, dev))
         result["extra"] = extra
     if not args.no_cpu_baseline:
         log("cpu baseline")

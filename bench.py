@@ -597,18 +597,23 @@ def bench_long_context(torch, dev, *, steps: int = 60, warmup: int = 10, L: int 
                        keep: int = 6, rho: float = 0.98):
     """C2's layer shape at a 131072-token context: 128 chunks of 1024 rows,
     32 hot (25 %) in HBM, 96 cold in pinned host memory, top-4 per layer per
-    step -- beyond the fused selection's 64 cold chunks, so each layer is the
-    two-launch path (the staged scorer, then the attention launch and its
-    merge) -- served by the HBM staging cache; L distinct layers, AR(1)
-    query drift.  Beside it the same layers with every chunk in HBM."""
+    step (96 x 8 = 768 (chunk, KV head) candidates: the fused selection's
+    widest catalog), served by the HBM staging cache; L distinct layers,
+    AR(1) query drift.  Beside it the same layers with every chunk in HBM,
+    fused and on the two-launch path (standalone scorer, then the attention
+    launch and its merge)."""
     H, H_kv, D, T, chunk, n_hot, top_k = 32, 8, 128, 131072, 1024, 32, 4
     from halo_amd.staging import ColdStaging
     from halo_amd.tiered import TieredDecodeLayer
     layers, qs, _ = make_layers(torch, L=L, H=H, H_kv=H_kv, D=D, T=T, chunk=chunk, n_hot=n_hot, top_k=top_k,
                                 n_planted=4, sigma=8.0, dev=dev, seed=7)
-    assert not layers[0].fused
+    assert layers[0].fused
     scale = 1.0 / math.sqrt(D)
     attn_avg, _ = kernel_level_c2(torch, layers, qs, scale=scale, reps=20, with_scorer=False)
+    two = [TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=lay.hot, cold=lay.cold,
+                             top_k=top_k, device=dev, cold_kmean=lay.kmean, fused=False) for lay in layers]
+    two_avg, _ = kernel_level_c2(torch, two, qs, scale=scale, reps=20, with_scorer=False)
+    del two
     tiers = host_tier(torch, layers)
     staged = [TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=lay.hot, cold=tiers[li],
                                 top_k=top_k, device=dev, cold_kmean=lay.kmean) for li, lay in enumerate(layers)]
@@ -620,11 +625,12 @@ def bench_long_context(torch, dev, *, steps: int = 60, warmup: int = 10, L: int 
     layer_bytes = rows * H_kv * D * 2 * 2 + 2 * H * D * 2 + H * 4 + (T // chunk - n_hot) * H_kv * D * 2
     out = {
         "workload": f"Llama-3-8B-shaped GQA decode at 131072 tokens: {L} layers, 128 chunks of 1024 rows, 32 hot in "
-                    f"HBM + top-4 of 96 cold chunks in pinned host memory per layer per step (staged scorer + "
+                    f"HBM + top-4 of 96 cold chunks in pinned host memory per layer per step (selection fused in the "
                     f"attention launch), HBM staging cache of {slots} slots (keep {keep}), AR(1) drift rho {rho}",
         "layers": L, "hbm_resident_fraction": (n_hot + slots) / (T // chunk),
         "all_hbm_us_per_layer": attn_avg * 1e3,
         "all_hbm_gbps": layer_bytes / (attn_avg * 1e-3) / 1e9,
+        "all_hbm_two_launch_us_per_layer": two_avg * 1e3,
         "staged_us_per_layer": rd["ms_per_step"] * 1e3 / L,
         **{k: v for k, v in rd.items() if k != "tokens_per_s"},
     }

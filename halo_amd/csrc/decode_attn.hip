@@ -59,6 +59,7 @@ struct DecodeParams {
   float* ws_o;   // [n_work][REP][D]  per-item partial o (unnormalised)
   float* ws_ml;  // [n_work][REP][2]  per-item (m in log2 units, l)
   int sel_on;     // fused chunk selection (halo_decode_attn_tiered)
+  int sel_wide;   // the selection needs the wide form (more than 64 candidates or 512 triples)
   float inv_rep;  // fp32(1/rep): the GQA query-mean factor
   halo_select_cfg sel;
 };
@@ -245,17 +246,27 @@ __device__ __forceinline__ void pv_pair(const uint4& va, const uint4& vb, const 
 // trip; workgroups the launch marks as leading slot items issue those loads
 // before reading their work record.
 // ---------------------------------------------------------------------------
-constexpr int kSelMaxCold = 64;
-constexpr int kSelTPT = 2;  // (page, row, head) triples per thread: at most 2 x 256 per selection
+// Candidates and (chunk, row, KV head) triples one fused selection takes:
+// the narrow form (64 and 512) serves most layers; the wide form (128 and
+// 768: two ranking waves, more descriptor words per thread, 16-bit K/V only)
+// is a kernel of its own, so layers within the narrow limits do not carry
+// its costs.
+constexpr int kSelMaxColdNarrow = 64, kSelMaxTriplesNarrow = 512;
+constexpr int kSelMaxColdWide = 128, kSelMaxTriplesWide = 768;
 static_assert(sizeof(halo_chunk_desc) % 8 == 0, "descriptors are copied as 8-byte words");
 constexpr int kSelMaxQbar = 2048;
 constexpr int kSelQbarLds = kSelMaxQbar + 4 * 64;  // padded rows: at most 2048 / 64 rows of +4 floats
 constexpr int kSelMaxSlots = 64;  // HBM staging slots per selection
 // LDS of the selection: q-bar rows, dot products, scores, picks, then the
 // candidate descriptors, the staging-slot descriptors right after them (so
-// entry kSelMaxCold + r of the combined table is slot r) and the residency.
-constexpr int kSelCatOff = kSelQbarLds * 4 + (kSelTPT + 3) * 256 * 4;
-constexpr int kSelBytes = kSelCatOff + (kSelMaxCold + kSelMaxSlots) * (int)sizeof(halo_chunk_desc) + kSelMaxCold * 4;
+// entry max_cold + r of the combined table is slot r) and the residency.
+template <bool WIDE>
+struct SelCap {
+  static constexpr int max_cold = WIDE ? kSelMaxColdWide : kSelMaxColdNarrow;
+  static constexpr int tpt = (WIDE ? kSelMaxTriplesWide : kSelMaxTriplesNarrow) / 256;  // triples per thread
+  static constexpr int cat_off = kSelQbarLds * 4 + (tpt + 3) * 256 * 4;
+  static constexpr int bytes = cat_off + (max_cold + kSelMaxSlots) * (int)sizeof(halo_chunk_desc) + max_cold * 4;
+};
 static_assert(sizeof(halo_select_cfg) == 128, "halo_select_cfg layout");
 
 __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d) {
@@ -282,8 +293,9 @@ __device__ __forceinline__ halo_chunk_desc uniform_desc(const halo_chunk_desc& d
   return u;
 }
 
-template <int DT, int D, int NT>
+template <int DT, int D, int NT, bool WIDE>
 struct Selector {
+  using Cap = SelCap<WIDE>;
   using E = Elem<DT>;
   static constexpr int EP = E::per16;
   static constexpr int PIECES = D / EP;                               // 16-byte pieces per row
@@ -291,7 +303,7 @@ struct Selector {
   static_assert(D % 16 == 0, "dot-product slices");
   static constexpr int QP = (kSelMaxQbar / EP + NT - 1) / NT;         // q-bar pieces per thread
   static constexpr int DW2 = (int)sizeof(halo_chunk_desc) / 8;        // 8-byte words per descriptor
-  static constexpr int CW = (kSelMaxCold * DW2 + NT - 1) / NT;        // descriptor words per thread
+  static constexpr int CW = (Cap::max_cold * DW2 + NT - 1) / NT;      // descriptor words per thread
   static constexpr int QB = EP == 8 ? 8 : 4;                          // query heads summed per load batch (LDS path)
   static constexpr int QS = D + 4;                                    // q-bar row stride in LDS (floats)
   // Dot products are cut into units: unit u = (triple t = u / G, slice
@@ -408,18 +420,18 @@ struct Selector {
   // order, then a balanced pairwise tree over the slices), max over (row, KV
   // head), rank by (score desc, index asc).  Returns the chunk index p for
   // `slot` (-1: slot past the eligible count); the chunk's catalog entry is
-  // left in LDS at kSelCatOff and staged_slot names the staging slot that
-  // holds it (-1: none; its descriptor is entry kSelMaxCold + staged_slot).
+  // left in LDS at Cap::cat_off and staged_slot names the staging slot that
+  // holds it (-1: none; its descriptor is entry Cap::max_cold + staged_slot).
   __device__ __forceinline__ int finish(const DecodeParams& P, char* smem, int slot, bool writer) {
     const halo_select_cfg& S = P.sel;
     const int tid = threadIdx.x;
     const int H_kv = P.H_kv, rep = P.rep;
     float* s_qbar = reinterpret_cast<float*>(smem);  // rows of QS floats (padded: conflict-free reads)
     float* s_dot = s_qbar + kSelQbarLds;
-    float* s_sc = s_dot + kSelTPT * 256;  // per-candidate scores for the ranking (64, -inf past n)
-    int* s_pick = reinterpret_cast<int*>(s_dot + (kSelTPT + 2) * 256);
+    float* s_sc = s_dot + Cap::tpt * 256;  // per-candidate scores for the ranking (-inf past n)
+    int* s_pick = reinterpret_cast<int*>(s_dot + (Cap::tpt + 2) * 256);
     halo_chunk_desc* s_cat = reinterpret_cast<halo_chunk_desc*>(s_pick + 256);
-    halo_chunk_desc* s_slot = s_cat + kSelMaxCold;
+    halo_chunk_desc* s_slot = s_cat + Cap::max_cold;
     int* s_res = reinterpret_cast<int*>(s_slot + kSelMaxSlots);
     // GQA-mean query rows: fp32 sum over the rep heads in head order, times
     // fp32(1/rep), one rounding to the q dtype (rep == 1: q itself).
@@ -576,57 +588,75 @@ struct Selector {
       const int u0 = k * NT;
       if (u0 < n_units && tid + u0 < n_units) unit(tid + u0, kb[k]);
     }
-    for (int u0 = KU * NT; u0 < n_units; u0 += NT) {
-      const int u = tid + u0;
-      if (u < n_units) {
-        uint4 pc[PPS];
-        const char* row = km_row(S, u / G, H_kv);
+    // units past the first KU per thread (more than 192 triples at G = 8):
+    // one at a time in the narrow form, in the wide form batches of KU units
+    // per thread, every load of a batch issued first
+    if constexpr (!WIDE) {
+      for (int u0 = KU * NT; u0 < n_units; u0 += NT) {
+        const int u = tid + u0;
+        if (u < n_units) {
+          uint4 pc[PPS];
+          const char* row = km_row(S, u / G, H_kv);
 #pragma unroll
-        for (int j = 0; j < PPS; ++j) pc[j] = *reinterpret_cast<const uint4*>(row + (u % G + j * G) * 16);
-        unit(u, pc);
+          for (int j = 0; j < PPS; ++j) pc[j] = *reinterpret_cast<const uint4*>(row + (u % G + j * G) * 16);
+          unit(u, pc);
+        }
+      }
+    }
+    for (int u0 = KU * NT; WIDE && u0 < n_units; u0 += KU * NT) {
+      uint4 pcs[KU][PPS];
+#pragma unroll
+      for (int k = 0; k < KU; ++k) {
+        const int u = tid + u0 + k * NT;
+        const int t = min(u / G, triples - 1), sl = u % G;
+        const char* row = km_row(S, t, H_kv);
+#pragma unroll
+        for (int j = 0; j < PPS; ++j) pcs[k][j] = *reinterpret_cast<const uint4*>(row + (sl + j * G) * 16);
+      }
+#pragma unroll
+      for (int k = 0; k < KU; ++k) {
+        const int u = tid + u0 + k * NT;
+        if (u < n_units) unit(u, pcs[k]);
       }
     }
     __syncthreads();
-    // One wave ranks the candidates (lane i = chunk i, n <= 64): score = max
-    // over (row, KV head), NaN -> -inf; each lane counts the candidates
-    // ranked before it (score desc, index asc) from broadcast LDS reads of
-    // all 64 scores (lanes past n hold -inf, which never outranks); the
-    // chosen chunks are listed in ascending index order with a ballot
-    // prefix count.
-    if (tid < kWave) {
-      const int i = tid;
-      float sc = -INFINITY;
-      if (i < n) {
-        const float* dr = s_dot + i * nrh;
-        float b4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        int rh = 0;
-        if ((nrh & 3) == 0) {  // rows 16-byte aligned: 4 scores per read, 4 reads in flight
-          for (; rh + 16 <= nrh; rh += 16) {
-            float4 v[4];
+    // One lane per candidate ranks it (lane i = chunk i: one wave, or two in
+    // the wide form past 64 candidates): score = max over (row, KV head),
+    // NaN -> -inf; each lane counts the candidates ranked before it (score
+    // desc, index asc) from broadcast LDS reads of the scores (entries past n
+    // hold -inf, which never outranks); the chosen chunks are listed in
+    // ascending index order with a ballot prefix count (two waves: wave 1
+    // adds wave 0's count).
+    auto cand_score = [&](int i) __attribute__((always_inline)) -> float {
+      const float* dr = s_dot + i * nrh;
+      float b4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      int rh = 0;
+      if ((nrh & 3) == 0) {  // rows 16-byte aligned: 4 scores per read, 4 reads in flight
+        for (; rh + 16 <= nrh; rh += 16) {
+          float4 v[4];
 #pragma unroll
-            for (int x = 0; x < 4; ++x) v[x] = *reinterpret_cast<const float4*>(dr + rh + 4 * x);
+          for (int x = 0; x < 4; ++x) v[x] = *reinterpret_cast<const float4*>(dr + rh + 4 * x);
 #pragma unroll
-            for (int x = 0; x < 4; ++x) {
-              b4[0] = fmaxf(b4[0], v[x].x);
-              b4[1] = fmaxf(b4[1], v[x].y);
-              b4[2] = fmaxf(b4[2], v[x].z);
-              b4[3] = fmaxf(b4[3], v[x].w);
-            }
-          }
-          for (; rh < nrh; rh += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(dr + rh);
-            b4[0] = fmaxf(b4[0], v.x);
-            b4[1] = fmaxf(b4[1], v.y);
-            b4[2] = fmaxf(b4[2], v.z);
-            b4[3] = fmaxf(b4[3], v.w);
+          for (int x = 0; x < 4; ++x) {
+            b4[0] = fmaxf(b4[0], v[x].x);
+            b4[1] = fmaxf(b4[1], v[x].y);
+            b4[2] = fmaxf(b4[2], v[x].z);
+            b4[3] = fmaxf(b4[3], v[x].w);
           }
         }
-        for (; rh < nrh; ++rh) b4[0] = fmaxf(b4[0], dr[rh]);
-        const float best = fmaxf(fmaxf(b4[0], b4[1]), fmaxf(b4[2], b4[3]));
-        sc = (best != best) ? -INFINITY : best;
+        for (; rh < nrh; rh += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(dr + rh);
+          b4[0] = fmaxf(b4[0], v.x);
+          b4[1] = fmaxf(b4[1], v.y);
+          b4[2] = fmaxf(b4[2], v.z);
+          b4[3] = fmaxf(b4[3], v.w);
+        }
       }
-      s_sc[i] = sc;
-      wave_lds_fence();
+      for (; rh < nrh; ++rh) b4[0] = fmaxf(b4[0], dr[rh]);
+      const float best = fmaxf(fmaxf(b4[0], b4[1]), fmaxf(b4[2], b4[3]));
+      return (best != best) ? -INFINITY : best;
+    };
+    auto rank_of = [&](int i, float sc) __attribute__((always_inline)) -> int {
       int rank = 0;
       for (int j0 = 0; j0 < n; j0 += 16) {
         float4 v[4];
@@ -642,11 +672,49 @@ struct Selector {
           }
         }
       }
-      const bool chosen = i < n && rank < kk;
-      const uint64_t mask = __ballot(chosen);
-      const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-      if (chosen) s_pick[pos] = i;
-      if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
+      return rank;
+    };
+    auto prefix = [](uint64_t mask) __attribute__((always_inline)) {
+      return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+    };
+    if constexpr (!WIDE) {
+      if (tid < kWave) {
+        const int i = tid;
+        const float sc = i < n ? cand_score(i) : -INFINITY;
+        s_sc[i] = sc;
+        wave_lds_fence();
+        const bool chosen = i < n && rank_of(i, sc) < kk;
+        const uint64_t mask = __ballot(chosen);
+        if (chosen) s_pick[prefix(mask)] = i;
+        if (writer && S.score_out && i < n) S.score_out[(int64_t)sel * S.n_cold + i] = sc;
+      }
+    } else {
+      const int nw_rank = n > kWave ? 2 : 1;
+      const int n_pad = nw_rank * kWave;
+      int* s_cnt = s_pick + Cap::max_cold;  // wave 0's chosen count
+      float sc = -INFINITY;
+      if (tid < n_pad) {
+        if (tid < n) sc = cand_score(tid);
+        s_sc[tid] = sc;
+      }
+      if (nw_rank == 1) {
+        wave_lds_fence();
+      } else {
+        __syncthreads();  // both waves' scores are in LDS
+      }
+      bool chosen = false;
+      uint64_t mask = 0;
+      if (tid < n_pad) {
+        chosen = tid < n && rank_of(tid, sc) < kk;
+        mask = __ballot(chosen);
+        if (nw_rank == 2 && tid == 0) *s_cnt = __builtin_popcountll(mask);
+      }
+      if (nw_rank == 2) __syncthreads();  // wave 0's count for wave 1's positions
+      if (tid < n_pad) {
+        const int base = (nw_rank == 2 && tid >= kWave) ? *s_cnt : 0;
+        if (chosen) s_pick[base + prefix(mask)] = tid;
+        if (writer && S.score_out && tid < n) S.score_out[(int64_t)sel * S.n_cold + tid] = sc;
+      }
     }
     __syncthreads();
     const bool staged = S.residency != nullptr;
@@ -1181,9 +1249,10 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const Pla
   write_partial_pairs_mfma<D, REP, NP, DB>(P, wslot, kwave, pair, acc_pv, m_run, l_head, s_wo, s_wm, s_wl);
 }
 
-template <int DT, int D, int REP, int NW>
+template <int DT, int D, int REP, int NW, bool WIDE = false>
 __global__ void __launch_bounds__(64 * NW, 2)
 decode_attn_kernel(DecodeParams P) {
+  using Cap = SelCap<WIDE>;
   using E = Elem<DT>;
   constexpr bool kMfma = DT != HALO_F32;  // q.k on the matrix cores
   constexpr int EP = E::per16;          // elements per 16-byte piece
@@ -1205,7 +1274,7 @@ decode_attn_kernel(DecodeParams P) {
   constexpr int SZ_K = kMfma ? 0 : NW * TILE * KROW;
   constexpr int SZ_P = kMfma ? 0 : NW * TILE * REP * 4;
   constexpr int SZ_A0 = kMfma ? PlainMfmaLds<D, REP, NW>::bytes : SZ_Q + SZ_K + SZ_P;
-  constexpr int SZ_A = SZ_A0 > kSelBytes ? SZ_A0 : kSelBytes;
+  constexpr int SZ_A = SZ_A0 > Cap::bytes ? SZ_A0 : Cap::bytes;
   constexpr int SZ_B = kMfma ? 0 : NW * REP * D * 4;
   __shared__ __attribute__((aligned(16))) char smem[SZ_A > SZ_B ? SZ_A : SZ_B];
   char* s_q = smem + (threadIdx.x / kWave) * REP * RB;
@@ -1222,7 +1291,7 @@ decode_attn_kernel(DecodeParams P) {
   const int witem = blockIdx.x;
   // Leading selection-slot items start the selection's loads at once (the
   // selection does not depend on the record unless it is per batch row).
-  Selector<DT, D, 64 * NW> selr;
+  Selector<DT, D, 64 * NW, WIDE> selr;
   const bool early_sel = P.sel_on && !P.sel.per_row && witem < P.sel.lead_items;
   if (early_sel) selr.issue(P, 0);
 
@@ -1250,10 +1319,10 @@ decode_attn_kernel(DecodeParams P) {
     if (pick >= 0) {
       // the chunk's own catalog entry (rows, start, flags); a staged chunk is
       // read through its slot's addresses and strides
-      const halo_chunk_desc* tbl = reinterpret_cast<const halo_chunk_desc*>(smem + kSelCatOff);
+      const halo_chunk_desc* tbl = reinterpret_cast<const halo_chunk_desc*>(smem + Cap::cat_off);
       halo_chunk_desc d = tbl[pick];
       if (selr.staged_slot >= 0) {
-        const halo_chunk_desc& sd = tbl[kSelMaxCold + selr.staged_slot];
+        const halo_chunk_desc& sd = tbl[Cap::max_cold + selr.staged_slot];
         d.k = sd.k;
         d.v = sd.v;
         d.k_stride_b = sd.k_stride_b;
@@ -1265,7 +1334,7 @@ decode_attn_kernel(DecodeParams P) {
       }
       dsc = uniform_desc(d);
       if (selr.wa_slot >= 0) {
-        wdst = uniform_desc(tbl[kSelMaxCold + selr.wa_slot]);
+        wdst = uniform_desc(tbl[Cap::max_cold + selr.wa_slot]);
         wa = true;
       }
     } else {
@@ -2121,6 +2190,9 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
     if (kivi) {
       hipLaunchKernelGGL((decode_attn_kivi_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work),
                          dim3(64 * kWavesPerItem), 0, st, p);
+    } else if (p.sel_wide) {
+      hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem, true>), dim3(n_work),
+                         dim3(64 * kWavesPerItem), 0, st, p);
     } else {
       hipLaunchKernelGGL((decode_attn_kernel<DT, D, REP, kWavesPerItem>), dim3(n_work), dim3(64 * kWavesPerItem),
                          0, st, p);
@@ -2228,25 +2300,30 @@ int decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, int dtype
   p.inv_rep = 1.0f / (float)rep;
   p.sel_on = sel != nullptr;
   p.sel = {};
+  p.sel_wide = 0;
   if (sel) {
     const halo_select_cfg& S = *sel;
     const int esz = elem_size(dtype);
     const int rows = S.per_row ? 1 : B;
     HALO_CHECK_ARG(S.kmean && S.catalog, "selection needs kmean and catalog");
-    HALO_CHECK_ARG(S.n_cold >= 1 && S.n_cold <= kSelMaxCold, "n_cold must be in [1, 64]");
+    const bool f32 = dtype == HALO_F32;
+    HALO_CHECK_ARG(S.n_cold >= 1 && S.n_cold <= (f32 ? kSelMaxColdNarrow : kSelMaxColdWide),
+                   "n_cold must be in [1, 128] (bf16/fp16) or [1, 64] (fp32)");
     HALO_CHECK_ARG(S.top_k >= 1 && S.slot0 >= 0 && S.slot0 + S.top_k <= n_desc,
                    "selection slots [slot0, slot0 + top_k) must lie in the chunk table");
     HALO_CHECK_ARG(S.catalog_stride >= S.n_cold, "catalog_stride < n_cold");
     HALO_CHECK_ARG(S.lead_items >= 0, "lead_items must be >= 0");
     HALO_CHECK_ARG(S.residency == nullptr || (S.slot_catalog != nullptr && S.n_slots >= 1 && S.n_slots <= kSelMaxSlots),
                    "staging needs slot_catalog and 1 <= n_slots <= 64");
-    HALO_CHECK_ARG(S.n_cold * rows * H_kv <= kSelTPT * 256, "n_cold * rows * H_kv must be <= 512");
+    HALO_CHECK_ARG(S.n_cold * rows * H_kv <= (f32 ? kSelMaxTriplesNarrow : kSelMaxTriplesWide),
+                   "n_cold * rows * H_kv must be <= 768 (bf16/fp16) or 512 (fp32)");
     HALO_CHECK_ARG(rows * H_kv * D <= kSelMaxQbar, "rows * H_kv * D must be <= 2048");
     HALO_CHECK_ARG(D % 16 == 0, "in-kernel selection needs head_dim % 16 == 0");
     HALO_CHECK_ARG(reinterpret_cast<uintptr_t>(S.kmean) % 16 == 0 && (S.km_stride_b * esz) % 16 == 0 &&
                        (S.km_stride_h * esz) % 16 == 0 && (S.km_stride_p * esz) % 16 == 0,
                    "kmean rows must be 16-byte aligned");
     p.sel = S;
+    p.sel_wide = S.n_cold > kSelMaxColdNarrow || S.n_cold * rows * H_kv > kSelMaxTriplesNarrow;
   }
   MergeParams mp;
   mp.group_offsets = group_offsets;

@@ -30,10 +30,20 @@ from . import _native as nat
 from .chunk_scorer import chunk_means, score_topk
 from .decode import ChunkRef, DecodePlan, build_plan, descs_to_device, launch, pack_descs
 
-# In-kernel selection limits of halo_decode_attn_tiered (include/halo_hip.h).
-_SEL_MAX_COLD = 64
-_SEL_MAX_TRIPLES = 512
+# In-kernel selection limits of halo_decode_attn_tiered (include/halo_hip.h):
+# candidates and (chunk, row, KV head) triples per selection, 16-bit K/V
+# (the wide form) and fp32.
+_SEL_MAX_COLD = 128
+_SEL_MAX_TRIPLES = 768
+_SEL_MAX_COLD_F32 = 64
+_SEL_MAX_TRIPLES_F32 = 512
 _SEL_MAX_QBAR = 2048
+
+
+def _sel_limits(dtype: torch.dtype) -> tuple[int, int]:
+    if dtype == torch.float32:
+        return _SEL_MAX_COLD_F32, _SEL_MAX_TRIPLES_F32
+    return _SEL_MAX_COLD, _SEL_MAX_TRIPLES
 
 
 class TieredDecodeLayer:
@@ -47,7 +57,8 @@ class TieredDecodeLayer:
         self.n_hot, self.top_k = len(hot), top_k
         self.hot, self.cold = list(hot), list(cold)
         n_cold = len(cold)
-        self.fused = bool(fused) and n_cold <= _SEL_MAX_COLD and n_cold * B * H_kv <= _SEL_MAX_TRIPLES \
+        max_cold, max_triples = _sel_limits(dtype)
+        self.fused = bool(fused) and n_cold <= max_cold and n_cold * B * H_kv <= max_triples \
             and B * H_kv * D <= _SEL_MAX_QBAR and D % 16 == 0
         # Selection slots come first in the table (their workgroups are
         # dispatched first, which hides the selection work behind the hot
@@ -157,9 +168,10 @@ class RaggedTieredDecodeLayer:
         B = len(rows)
         n_cold = [len(cold) for _, cold in rows]
         max_cold = max(n_cold)
-        if max_cold > _SEL_MAX_COLD or max_cold * H_kv > _SEL_MAX_TRIPLES or H_kv * D > _SEL_MAX_QBAR or D % 16:
+        lim_cold, lim_triples = _sel_limits(dtype)
+        if max_cold > lim_cold or max_cold * H_kv > lim_triples or H_kv * D > _SEL_MAX_QBAR or D % 16:
             raise AssertionError(f"per-row selection over {max_cold} cold chunks x {H_kv} KV heads (D={D}) exceeds "
-                                 f"the in-kernel limits ({_SEL_MAX_COLD} chunks, {_SEL_MAX_TRIPLES} rows, "
+                                 f"the in-kernel limits ({lim_cold} chunks, {lim_triples} rows, "
                                  f"H_kv * D <= {_SEL_MAX_QBAR}, D % 16 == 0)")
         if top_k < 1:
             raise AssertionError("top_k must be >= 1")

@@ -130,8 +130,9 @@ int halo_decode_attn(const void* q, int64_t q_stride_b, int64_t q_stride_h, int 
  * (d - slot0)-th chosen chunk in ascending index order (top-k order: score
  * descending, then index ascending); a slot past the number of eligible
  * chunks attends nothing.  idx_out[s*top_k + j] / score_out[s*n_cold + p]
- * receive the selection when non-NULL.  Limits: n_cold <= 64,
- * n_cold * rows * H_kv <= 512, rows * H_kv * D <= 2048 per selection and
+ * receive the selection when non-NULL.  Limits: n_cold <= 128 and
+ * n_cold * rows * H_kv <= 768 for bf16/fp16 (64 and 512 for fp32),
+ * rows * H_kv * D <= 2048 per selection and
  * head_dim % 16 == 0 (rows = 1 when per_row).  The dot products use the
  * scorer's fixed summation order (halo_chunk_score_topk).  The work
  * items of a slot must cover as many rows as the largest catalog chunk (rows
@@ -317,7 +318,7 @@ int halo_chunk_score_topk(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * res_out[s*k + j] receives the entry used for the j-th chosen chunk (-1:
  * read in place; unfilled slots -1).  The two-launch selection path (this,
  * then halo_decode_attn over the table) of layers beyond the fused
- * selection's limits (more than 64 cold chunks or 512 (chunk, row, KV head)
+ * selection's limits (more than 128 cold chunks or 768 (chunk, row, KV head)
  * triples); the same residency protocol as halo_select_cfg.  The reference
  * selects on the host and refetches with HALORefetcher
  * (baselines/scorer_ablations.py:218-268, halo/refetcher.py:59-114).

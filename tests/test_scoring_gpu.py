@@ -391,3 +391,64 @@ def test_cold_chunks_read_in_place_from_pinned_host(dev, fused):
         res.append((layer.idx.clone(), layer.scores.clone(), out, lse))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n_cold,H,H_kv,B,per_row", [
+    (96, 32, 8, 1, False),     # 768 (chunk, row, KV head) triples: the 131072-token layer's catalog
+    (128, 24, 6, 1, False),    # 128 candidates, 768 triples
+    (65, 16, 4, 2, False),     # one candidate past a wave, 520 triples over two rows
+    (100, 16, 4, 2, True),     # per-row selection over 100 and 70 eligible chunks
+])
+def test_fused_selection_wide_catalog(dev, n_cold, H, H_kv, B, per_row):
+    """The fused selection over more than 64 cold chunks (two ranking waves)
+    and up to 768 triples: chunk scores bit-exact against the oracle's fixed
+    summation order, the top-k against the oracle's ranking (margin-checked),
+    and the output and LSE against the float64 closed form over the hot and
+    the chosen rows."""
+    from halo_amd import _native as nat
+    from halo_amd.chunk_scorer import chunk_means
+    from halo_amd.decode import ChunkRef, build_plan, descs_to_device, launch, pack_descs
+    dtype, D, c, n_hot, top_k = "bfloat16", 128, 64, 4, 4
+    T = (n_cold + n_hot) * c
+    x = decode_inputs(60 + n_cold, B=B, H=H, H_kv=H_kv, T=T, D=D, dtype=dtype, n_planted=4, sigma=8.0)
+    q, k, v = (_gpu(a, dtype, dev) for a in (x.q, x.k, x.v))
+    refs = [ChunkRef(k[..., i * c:(i + 1) * c, :], v[..., i * c:(i + 1) * c, :], i * c, True)
+            for i in range(T // c)]
+    cold, hot = refs[:n_cold], refs[n_cold:]
+    plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=TDT[dtype], chunks=[cold[0]] * top_k + hot, device=dev)
+    n_sel = B if per_row else 1
+    cat_np, keep = pack_descs(cold * n_sel, B=B, H_kv=H_kv, D=D, dtype=TDT[dtype])
+    cat = descs_to_device(cat_np, dev)
+    km = chunk_means(k, c, n_pages=n_cold)
+    n_el = np.array([n_cold, 70][:B] if per_row else [n_cold], np.int32)
+    n_el_d = torch.from_numpy(n_el).to(dev)
+    idx = torch.full((n_sel, top_k), -7, device=dev, dtype=torch.int32)
+    sc = torch.full((n_sel, n_cold), -7.0, device=dev)
+    cfg = nat.SelectCfg(kmean=km.data_ptr(), km_stride_b=km.stride(0), km_stride_h=km.stride(1),
+                        km_stride_p=km.stride(2), catalog=cat.data_ptr(), catalog_stride=n_cold,
+                        n_cold_per_sel=n_el_d.data_ptr() if per_row else None, n_cold=n_cold, top_k=top_k,
+                        slot0=0, per_row=int(per_row), idx_out=idx.data_ptr(), score_out=sc.data_ptr())
+    out = torch.empty((B, H, D), device=dev, dtype=torch.bfloat16)
+    lse = torch.empty((B, H), device=dev)
+    launch(plan, q[:, :, 0], scale=D ** -0.5, out=out, lse=lse, select=cfg)
+    torch.cuda.synchronize()
+    km_np = km.float().cpu().numpy()
+    for s in range(n_sel):
+        rows = slice(s, s + 1) if per_row else slice(0, B)
+        ne = int(n_el[s])
+        got = sc[s, :ne].cpu().numpy()
+        np.testing.assert_array_equal(got, S.ordered_scores(x.q[rows], km_np[rows], dtype)[:ne])
+        ref_sc = S.mean_key_scores(x.q[rows], km_np[rows], dtype)[:ne]
+        srt = np.sort(ref_sc.astype(np.float64))[::-1]
+        assert srt[top_k - 1] - srt[top_k] > 1e-4, "seed lost its top-k margin"
+        want = S.select_chunks(x.q[rows], km_np[rows], np.arange(ne), top_k, dtype).tolist()
+        assert idx[s].cpu().tolist() == want
+        for b in (range(s, s + 1) if per_row else range(B)):
+            keep_rows = np.zeros(T, bool)
+            keep_rows[n_cold * c:] = True
+            for j in want:
+                keep_rows[j * c:(j + 1) * c] = True
+            ro, rl = A.attention_f64(x.q[b:b + 1, :, 0], x.k[b:b + 1], x.v[b:b + 1], scale=D ** -0.5,
+                                     keep=keep_rows)
+            assert np.abs(out[b:b + 1].float().cpu().numpy() - ro).max() <= 2e-2
+            assert np.abs(lse[b:b + 1].cpu().numpy() - rl).max() <= 1e-3

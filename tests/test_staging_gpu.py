@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _setup(dev, *, L=2, n_chunks=16, chunk=256, n_hot=4, top_k=3, slots=6, keep=None, seed=0, fill_mode="dma",
-           adjacent=False):
+           adjacent=False, fused=True):
     """``adjacent``: each cold chunk's K and V rows adjacent in one pinned
     buffer (filled by one copy), else separate pinned tensors."""
     from halo_amd.decode import ChunkRef
@@ -35,7 +35,7 @@ def _setup(dev, *, L=2, n_chunks=16, chunk=256, n_hot=4, top_k=3, slots=6, keep=
                 for i in range(n_chunks)]
         n_cold = n_chunks - n_hot
         a = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:], cold=refs[:n_cold],
-                              top_k=top_k, device=dev)
+                              top_k=top_k, device=dev, fused=fused)
         host = []
         buf = torch.empty((n_cold, 2) + tuple(refs[0].k.shape), dtype=torch.bfloat16, pin_memory=True)
         for j, c in enumerate(refs[:n_cold]):
@@ -48,7 +48,7 @@ def _setup(dev, *, L=2, n_chunks=16, chunk=256, n_hot=4, top_k=3, slots=6, keep=
             hv.copy_(c.v)
             host.append(ChunkRef(hk, hv, c.chunk_start, True))
         b = TieredDecodeLayer(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, hot=refs[n_cold:], cold=host,
-                              top_k=top_k, device=dev, cold_kmean=a.kmean)
+                              top_k=top_k, device=dev, cold_kmean=a.kmean, fused=fused)
         hbm.append(a)
         staged.append(b)
     st = ColdStaging(staged, n_slots=slots, keep=keep, max_inflight=4, fill_mode=fill_mode)
@@ -330,21 +330,23 @@ def test_staged_ragged_batch_matches_all_hbm(dev):
                     assert torch.equal(st._slot_v[u][s].cpu(), cold[c].v), (li, b, s, c)
 
 
-def test_staged_layers_beyond_the_fused_selection_limits(dev):
-    """Layers with 72 cold chunks (beyond the fused selection's 64) run the
-    two-launch path -- the staged scorer writes the chosen descriptors,
-    with a staged chunk's slot addresses, into the table, then the attention
-    launch -- and match the all-HBM layers bit for bit through the
+@pytest.mark.parametrize("fused", [False, True], ids=["two_launch", "fused"])
+def test_staged_layers_wide_catalog(dev, fused):
+    """Layers with 72 cold chunks, on the two-launch path (the staged scorer
+    writes the chosen descriptors, with a staged chunk's slot addresses,
+    into the table, then the attention launch; the path of layers beyond the
+    fused selection's limits) and on the fused selection (two ranking
+    waves past 64 chunks), match the all-HBM layers bit for bit through the
     benchmark's loop, with hits and misses both served."""
     import bench
     from halo_amd.staging import ColdStaging
     hbm, staged, _, (H, D) = _setup(dev, L=4, n_chunks=96, chunk=64, n_hot=24, top_k=4, slots=10, keep=6,
-                                    seed=31, adjacent=True)
-    assert not staged[0].fused and not hbm[0].fused
+                                    seed=31, adjacent=True, fused=fused)
+    assert staged[0].fused == fused and hbm[0].fused == fused
     L, steps, k = len(hbm), 20, 4
     scale = 1 / math.sqrt(D)
     st = ColdStaging(staged, n_slots=10, keep=6, max_inflight=8)
-    assert not st.all_fused and staged[0].staging is not None
+    assert st.all_fused == fused and (staged[0].staging is not None) == (not fused)
     qtraj = bench.query_trajectory(torch, dev, steps=steps, L=L, H=H, D=D, rho=0.8, seed=32)
     out_hist = torch.zeros((steps, L, 1, H, D), device=dev, dtype=torch.bfloat16)
     idx_hist = torch.full((steps, L, k), -7, device=dev, dtype=torch.int32)

@@ -197,6 +197,54 @@ class HALOCacheChunked(HALOCache):
     def last_stats(self) -> ChunkedAttentionStats:
         return self._stats[max(self._stats)] if self._stats else ChunkedAttentionStats()
 
+    # ------------------------------------------------------------- helpers
+    @staticmethod
+    def _lse_merge(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor, lse_b: torch.Tensor):
+        """Two partial attention results over disjoint key sets merged into
+        one (halo/kv_cache_chunked.py:194-239): lse = logaddexp(lse_a,
+        lse_b), out = exp(lse_a - lse) out_a + exp(lse_b - lse) out_b, a side
+        whose lse is -inf adding nothing; fp32, on the GPU
+        (``halo_lse_merge``)."""
+        from .triton_chunked import lse_merge
+        return lse_merge(out_a, lse_a, out_b, lse_b)
+
+    @staticmethod
+    def _chunk_attention(q: torch.Tensor, k_chunk: torch.Tensor, v_chunk: torch.Tensor, *,
+                         scaling: Optional[float] = None, causal_mask: Optional[torch.Tensor] = None):
+        """Attention of q (B, H, T_q, D) over one chunk (B, H_kv, T_c, D),
+        query heads grouped over the KV heads, returning the fp32 partial
+        (out (B, H, T_q, D), lse (B, H, T_q)) (halo/kv_cache_chunked.py:
+        241-276): one prefill launch (``halo_prefill_attn``; fp32 through the
+        decode kernel).  The kernels mask by position, so ``causal_mask``
+        (T_q, T_c, additive) is taken in the form the reference's chunk walk
+        builds -- 0 where key j <= q_start + i, -inf elsewhere, for some
+        offset q_start -- and any other mask raises."""
+        from .decode import ChunkRef
+        from .prefill import prefill_attention
+
+        if q.dim() != 4 or k_chunk.dim() != 4 or v_chunk.shape != k_chunk.shape:
+            raise AssertionError(f"shapes: q {tuple(q.shape)}, k {tuple(k_chunk.shape)}, v {tuple(v_chunk.shape)}")
+        B, H, T_q, D = q.shape
+        H_kv, T_c = k_chunk.shape[1], k_chunk.shape[2]
+        if H % H_kv:
+            raise AssertionError(f"head count mismatch: q has {H}, kv has {H_kv}")
+        causal, q_start = False, T_c - T_q
+        if causal_mask is not None:
+            if tuple(causal_mask.shape) != (T_q, T_c):
+                raise AssertionError(f"causal_mask must be (T_q, T_c) = {(T_q, T_c)}")
+            visible = causal_mask == 0
+            q_start = int(visible[0].sum().item()) - 1
+            i = torch.arange(T_q, device=causal_mask.device).unsqueeze(1)
+            j = torch.arange(T_c, device=causal_mask.device).unsqueeze(0)
+            want = j <= q_start + i
+            if not (torch.equal(visible, want) and bool(torch.isneginf(causal_mask[~want]).all())):
+                raise NotImplementedError("only the causal mask of a position offset is supported: the kernels "
+                                          "mask by key and query positions")
+            causal = True
+        chunk = ChunkRef(k_chunk.to(q.dtype), v_chunk.to(q.dtype), 0, causal)
+        return prefill_attention(q, [chunk], scale=scaling, q_start=q_start, out_dtype=torch.float32,
+                                 return_lse=True)
+
     # ------------------------------------------------------------- peel
     def _keep_mask(self, layer_idx: int, T: int) -> Optional[np.ndarray]:
         """Rows the placement scorer keeps on the GPU (None: no scorer or no

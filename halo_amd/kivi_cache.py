@@ -19,6 +19,11 @@ and leave the window.  Differences:
     decode (T_q = 1) is one ``halo_decode_attn_kivi`` launch plus its merge,
     dequantising in registers; T_q > 1 runs the MFMA prefill over the
     dequantised blocks and the recent rows.
+As in the reference the class is a transformers ``DynamicCache`` when
+transformers is importable: ``update`` also leaves the dequantised cache in
+the layer's ``keys`` / ``values``, so the model's own attention and mask
+sizes see it, and ``wrap_with_kivi`` installs a fresh cache per
+``generate`` call (:205-226).
 """
 from __future__ import annotations
 
@@ -30,14 +35,24 @@ import torch
 from . import kivi
 from .decode import ChunkRef
 
+try:  # the HF cache protocol when transformers is importable (baselines/kivi_cache.py:27-34)
+    from transformers.cache_utils import DynamicCache as _BaseCache
+    from transformers.cache_utils import DynamicLayer as _Layer
+    HAS_TRANSFORMERS = True
+except Exception:  # pragma: no cover - exercised only without transformers
+    _BaseCache, _Layer = object, None
+    HAS_TRANSFORMERS = False
+
 GROUP = kivi.GROUP
 
 
-class KIVICache:
+class KIVICache(_BaseCache):
     """Per-layer recent window + packed KIVI blocks (B, H_kv, n, block_bytes)."""
 
     def __init__(self, *, bits: int = 2, group_size: int = 32, residual_length: int = 32,
                  materialize: bool = True, chunk_tokens: int = 2048) -> None:
+        if HAS_TRANSFORMERS:
+            super().__init__()
         if group_size != GROUP:
             raise AssertionError(f"KIVI blocks hold {GROUP} tokens; group_size={group_size} is not supported")
         if bits not in (2, 4):
@@ -70,6 +85,8 @@ class KIVICache:
     def reset(self) -> None:
         for lst in (self._k_recent, self._v_recent, self._blocks, self._n_seen, self._deq, self._n_deq):
             lst.clear()
+        if HAS_TRANSFORMERS:
+            self.layers = []
 
     def blocks(self, layer_idx: int) -> Optional[torch.Tensor]:
         """The layer's packed blocks (B, H_kv, n_seen / 32, block_bytes)."""
@@ -129,7 +146,16 @@ class KIVICache:
         self._v_recent[layer_idx] = new_v.contiguous()
         if not self.materialize:
             return None
-        return self._materialized(layer_idx)
+        k_full, v_full = self._materialized(layer_idx)
+        if HAS_TRANSFORMERS:
+            # the HF layer holds what attention reads: its length gives the mask sizes
+            while len(self.layers) <= layer_idx:
+                self.layers.append(_Layer())
+            lay = self.layers[layer_idx]
+            if not lay.is_initialized:
+                lay.lazy_initialization(key_states, value_states)
+            lay.keys, lay.values = k_full, v_full
+        return k_full, v_full
 
     def _materialized(self, layer_idx: int):
         """Dequantise the blocks not yet dequantised and place the recent
@@ -206,3 +232,25 @@ class KIVICache:
                 kd, vd = kivi.dequantize(self.blocks(layer_idx), D=D, dtype=q.dtype, bits=self.bits)
             chunks.append(ChunkRef(kd, vd, 0, True))
         return prefill_attention(q, chunks + recent, scale=scale, q_start=q0, return_lse=return_lse)
+
+
+def wrap_with_kivi(model, *, memory_ratio: int = 4, **kw):
+    """Install the KIVI cache on a HF model (baselines/kivi_cache.py:205-226):
+    ``generate`` resets one ``KIVICache`` (bits = max(16 // memory_ratio, 2);
+    ``kw`` are its other arguments) and passes it as ``past_key_values``
+    unless the caller passes a cache of its own.  Returns the model."""
+    cache = KIVICache.from_memory_ratio(memory_ratio=memory_ratio, **kw)
+    if getattr(model, "_kivi_patched", False):
+        return model
+    original_generate = model.generate
+
+    def kivi_generate(*args, **kwargs):
+        cache.reset()
+        kwargs.setdefault("past_key_values", cache)
+        kwargs.setdefault("use_cache", True)
+        return original_generate(*args, **kwargs)
+
+    model.generate = kivi_generate
+    model._kivi_patched = True
+    model._kivi_cache = cache
+    return model

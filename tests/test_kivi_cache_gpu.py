@@ -133,3 +133,58 @@ def test_attention_over_the_cache(dev, dtype, H, H_kv):
     assert np.abs(outp.float().cpu().numpy() - wp).max() <= 2e-2
     outl = lean.compute_attention(torch.from_numpy(qp).to(dev).to(TDT[dtype]), layer_idx=0)
     assert torch.equal(outl, outp)
+
+
+def _tiny_models(dev, dtype):
+    from transformers import AutoModelForCausalLM
+    from transformers.models.qwen2 import Qwen2Config
+
+    def cfg():
+        return Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                           num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=4096,
+                           rope_theta=10000.0, tie_word_embeddings=False, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    ref = AutoModelForCausalLM.from_config(cfg()).eval()
+    torch.manual_seed(0)
+    kv = AutoModelForCausalLM.from_config(cfg()).eval()
+    kv.load_state_dict(ref.state_dict())
+    return ref.to(dev, dtype), kv.to(dev, dtype)
+
+
+def test_wrap_with_kivi_generate(dev):
+    """``wrap_with_kivi`` (baselines/kivi_cache.py:205-226) inside a tiny
+    randomly initialised Qwen2 in fp16: with a recent window longer than the
+    sequence nothing is quantised and greedy generation equals the plain
+    model's token for token; with a 32-token window the blocks form, every
+    layer's cache holds the dequantised blocks followed by the recent rows,
+    and the sequence length counts every token."""
+    pytest.importorskip("transformers")
+    from halo_amd import kivi
+    from halo_amd.kivi_cache import KIVICache, wrap_with_kivi
+    ref, kv = _tiny_models(dev, torch.float16)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(10, 500, (1, 200), generator=g).to(dev)
+    with torch.no_grad():
+        want = ref.generate(ids, max_new_tokens=12, do_sample=False)
+        wrap_with_kivi(kv, memory_ratio=8, residual_length=4096)
+        got = kv.generate(ids, max_new_tokens=12, do_sample=False)
+    assert torch.equal(got, want)
+    assert kv._kivi_cache.bits == 2
+    # quantised: a 32-token recent window
+    _, kv2 = _tiny_models(dev, torch.float16)
+    wrap_with_kivi(kv2, memory_ratio=8, residual_length=32)
+    with torch.no_grad():
+        out = kv2.generate(ids, max_new_tokens=8, do_sample=False)
+    cache = kv2._kivi_cache
+    assert isinstance(cache, KIVICache) and out.shape == (1, 208)
+    T = cache.get_seq_length(0)
+    assert T == 207                       # the last generated token is not fed back
+    for li in range(2):
+        blocks = cache.blocks(li)
+        n = blocks.shape[2]
+        assert n * 32 + cache.recent(li)[0].shape[-2] == T and n >= 5
+        kd, vd = kivi.dequantize(blocks, D=64, dtype=torch.float16, bits=2)
+        lay = cache.layers[li]
+        assert lay.keys.shape[-2] == T
+        assert torch.equal(lay.keys[:, :, : n * 32], kd) and torch.equal(lay.values[:, :, : n * 32], vd)
+        assert torch.equal(lay.keys[:, :, n * 32:], cache.recent(li)[0])

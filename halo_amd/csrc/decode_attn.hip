@@ -1988,16 +1988,22 @@ decode_attn_kivi_kernel(DecodeParams P) {
 // ---------------------------------------------------------------------------
 // Merge: one workgroup per (query-head group, head) combines that head's
 // partials over the group's work items with the caller's accumulators and
-// writes (m,l,o) and/or (out, lse).  Thread t owns float4 column t % C4 and
-// the partials p = t / C4 + k * TPC; it merges them online (its own running
-// max), so every load is independent and the whole merge costs one memory
-// round trip; the TPC per-thread results are then combined in a fixed order
-// through LDS (deterministic run to run).
+// writes (m,l,o) and/or (out, lse).  A head's D columns are split over CS
+// workgroups (blockIdx.z); thread t owns float4 column t % C4 of its
+// workgroup's share and the partials p = t / C4 + k * TPC; it merges them
+// online (its own running max), so every load is independent and the whole
+// merge costs one memory round trip; the TPC per-thread results are then
+// combined in a fixed order through LDS (deterministic run to run).  With
+// CS > 1 every workgroup of a head reads the incoming accumulator and the
+// first writes m/l, so a launch that both reads and writes m/l (acc_mode 3)
+// runs with CS = 1.
 // ---------------------------------------------------------------------------
-template <int D, int REP, int NT, int MB>
+template <int D, int REP, int NT, int MB, int CS>
 __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
-  constexpr int C4 = D / 4;           // float4 columns of one head
+  constexpr int C4A = D / 4;          // float4 columns of one head
+  constexpr int C4 = C4A / CS;        // float4 columns of this workgroup
   constexpr int TPC = NT / C4;        // threads sharing a column
+  static_assert(C4A % CS == 0 && NT % C4 == 0, "merge shape");
   __shared__ float4 s_o[NT];
   __shared__ float s_m[NT], s_l[NT];
   const int tid = threadIdx.x;
@@ -2019,10 +2025,11 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
   const bool write_acc = has_acc && (P.acc_mode & 2);
   const int64_t aidx = (int64_t)b * P.acc_stride_b + hq;
   const int col = tid % C4, phase = tid / C4;
+  const int gcol = blockIdx.z * C4 + col;  // float4 column within the head
 
   float mt = -INFINITY, lt = 0.f;
   float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4 + col;
+  const float4* wo4 = reinterpret_cast<const float4*>(P.ws_o) + ((int64_t)gbeg * REP + r) * C4A + gcol;
   const float* wml = P.ws_ml + ((int64_t)gbeg * REP + r) * 2;
   // MB: partials per thread whose loads are issued together (one batch
   // covers TPC * MB partials of the group)
@@ -2036,7 +2043,7 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
     for (int k = 0; k < MB; ++k) {
       const int pp = min(p0 + k * TPC, np - 1);
       ml[k] = *reinterpret_cast<const float2*>(wml + (int64_t)pp * REP * 2);
-      op[k] = wo4[(int64_t)pp * REP * C4];
+      op[k] = wo4[(int64_t)pp * REP * C4A];
     }
     // the batch's max first, then independent weights (one rescale of the
     // running values per batch instead of a dependent chain per partial)
@@ -2098,7 +2105,7 @@ __global__ void __launch_bounds__(NT) decode_merge_kernel(MergeParams P) {
     o4[2] += w * po[ph].z;
     o4[3] += w * po[ph].w;
   }
-  const int d0 = col * 4;
+  const int d0 = gcol * 4;
   const int64_t obase = aidx * D + d0;
   if (merge_in) {
     const float w = __builtin_amdgcn_exp2f(am - Ms);
@@ -2203,19 +2210,33 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, int n_work, int 
   }
   HALO_CHECK_HIP(hipGetLastError());
   // The merge block and its load batch are sized so that one batch of loads
-  // covers a group's partials where that is cheap: 256 threads x 8 partials,
-  // 512 x 8, and 512 x 9 for groups just past that (a 131072-token KIVI
-  // decode: 128 block items plus the recent rows); a second batch is a second
+  // covers a group's partials where that is cheap; a second batch is a second
   // dependent round trip, but much larger batches measured slower (512 x 16
-  // at 129 partials: +0.7 us).
+  // at 129 partials: +0.7 us).  Up to 144 partials per group, each head's
+  // columns are split over small workgroups (one wave each): 32 columns and
+  // 8 partials per thread up to 64 partials, 16 columns and 5 or 9 partials
+  // per thread up to 80 / 144 (C2's 64: 17.15 -> 16.92 us per layer; the
+  // 131072-token KIVI decode's 129: 22.8 -> 22.2 us; against one workgroup
+  // of 256-512 threads per head).  Launches that both read and write the
+  // caller's m/l keep one workgroup per head.
   const int per_group = (n_work + n_groups - 1) / n_groups;
   constexpr int C4 = D / 4;
-  if (per_group <= (256 / C4) * 8) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 256, 8>), dim3(n_groups, REP), dim3(256), 0, st, mp);
+  const bool split_ok = !(mp.m != nullptr && (mp.acc_mode & 3) == 3);
+  if (split_ok && per_group <= 64) {
+    constexpr int CS = D / 32;
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 64, 8, CS>), dim3(n_groups, REP, CS), dim3(64), 0, st, mp);
+  } else if (split_ok && per_group <= 80) {
+    constexpr int CS = D / 16;
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 64, 5, CS>), dim3(n_groups, REP, CS), dim3(64), 0, st, mp);
+  } else if (split_ok && per_group <= 144) {
+    constexpr int CS = D / 16;
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 64, 9, CS>), dim3(n_groups, REP, CS), dim3(64), 0, st, mp);
+  } else if (per_group <= (256 / C4) * 8) {
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 256, 8, 1>), dim3(n_groups, REP), dim3(256), 0, st, mp);
   } else if (per_group > (512 / C4) * 8 && per_group <= (512 / C4) * 9) {
-    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 9>), dim3(n_groups, REP), dim3(512), 0, st, mp);
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 9, 1>), dim3(n_groups, REP), dim3(512), 0, st, mp);
   } else {
-    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 8>), dim3(n_groups, REP), dim3(512), 0, st, mp);
+    hipLaunchKernelGGL((decode_merge_kernel<D, REP, 512, 8, 1>), dim3(n_groups, REP), dim3(512), 0, st, mp);
   }
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;

@@ -4,8 +4,17 @@
 //
 // The kernels that consume it are the fused selection of
 // halo_decode_attn_tiered (residency entries, slot catalog, feedback row);
-// this file only enqueues work on HIP streams (hipMemcpyAsync, events, the
-// int32 store kernel) and keeps the host mirror of the cache.
+// this file enqueues work on HIP streams (fill copies and their events, and
+// one small boundary kernel per segment) and keeps the host mirror of the
+// cache.
+//
+// Segment boundary: halo_staging_after only marks the segment's feedback rows
+// for publication; the next halo_staging_before on the same stream enqueues
+// ONE kernel that stores the batched residency entries and copies the marked
+// rows into a pinned host ring entry, then sets that entry's sequence word
+// (system-scope release).  The host polls the word instead of waiting on an
+// event: a device-to-host copy plus an event record cost ~8 us of stream
+// time per segment, a store launch ~5 us more, the one kernel ~5 us.
 //
 // The unit of the cache is a selection: one per layer, or one per batch row
 // of a layer with per-row selection (B selections per layer, each over its
@@ -26,15 +35,15 @@
 //    (the chunk was among the layer's current top-k, so the next launch
 //    would otherwise read it over the link);
 //  * evictions are decided only for layers whose feedback rows came back:
-//    every launch of such a layer has finished (the feedback copy ran
-//    behind it) and its next launch is not enqueued yet, so the slot can
-//    take a fill at once; the -1 store waits for the layer's next
+//    every launch of such a layer has finished (the kernel that published
+//    the rows ran behind it) and its next launch is not enqueued yet, so the
+//    slot can take a fill at once; the -1 store waits for the layer's next
 //    halo_staging_before and goes out in the same batched store as that
-//    call's commits (one small launch per segment instead of two), ahead of
-//    them, so it precedes every later read.
+//    call's commits, ahead of them, so it precedes every later read.
 #include <algorithm>
 #include <chrono>
 #include <numeric>
+#include <thread>
 #include <vector>
 
 #include "common.hpp"
@@ -62,9 +71,13 @@ struct halo_staging {
   std::vector<int64_t> nbytes;          // (U, n) bytes per K (or V) tensor
   std::vector<int32_t> ncold;           // (U) cold chunks of each unit (<= n)
   std::vector<float*> ring;             // pinned (L, W) rows per ring entry
-  std::vector<hipEvent_t> ring_ev;
+  std::vector<float*> ring_dev;         // the same rows' device-visible addresses
+  uint64_t* ring_seq = nullptr;         // pinned: entry r's sequence word at [r * 8]
+  uint64_t* ring_seq_dev = nullptr;
+  std::vector<hipStream_t> ring_stream; // stream of the kernel that publishes entry r
   std::vector<std::pair<int, int>> ring_rows;
   int64_t queued = 0, seen = 0;
+  int64_t launched = 0;                 // entries [0, launched) have their publish enqueued
   std::vector<int64_t> slot_of, holds, last_rank, wa_slot, launches, processed;
   std::vector<int8_t> state;
   std::vector<hipEvent_t> fill_ev;      // (U, S): the event of the slot's fill in flight
@@ -129,13 +142,129 @@ void take_deferred(halo_staging* h, int ulo, int uhi) {
   h->def_unit.resize(w);
 }
 
+// One segment boundary on the compute stream: up to kBoundaryPairs residency
+// stores and, when `seq` is set, the publication of feedback rows into a
+// pinned ring entry followed by its sequence word.  One workgroup.
+constexpr int kBoundaryPairs = 32;
+constexpr int kBoundaryThreads = 256;
+struct BoundaryArgs {
+  const float* src;   // device feedback rows
+  float* dst;         // device-visible address of the ring entry's rows
+  uint64_t* seq;      // device-visible address of its sequence word; NULL: no publication
+  uint64_t seq_val;
+  int32_t* base;      // residency entries
+  int64_t n_elems;
+  int n_floats, n_pairs;
+  int64_t idx[kBoundaryPairs];
+  int32_t val[kBoundaryPairs];
+};
+
+__global__ void __launch_bounds__(kBoundaryThreads) boundary_kernel(BoundaryArgs a) {
+  const int t = threadIdx.x;
+  if (t < a.n_pairs && a.idx[t] >= 0 && a.idx[t] < a.n_elems) a.base[a.idx[t]] = a.val[t];
+  if (a.seq == nullptr) return;  // uniform
+  // System-scope stores write through to host memory; the wait for their
+  // acknowledgements, then the barrier, order every row before the sequence
+  // word without a fence (a release fence would also write back the L2's
+  // dirty lines of the preceding launches).
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(a.src);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(a.dst);
+  for (int i = t; i < a.n_floats; i += kBoundaryThreads)
+    __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) __hip_atomic_store(a.seq, a.seq_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Enqueue a boundary kernel on `st`: the residency pairs [i0, i0 + cnt) of
+// the store batch and, with `publish`, the oldest unpublished ring entry.
+int launch_boundary(halo_staging* h, hipStream_t st, bool publish, size_t i0, int cnt) {
+  BoundaryArgs a{};
+  a.base = h->dev_i32;
+  a.n_elems = (int64_t)h->U * h->n + h->L;
+  a.n_pairs = cnt;
+  for (int j = 0; j < cnt; ++j) {
+    a.idx[j] = h->idx_buf[i0 + j];
+    a.val[j] = h->val_buf[i0 + j];
+  }
+  if (publish) {
+    const int64_t e = h->launched;
+    const int r = (int)(e % h->ring_n);
+    const int lo = h->ring_rows[r].first, hi = h->ring_rows[r].second;
+    const size_t off = (size_t)lo * h->W;
+    a.src = h->feedback + off;
+    a.dst = h->ring_dev[r] + off;
+    a.n_floats = (int)((size_t)(hi - lo) * h->W);
+    a.seq = h->ring_seq_dev + (size_t)r * 8;
+    a.seq_val = (uint64_t)(e + 1);
+    h->launched += 1;
+  }
+  hipLaunchKernelGGL(boundary_kernel, dim3(1), dim3(kBoundaryThreads), 0, st, a);
+  HALO_CHECK_HIP(hipGetLastError());
+  return HALO_OK;
+}
+
+// Publish the marked entries up to the first one on `compute` (all of them
+// when `all`), each alone on its own stream, behind the launches it follows.
+int publish_marked(halo_staging* h, hipStream_t compute, bool all) {
+  while (h->launched < h->queued) {
+    const hipStream_t ps = h->ring_stream[(size_t)(h->launched % h->ring_n)];
+    if (ps == compute && !all) break;
+    const int rc = launch_boundary(h, ps, true, 0, 0);
+    if (rc != HALO_OK) return rc;
+  }
+  return HALO_OK;
+}
+
+// The batched residency store and the pending feedback publication on
+// `compute`, as few boundary kernels as the batch needs (usually one).
 int store(halo_staging* h, hipStream_t compute) {
-  if (h->idx_buf.empty()) return HALO_OK;
-  const int rc = halo_store_i32(h->dev_i32, (int64_t)h->U * h->n + h->L, h->idx_buf.data(), h->val_buf.data(),
-                                (int)h->idx_buf.size(), compute);
+  int rc = publish_marked(h, compute, false);
+  if (rc != HALO_OK) return rc;
+  const size_t n = h->idx_buf.size();
+  size_t i0 = 0;
+  while (rc == HALO_OK && (i0 < n || h->launched < h->queued)) {
+    const int cnt = (int)std::min<size_t>(kBoundaryPairs, n - i0);
+    rc = launch_boundary(h, compute, h->launched < h->queued, i0, cnt);
+    i0 += cnt;
+  }
   h->idx_buf.clear();
   h->val_buf.clear();
   return rc;
+}
+
+// Wait until ring entry `e` has been published: a spin on its sequence
+// word.  After 2 ms the stream that carries the publication is queried once
+// per millisecond (a query is not free: it is kept off the normal path), so a
+// failed or drained stream ends the wait with an error instead of a hang.
+int wait_entry(halo_staging* h, int64_t e) {
+  const int r = (int)(e % h->ring_n);
+  volatile uint64_t* w = h->ring_seq + (size_t)r * 8;
+  const uint64_t want = (uint64_t)(e + 1);
+  const int64_t t0 = now_ns();
+  int64_t next_query = t0 + 2000000;
+  for (int64_t spin = 0;; ++spin) {
+    if (__atomic_load_n(w, __ATOMIC_ACQUIRE) >= want) return HALO_OK;
+    __builtin_ia32_pause();
+    if ((spin & 1023) != 1023) continue;
+    const int64_t t = now_ns();
+    if (t < next_query) continue;
+    next_query = t + 1000000;
+    const hipError_t q = hipStreamQuery(h->ring_stream[r]);
+    if (q == hipSuccess) {
+      if (__atomic_load_n(w, __ATOMIC_ACQUIRE) >= want) return HALO_OK;
+      set_error("staging feedback: the publishing stream drained without the entry's sequence word");
+      return HALO_E_HIP;
+    }
+    if (q != hipErrorNotReady) HALO_CHECK_HIP(q);
+    (void)hipGetLastError();
+    std::this_thread::yield();
+  }
+}
+
+bool entry_ready(const halo_staging* h, int64_t e) {
+  const volatile uint64_t* w = h->ring_seq + (size_t)(e % h->ring_n) * 8;
+  return __atomic_load_n(w, __ATOMIC_ACQUIRE) >= (uint64_t)(e + 1);
 }
 
 // Give every empty write-allocate reservation a free slot (highest index
@@ -393,18 +522,28 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
   h->processed.assign(L, 0);
   h->fill_ev.assign(U * S, nullptr);
   h->ring.assign(h->ring_n, nullptr);
-  h->ring_ev.assign(h->ring_n, nullptr);
+  h->ring_dev.assign(h->ring_n, nullptr);
+  h->ring_stream.assign(h->ring_n, nullptr);
   h->ring_rows.assign(h->ring_n, {0, 0});
   int rc = HALO_OK;
   for (auto& e : h->fill_ev)
     if (rc == HALO_OK && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) rc = HALO_E_HIP;
+  // Coherent pinned memory: the boundary kernel's stores go to host memory
+  // rather than into the GPU's caches.
   for (int r = 0; r < h->ring_n && rc == HALO_OK; ++r) {
-    if (hipEventCreateWithFlags(&h->ring_ev[r], hipEventDisableTiming) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&h->ring[r]), L * h->W * sizeof(float), hipHostMallocDefault) !=
-            hipSuccess)
+    if (hipHostMalloc(reinterpret_cast<void**>(&h->ring[r]), L * h->W * sizeof(float), hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&h->ring_dev[r]), h->ring[r], 0) != hipSuccess)
       rc = HALO_E_HIP;
   }
+  if (rc == HALO_OK &&
+      (hipHostMalloc(reinterpret_cast<void**>(&h->ring_seq), (size_t)h->ring_n * 8 * sizeof(uint64_t),
+                     hipHostMallocCoherent) != hipSuccess ||
+       hipHostGetDevicePointer(reinterpret_cast<void**>(&h->ring_seq_dev), h->ring_seq, 0) != hipSuccess))
+    rc = HALO_E_HIP;
+  if (rc == HALO_OK) std::fill(h->ring_seq, h->ring_seq + (size_t)h->ring_n * 8, (uint64_t)0);
   if (rc != HALO_OK) {
+    (void)hipGetLastError();
     set_error("halo_staging_create: event or pinned ring allocation failed");
     halo_staging_destroy(h);
     return rc;
@@ -416,18 +555,17 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
 
 extern "C" int halo_staging_destroy(halo_staging* h) {
   if (h == nullptr) return HALO_OK;
-  // pending copies and feedback reads must end before their events and the
-  // ring go away
-  for (auto e : h->ring_ev)
-    if (e) (void)hipEventSynchronize(e);
+  // pending copies and feedback publications must end before their events
+  // and the ring go away (an entry marked but never enqueued is dropped)
+  if (h->ring_seq != nullptr)
+    for (int64_t e = h->seen; e < h->launched; ++e) (void)wait_entry(h, e);
   for (auto e : h->fill_ev)
     if (e) (void)hipEventSynchronize(e);
-  for (auto e : h->ring_ev)
-    if (e) (void)hipEventDestroy(e);
   for (auto e : h->fill_ev)
     if (e) (void)hipEventDestroy(e);
   for (auto p : h->ring)
     if (p) (void)hipHostFree(p);
+  if (h->ring_seq) (void)hipHostFree(h->ring_seq);
   (void)hipGetLastError();
   delete h;
   return HALO_OK;
@@ -491,12 +629,13 @@ extern "C" int halo_staging_after(halo_staging* h, int lo, int hi, void* stream)
     return HALO_E_INVALID;
   }
   hipStream_t compute = static_cast<hipStream_t>(stream);
+  // an entry still marked goes out alone first: one publication per kernel
+  const int rc = publish_marked(h, compute, true);
+  if (rc != HALO_OK) return rc;
   const int r = (int)(h->queued % h->ring_n);
-  const size_t off = (size_t)lo * h->W, bytes = (size_t)(hi - lo) * h->W * sizeof(float);
-  HALO_CHECK_HIP(hipMemcpyAsync(h->ring[r] + off, h->feedback + off, bytes, hipMemcpyDeviceToHost, compute));
-  HALO_CHECK_HIP(hipEventRecord(h->ring_ev[r], compute));
   h->ring_rows[r] = {lo, hi};
-  h->queued += 1;
+  h->ring_stream[r] = compute;
+  h->queued += 1;  // marked: the next boundary kernel on `compute` publishes it
   return HALO_OK;
 }
 
@@ -509,16 +648,16 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
   while (h->seen < h->queued) {
     const int r = (int)(h->seen % h->ring_n);
     if (h->seen < target) {
-      const int64_t t0 = now_ns();
-      HALO_CHECK_HIP(hipEventSynchronize(h->ring_ev[r]));
-      h->st.ns_wait += now_ns() - t0;
-    } else {
-      const hipError_t e = hipEventQuery(h->ring_ev[r]);
-      if (e == hipErrorNotReady) {
-        (void)hipGetLastError();
-        break;
+      if (h->seen >= h->launched) {  // marked, not enqueued yet: publish it now
+        const int rc = publish_marked(h, compute, true);
+        if (rc != HALO_OK) return rc;
       }
-      HALO_CHECK_HIP(e);
+      const int64_t t0 = now_ns();
+      const int rc = wait_entry(h, h->seen);
+      h->st.ns_wait += now_ns() - t0;
+      if (rc != HALO_OK) return rc;
+    } else if (h->seen >= h->launched || !entry_ready(h, h->seen)) {
+      break;
     }
     const int lo = h->ring_rows[r].first, hi = h->ring_rows[r].second;
     const float* fb = h->ring[r] + (size_t)lo * h->W;
@@ -550,7 +689,11 @@ extern "C" int halo_staging_service(halo_staging* h, int lag, void* stream) {
 
 extern "C" int halo_staging_reset(halo_staging* h) {
   HALO_CHECK_ARG(h != nullptr, "null staging cache");
-  for (auto e : h->ring_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
+  for (int64_t e = h->seen; e < h->launched; ++e) {
+    const int rc = wait_entry(h, e);
+    if (rc != HALO_OK) return rc;
+  }
+  h->launched = h->queued;  // entries marked but not enqueued are dropped
   for (auto e : h->fill_ev) HALO_CHECK_HIP(hipEventSynchronize(e));
   h->pending.clear();
   h->def_idx.clear();

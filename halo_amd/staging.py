@@ -35,8 +35,8 @@ Ordering (no kernel observes a change while it runs):
     one (a chunk among its layer's current top-k, which the next launch would
     otherwise read over the link): the compute stream waits for its copy;
   * evictions are decided only for layers whose feedback just came back:
-    every launch of such a layer has finished (its feedback copy ran behind
-    it) and its next launch is not enqueued yet.  So the slot can take a
+    every launch of such a layer has finished (the kernel that published its
+    feedback ran behind it) and its next launch is not enqueued yet.  So the slot can take a
     fill at once, and the eviction's -1 store goes out with the layer's next
     ``before_step`` batch, ahead of that batch's commits: it runs before any
     later launch of the layer, and the new chunk's entry is committed only
@@ -268,8 +268,12 @@ class ColdStaging:
         nat.check(self._L.halo_staging_before(self._h, lo, hi, nat.stream_ptr()), "halo_staging_before")
 
     def after_step(self, lo: int = 0, hi: Optional[int] = None) -> None:
-        """Queue the feedback rows of layers [lo, hi) (scores, picks,
-        residency used) for the host: one copy after those layers' launches."""
+        """Mark the feedback rows of layers [lo, hi) (scores, picks,
+        residency used) for the host.  The next ``before_step`` on the same
+        stream enqueues one small kernel that writes the rows into a pinned
+        ring entry and stores that call's residency entries (``service`` and
+        ``drain`` publish a marked entry themselves when they must wait for
+        it)."""
         hi = len(self.layers) if hi is None else hi
         rc = self._L.halo_staging_after(self._h, lo, hi, nat.stream_ptr())
         if rc == nat.HALO_E_INVALID and b"overrun" in self._L.halo_last_error():

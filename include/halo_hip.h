@@ -591,10 +591,14 @@ typedef struct halo_staging halo_staging;
  * one graph (or launches) on the compute `stream`:
  *   halo_staging_before  -- commit the landed (and, after a compute-stream
  *                           wait, the urgent) fills of the segment's layers
- *                           and name their write-allocate slots: one store
- *                           kernel; call before the segment's launches;
- *   halo_staging_after   -- queue the segment's feedback rows for the host
- *                           (one device-to-host copy + event); call after;
+ *                           and name their write-allocate slots; call before
+ *                           the segment's launches;
+ *   halo_staging_after   -- mark the segment's feedback rows for the host;
+ *                           call after.  One small kernel per segment does
+ *                           both: the next halo_staging_before on the same
+ *                           stream stores the residency entries and writes
+ *                           the marked rows into a pinned ring entry, then
+ *                           its sequence word, which the host polls;
  *   halo_staging_service -- process returned feedback (waiting for all but
  *                           the `lag` newest segments, taking those too when
  *                           done): count hits and misses, evict, and issue

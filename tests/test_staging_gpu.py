@@ -136,6 +136,67 @@ def test_constant_query_ends_all_hits_in_a_graph(dev):
         assert torch.equal(outs[li], ref[li])
 
 
+def test_feedback_publication_in_unusual_call_orders(dev):
+    """after_step only marks a segment's feedback rows; the next before_step
+    on the same stream publishes them (one boundary kernel with its
+    residency stores).  Every other order still gets every row processed
+    exactly once: two after_step calls in a row, after_step on one stream and
+    before_step on another, a lagged service that must not wait for a marked
+    entry, and clear() with a marked entry (dropped)."""
+    hbm, staged, st, (H, D) = _setup(dev, seed=5)
+    L = len(hbm)
+    k = staged[0].top_k
+    scale = 1 / math.sqrt(D)
+    q = _queries(dev, 1, L, H, D, 0.0, 6)[0]
+    out = torch.empty((1, H, D), device=dev, dtype=torch.bfloat16)
+
+    def run(li):
+        staged[li].step(q[li], scale=scale, out=out)
+
+    def counted():
+        return st.hits + st.misses
+
+    st.reset_counters()
+    # two segments marked back to back (no before_step between them)
+    st.before_step(0, 1)
+    run(0)
+    st.after_step(0, 1)
+    run(1)
+    st.after_step(1, 2)
+    st.service(lag=1)          # must not wait for the newest, unpublished entry
+    st.drain()
+    assert counted() == L * k
+    # marked on a side stream, the next before_step on the default stream
+    s2 = torch.cuda.Stream()
+    s2.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s2):
+        for li in range(L):
+            run(li)
+        st.after_step()
+    torch.cuda.current_stream().wait_stream(s2)
+    st.before_step()
+    for li in range(L):
+        run(li)
+    st.after_step()
+    st.drain()
+    assert counted() == 3 * L * k
+    # a marked entry is dropped by clear(); the next steps count normally
+    st.before_step()
+    for li in range(L):
+        run(li)
+    st.after_step()
+    st.clear()
+    assert counted() == 0
+    for _ in range(2):
+        st.before_step()
+        for li in range(L):
+            run(li)
+        st.after_step()
+        st.service()
+    st.drain()
+    assert counted() == 2 * L * k
+
+
 def test_staging_validates_its_inputs(dev):
     from halo_amd.staging import ColdStaging
     hbm, staged, st, _ = _setup(dev, L=1, slots=4)

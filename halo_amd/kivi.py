@@ -20,6 +20,8 @@ import torch
 from . import _native as nat
 
 GROUP = 32
+# rows per work item of the unquantised recent rows in a KIVI launch
+RECENT_ITEM_ROWS = 32
 
 
 def block_bytes(D: int, bits: int = 2) -> int:
@@ -93,6 +95,30 @@ class KiviChunkRef:
         return int(self.blocks.shape[2]) * GROUP
 
 
+def plan_kivi(*, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype, cold, recent, device, split=None):
+    """The work plan of one KIVI decode launch: the KIVI block runs
+    ``cold`` (``KiviChunkRef``) in items of ``split`` tokens (default: about
+    two per resident workgroup slot), then the unquantised ``recent`` rows
+    (``decode.ChunkRef``) in items of ``RECENT_ITEM_ROWS``.
+
+    The KIVI items fill the resident workgroup slots in the first round; the
+    short recent-row items go last, into the slots that free up first,
+    instead of holding back a KIVI item to a second round.  They are cut into
+    32-row items (one plain tile each): they start when the first KIVI items
+    end and are latency-bound, so more, shorter items end sooner (131072-token
+    layer: 22.3 -> 21.6 us against one 128-row item per KV head)."""
+    from .decode import _num_cus, build_plan, choose_rep_t, choose_split
+    chunks = list(cold) + list(recent)
+    if not cold:  # no KIVI blocks yet: a plain decode launch
+        return build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=chunks, device=device, split=split)
+    if split is None:
+        n_sub = -(-(H // H_kv) // choose_rep_t(H // H_kv))
+        rows = sum(int(c.T) for c in chunks) * B * H_kv * n_sub
+        split = choose_split(rows, _num_cus(device), kivi=True)
+    return build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=chunks, device=device,
+                      split=RECENT_ITEM_ROWS, first=range(len(cold)), split_first=split)
+
+
 class KiviDecodeLayer:
     """Decode over a KIVI-quantised cold region plus unquantised recent rows.
 
@@ -107,18 +133,14 @@ class KiviDecodeLayer:
 
     def __init__(self, *, B: int, H: int, H_kv: int, D: int, dtype: torch.dtype, cold_blocks: torch.Tensor,
                  recent, device, chunk_tokens: int = 2048, split=None) -> None:
-        from .decode import build_plan
         if chunk_tokens % GROUP:
             raise AssertionError(f"chunk_tokens={chunk_tokens} must be a multiple of {GROUP}")
         n = int(cold_blocks.shape[2])
         per = chunk_tokens // GROUP
         cold = [KiviChunkRef(cold_blocks[:, :, j:min(j + per, n)], j * GROUP, True) for j in range(0, n, per)]
         self.B, self.H, self.D = B, H, D
-        # The KIVI items fill the resident workgroup slots in the first
-        # round; the short recent-row items go last, into the slots that free
-        # up first, instead of holding back a KIVI item to a second round.
-        self.plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, chunks=cold + list(recent or []),
-                               device=device, split=split, first=range(len(cold)))
+        self.plan = plan_kivi(B=B, H=H, H_kv=H_kv, D=D, dtype=dtype, cold=cold, recent=list(recent or []),
+                              device=device, split=split)
 
     def step(self, q: torch.Tensor, *, scale: float, out: torch.Tensor, lse=None, q_pos=None) -> None:
         from .decode import launch

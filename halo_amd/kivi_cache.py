@@ -197,7 +197,7 @@ class KIVICache(_BaseCache):
         query row i at position query_pos_offset + i (default T - T_q).
         Decode reads the blocks directly; T_q > 1 attends the dequantised
         blocks and the recent rows with the MFMA prefill."""
-        from .decode import build_plan, launch
+        from .decode import launch
         from .prefill import prefill_attention
         if layer_idx >= len(self._n_seen) or self._k_recent[layer_idx] is None:
             raise AssertionError(f"layer {layer_idx} has no cache")
@@ -217,7 +217,7 @@ class KIVICache(_BaseCache):
             per = self.chunk_tokens // GROUP
             cold = [kivi.KiviChunkRef(blocks[:, :, j:min(j + per, n)], j * GROUP, True, bits=self.bits)
                     for j in range(0, n, per)]
-            plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=q.dtype, chunks=cold + recent, device=q.device)
+            plan = kivi.plan_kivi(B=B, H=H, H_kv=H_kv, D=D, dtype=q.dtype, cold=cold, recent=recent, device=q.device)
             out = torch.empty((B, H, D), device=q.device, dtype=q.dtype)
             lse = torch.empty((B, H), device=q.device, dtype=torch.float32) if return_lse else None
             q_pos = torch.full((B,), q0, dtype=torch.int64, device=q.device)

@@ -182,6 +182,37 @@ def test_edge_cases(dev):
     _check(out2, lse2, ref2, ref2_lse, "float32")
 
 
+@pytest.mark.parametrize("D,H,H_kv", [(64, 8, 2), (128, 16, 2), (256, 6, 2)])
+@pytest.mark.parametrize("n_items", [12, 70, 130, 200])
+def test_merge_shapes_by_partials_per_group(dev, D, H, H_kv, n_items):
+    """The split-K merge takes a head's columns in slices (64 partials per
+    group or fewer: 32-column slices; up to 80 and up to 144: 16-column
+    slices) and one workgroup per head beyond that and whenever it reads and
+    writes the caller's m/l: every form against the float64 closed form."""
+    from halo_amd.decode import ChunkRef, build_plan, launch
+    split = 64
+    T = n_items * split - 17            # a short last item
+    x = decode_inputs(40 + n_items, B=1, H=H, H_kv=H_kv, T=T, D=D, dtype="bfloat16")
+    q, k, v = (_gpu(a, "bfloat16", dev) for a in (x.q, x.k, x.v))
+    plan = build_plan(B=1, H=H, H_kv=H_kv, D=D, dtype=torch.bfloat16, chunks=[ChunkRef(k, v, 0, True)],
+                      device=dev, split=split)
+    assert plan.n_work == plan.n_groups * n_items
+    scale = 1 / math.sqrt(D)
+    ref, ref_lse = A.attention_f64(x.q[:, :, 0], x.k, x.v, scale=scale)
+    out = torch.empty(1, H, D, device=dev, dtype=torch.bfloat16)
+    lse = torch.empty(1, H, device=dev)
+    launch(plan, q[:, :, 0], scale=scale, out=out, lse=lse)
+    _check(out, lse, ref, ref_lse, "bfloat16")
+    # read-and-write accumulators (one workgroup per head): from an empty
+    # accumulator the result is the attention's (m, l, o)
+    m = torch.full((1, H), -math.inf, device=dev)
+    l = torch.zeros((1, H), device=dev)
+    o = torch.zeros((1, H, D), device=dev)
+    launch(plan, q[:, :, 0], scale=scale, m=m, l=l, o=o, acc_mode=3)
+    fin = (o / l[..., None]).to(torch.bfloat16)
+    _check(fin, m + torch.log(l), ref, ref_lse, "bfloat16")
+
+
 def test_strided_views_need_no_copy(dev):
     """Chunks may be strided views of a larger cache (rows 16-byte aligned)."""
     from halo_amd.decode import ChunkRef, build_plan, launch

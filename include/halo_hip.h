@@ -521,8 +521,10 @@ int halo_stage_fills_read(const halo_fill* fills, int n, void* stream);
 /*
  * base[idx[i]] = vals[i] for i < n (entries with idx outside [0, n_elems)
  * are skipped), as kernels on `stream` whose pairs travel in the kernel
- * arguments: the host arrays are read during the call only.  The staging
- * cache commits and releases residency entries with it.  No counterpart in
+ * arguments: the host arrays are read during the call only.  For a policy of
+ * the caller's own that commits and releases residency entries on the
+ * compute stream (the halo_staging runtime does the same inside its
+ * segment-boundary kernel).  No counterpart in
  * the reference (whose tier directory is a host dict,
  * halo/memory_tier.py:133).
  */

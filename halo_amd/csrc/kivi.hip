@@ -1,4 +1,4 @@
-// KIVI-style 2/4-bit cold-chunk format: quantize and dequantize kernels
+// KIVI-style 2/4/8-bit cold-chunk format: quantize and dequantize kernels
 // (gfx950, wave64).  Byte/integer work bound by HBM; nothing here is a GEMM.
 //
 // Arithmetic: baselines/kivi_cache.py:44-78 with every operation rounded to
@@ -29,7 +29,8 @@
 // 4g..4g+3 of both 16-token halves).  So the P.V operand of one lane is 8
 // slots = 16 contiguous bits of one channel, its scales (or zeros) are 16
 // contiguous bytes of one group, and its p values are its own scores.
-// Code positions within a row: 4-bit codes, element e at bit 4e; 2-bit
+// Code positions within a row: 4- and 8-bit codes, element e at bit e*bits
+// (8-bit: one byte per code); 2-bit
 // codes, each 16-bit word holds 8 elements, the even ones (2j) at bits 2j
 // of its low byte and the odd ones (2j+1) at bits 8+2j of its high byte, so
 // that w | w << 8 holds elements 2j and 2j+1 at bits 2j and 16+2j: one mask
@@ -148,6 +149,25 @@ __device__ __forceinline__ uint32_t kivi_code_fma(float x, float4 p) {
   }
 }
 
+// Store a thread's NB packed code bytes (NB in {2, 4, 8, 16, 32}; dst aligned
+// to min(NB, 16) bytes) with vector stores.
+template <int NB>
+__device__ __forceinline__ void store_codes(uint8_t* dst, const uint64_t (&acc)[4]) {
+  static_assert(NB == 2 || NB == 4 || NB == 8 || NB == 16 || NB == 32, "packed code bytes per thread");
+  if constexpr (NB == 2) {
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)acc[0];
+  } else if constexpr (NB == 4) {
+    *reinterpret_cast<uint32_t*>(dst) = (uint32_t)acc[0];
+  } else if constexpr (NB == 8) {
+    *reinterpret_cast<uint64_t*>(dst) = acc[0];
+  } else {
+#pragma unroll
+    for (int h = 0; h < NB / 16; ++h)
+      reinterpret_cast<uint4*>(dst)[h] = make_uint4((uint32_t)acc[2 * h], (uint32_t)(acc[2 * h] >> 32),
+                                                    (uint32_t)acc[2 * h + 1], (uint32_t)(acc[2 * h + 1] >> 32));
+  }
+}
+
 // One workgroup per block, 256 threads.  The 32 x D K and V tiles are staged
 // in LDS in their storage dtype (16-byte loads; rows padded by 16 bytes so
 // column and row-run reads spread over the banks); pairs of threads reduce
@@ -252,7 +272,7 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
   constexpr int RKB = D * BITS / 8;          // K code bytes per token row
   {
     const int t = tid / (D / KR), e0 = (tid % (D / KR)) * KR;
-    uint64_t acc0 = 0, acc1 = 0;             // up to 128 bits (32 elements x 4 bits)
+    uint64_t acc[4] = {0, 0, 0, 0};          // up to 256 bits (32 elements x 8 bits)
     const uint4* row = reinterpret_cast<const uint4*>(&s_k[t * RS + e0]);
 #pragma unroll
     for (int v8 = 0; v8 < KR / 8; ++v8) {
@@ -265,17 +285,11 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
         const uint16_t xb = (uint16_t)(i & 1 ? w[i >> 1] >> 16 : w[i >> 1]);
         const uint32_t c = kivi_code_fma<DT, BITS>(from_bits<DT>(xb), pk);
         const int bit = kivi_bit<BITS>(8 * v8 + i);          // e0 is a multiple of 8
-        if (bit < 64) acc0 |= (uint64_t)c << bit;
-        else acc1 |= (uint64_t)c << (bit - 64);
+        acc[bit >> 6] |= (uint64_t)c << (bit & 63);
       }
     }
     uint8_t* dst = out + t * RKB + kivi_bit<BITS>(e0) / 8;
-    constexpr int NB = KR * BITS / 8;        // bytes this thread stores
-    if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)acc0;
-    else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)acc0;
-    else if constexpr (NB == 8) *reinterpret_cast<uint64_t*>(dst) = acc0;
-    else *reinterpret_cast<uint4*>(dst) = make_uint4((uint32_t)acc0, (uint32_t)(acc0 >> 32), (uint32_t)acc1,
-                                                     (uint32_t)(acc1 >> 32));
+    store_codes<KR * BITS / 8>(dst, acc);
   }
   // V codes: D rows (channels) x 32 slots; thread = (channel, run of VR
   // consecutive slots starting at a multiple of 8)
@@ -284,23 +298,17 @@ __global__ void __launch_bounds__(256) kivi_quantize_kernel(KiviQuantParams P) {
   {
     const int d = tid / (G / VR), s0 = (tid % (G / VR)) * VR;
     const int g = d / G;
-    uint64_t acc0 = 0, acc1 = 0;
+    uint64_t acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
       const int s = s0 + i, t = kivi_vtok(s);
       const float4 pv = s_vp[t * NG + g];
       const uint32_t c = kivi_code_fma<DT, BITS>(from_bits<DT>(s_v[t * RS + d]), pv);
       const int bit = kivi_bit<BITS>(s) - kivi_bit<BITS>(s0);
-      if (bit < 64) acc0 |= (uint64_t)c << bit;
-      else acc1 |= (uint64_t)c << (bit - 64);
+      acc[bit >> 6] |= (uint64_t)c << (bit & 63);
     }
     uint8_t* dst = out + C + 4 * D + d * VRB + kivi_bit<BITS>(s0) / 8;
-    constexpr int NB = VR * BITS / 8;
-    if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)acc0;
-    else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst) = (uint32_t)acc0;
-    else if constexpr (NB == 8) *reinterpret_cast<uint64_t*>(dst) = acc0;
-    else *reinterpret_cast<uint4*>(dst) = make_uint4((uint32_t)acc0, (uint32_t)(acc0 >> 32), (uint32_t)acc1,
-                                                     (uint32_t)(acc1 >> 32));
+    store_codes<VR * BITS / 8>(dst, acc);
   }
 }
 
@@ -351,7 +359,7 @@ __global__ void __launch_bounds__(256) kivi_dequant_kernel(KiviDequantParams P) 
 using namespace halo;
 
 extern "C" size_t halo_kivi_block_bytes(int D, int bits) {
-  if ((bits != 2 && bits != 4) || D <= 0 || D % kKiviG) return 0;
+  if ((bits != 2 && bits != 4 && bits != 8) || D <= 0 || D % kKiviG) return 0;
   return (size_t)kivi_block_bytes(D, bits);
 }
 
@@ -360,14 +368,16 @@ namespace {
 template <int DT, int D>
 int quant_bits(const KiviQuantParams& p, int bits, int n, hipStream_t st) {
   if (bits == 2) hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 2>), dim3(n), dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  else if (bits == 4) hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kivi_quantize_kernel<DT, D, 8>), dim3(n), dim3(256), 0, st, p);
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
 template <int DT, int D>
 int dequant_bits(const KiviDequantParams& p, int bits, int n, hipStream_t st) {
   if (bits == 2) hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 2>), dim3(n), dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  else if (bits == 4) hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 4>), dim3(n), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kivi_dequant_kernel<DT, D, 8>), dim3(n), dim3(256), 0, st, p);
   HALO_CHECK_HIP(hipGetLastError());
   return HALO_OK;
 }
@@ -380,7 +390,7 @@ extern "C" int halo_kivi_quantize(const void* k, int64_t k_stride_b, int64_t k_s
                                   void* blocks, int64_t blk_stride_b, int64_t blk_stride_h, void* stream) {
   HALO_CHECK_ARG(k && v && blocks, "null pointer");
   HALO_CHECK_ARG(dtype == HALO_F16 || dtype == HALO_BF16, "KIVI storage dtype must be fp16 or bf16");
-  HALO_CHECK_ARG(bits == 2 || bits == 4, "bits must be 2 or 4");
+  HALO_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");
   HALO_CHECK_ARG(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
   HALO_CHECK_ARG(B >= 0 && H_kv > 0 && T >= 0 && T % kKiviG == 0, "T must be a multiple of the group size 32");
   const int n_blk = T / kKiviG;
@@ -414,7 +424,7 @@ extern "C" int halo_kivi_dequantize(const void* blocks, int64_t blk_stride_b, in
                                     void* stream) {
   HALO_CHECK_ARG(k && v && blocks, "null pointer");
   HALO_CHECK_ARG(dtype == HALO_F16 || dtype == HALO_BF16, "KIVI storage dtype must be fp16 or bf16");
-  HALO_CHECK_ARG(bits == 2 || bits == 4, "bits must be 2 or 4");
+  HALO_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "bits must be 2, 4 or 8");
   HALO_CHECK_ARG(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
   HALO_CHECK_ARG(B >= 0 && H_kv > 0 && n_blocks >= 0, "bad sizes");
   const int64_t n = (int64_t)B * H_kv * n_blocks;

@@ -1,4 +1,4 @@
-"""KIVI-style 2/4-bit cold-chunk format on the GPU.
+"""KIVI-style 2/4/8-bit cold-chunk format on the GPU.
 
 ``quantize(k, v)`` packs K (per channel over 32 tokens) and V (per token
 over 32 channels) into self-contained 32-token blocks; ``dequantize``

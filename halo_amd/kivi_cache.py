@@ -55,8 +55,8 @@ class KIVICache(_BaseCache):
             super().__init__()
         if group_size != GROUP:
             raise AssertionError(f"KIVI blocks hold {GROUP} tokens; group_size={group_size} is not supported")
-        if bits not in (2, 4):
-            raise AssertionError(f"bits must be 2 or 4, got {bits}")
+        if bits not in (2, 4, 8):
+            raise AssertionError(f"bits must be 2, 4 or 8, got {bits}")
         if residual_length < 0:
             raise AssertionError("residual_length must be >= 0")
         self.bits = bits
@@ -195,9 +195,10 @@ class KIVICache(_BaseCache):
                           query_pos_offset: Optional[int] = None, return_lse: bool = False):
         """Attention of q (B, H, T_q, D) over the layer's cache, causal with
         query row i at position query_pos_offset + i (default T - T_q).
-        Decode reads the blocks directly; T_q > 1 attends the dequantised
-        blocks and the recent rows with the MFMA prefill."""
-        from .decode import launch
+        Decode reads 2-bit blocks directly; 4- and 8-bit decode and T_q > 1
+        attend the dequantised blocks and the recent rows (the decode kernel,
+        or the MFMA prefill)."""
+        from .decode import build_plan, launch
         from .prefill import prefill_attention
         if layer_idx >= len(self._n_seen) or self._k_recent[layer_idx] is None:
             raise AssertionError(f"layer {layer_idx} has no cache")
@@ -211,7 +212,7 @@ class KIVICache(_BaseCache):
         if q.dtype != k_rec.dtype:
             raise AssertionError(f"q dtype {q.dtype} != cache dtype {k_rec.dtype}")
         recent = [ChunkRef(k_rec, v_rec, n_seen, True)] if k_rec.shape[-2] > 0 else []
-        if T_q == 1:
+        if T_q == 1 and self.bits == 2:
             blocks = self.blocks(layer_idx)
             n = 0 if blocks is None else blocks.shape[2]
             per = self.chunk_tokens // GROUP
@@ -231,6 +232,19 @@ class KIVICache(_BaseCache):
             else:
                 kd, vd = kivi.dequantize(self.blocks(layer_idx), D=D, dtype=q.dtype, bits=self.bits)
             chunks.append(ChunkRef(kd, vd, 0, True))
+        if T_q == 1:
+            out = torch.empty((B, H, D), device=q.device, dtype=q.dtype)
+            lse = torch.empty((B, H), device=q.device, dtype=torch.float32) if return_lse else None
+            if chunks + recent:
+                plan = build_plan(B=B, H=H, H_kv=H_kv, D=D, dtype=q.dtype, chunks=chunks + recent, device=q.device)
+                q_pos = torch.full((B,), q0, dtype=torch.int64, device=q.device)
+                launch(plan, q[:, :, 0], scale=scale, q_pos=q_pos, out=out, lse=lse)
+            else:
+                out.zero_()
+                if lse is not None:
+                    lse.fill_(float("-inf"))
+            out = out.unsqueeze(2)
+            return (out, lse.unsqueeze(2)) if return_lse else out
         return prefill_attention(q, chunks + recent, scale=scale, q_start=q0, return_lse=return_lse)
 
 

@@ -390,7 +390,7 @@ int halo_halo_score(const float* attention, int K, int step, float alpha, float 
  */
 int halo_topk_sorted(const float* score, int K, int k, int64_t* idx_out, void* stream);
 
-/* ---- KIVI 2/4-bit cold-chunk format ------------------------------------ */
+/* ---- KIVI 2/4/8-bit cold-chunk format ---------------------------------- */
 
 /*
  * Block format: one block = 32 tokens of one (b, h_kv), all in one
@@ -402,9 +402,10 @@ int halo_topk_sorted(const float* score, int K, int k, int64_t* idx_out, void* s
  *             (V is grouped per token over 32 channels); slot 8g + j holds
  *             token 4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4)
  *   V scale   D/32 groups x 32 token slots (group-major), then V zero (same)
- * Code positions within a row: 4-bit codes, element e at bit 4e; 2-bit
- * codes, each 16-bit word holds 8 elements, the even ones (2j) at bits 2j of
- * its low byte and the odd ones (2j+1) at bits 8+2j of its high byte.
+ * Code positions within a row: 4- and 8-bit codes, element e at bit
+ * e*bits; 2-bit codes, each 16-bit word holds 8 elements, the even ones (2j)
+ * at bits 2j of its low byte and the odd ones (2j+1) at bits 8+2j of its
+ * high byte.  bits is 2, 4 or 8 (the decode kernel reads 2-bit blocks).
  * D=128, bits=2: 3072 bytes per block (5.33x smaller than fp16 K+V).
  * The reference keeps unpacked int8 codes plus separate scale/zero tensors
  * (baselines/kivi_cache.py:50-69, :121-195); this layout is this library's.

@@ -286,3 +286,28 @@ def test_generate_hook_keeps_a_callers_own_cache():
     own = object()
     kw = m.generate(past_key_values=own, use_cache=False)
     assert kw["past_key_values"] is own and kw["use_cache"] is False and m._halo_cache.resets == 2
+
+
+def test_kivi_from_memory_ratio_picks_bits():
+    """tests/test_kivi_cache.py:99-107: memory_ratio 4 -> 4 bits, 8 -> 2, 2 -> 8
+    (bits = max(16 // memory_ratio, 2))."""
+    from halo_amd.kivi_cache import KIVICache
+    assert KIVICache.from_memory_ratio(memory_ratio=4).bits == 4
+    assert KIVICache.from_memory_ratio(memory_ratio=8).bits == 2
+    assert KIVICache.from_memory_ratio(memory_ratio=2).bits == 8
+    assert KIVICache.from_memory_ratio(memory_ratio=16).bits == 2
+    with pytest.raises(AssertionError):
+        KIVICache(bits=3)
+
+
+def test_scorer_jaccard_extremes(small_config):
+    """tests/test_scorer.py:43-52: identical index sets 1, disjoint 0; both
+    empty 1 and a partial overlap |a & b| / |a | b| (halo/scorer.py:92-97)."""
+    import torch
+    from halo_amd.scorer import HALOScorer
+    s = HALOScorer(small_config)
+    a = torch.tensor([1, 2, 3, 4])
+    assert s.jaccard(a, torch.tensor([1, 2, 3, 4])) == pytest.approx(1.0)
+    assert s.jaccard(a, torch.tensor([5, 6, 7, 8])) == pytest.approx(0.0)
+    assert s.jaccard(torch.tensor([], dtype=torch.long), torch.tensor([], dtype=torch.long)) == pytest.approx(1.0)
+    assert s.jaccard(a, torch.tensor([3, 4, 5])) == pytest.approx(2 / 5)

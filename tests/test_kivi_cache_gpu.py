@@ -25,13 +25,13 @@ def _rows(rng, shape, dtype):
     return round_to(rng.standard_normal(shape).astype(np.float32), dtype)
 
 
-def _deq(k, v, n, dtype):
+def _deq(k, v, n, dtype, bits=2):
     """Oracle view of the cache after n tokens were demoted: dequantised
     blocks for [0, n), the raw rows after."""
     if n == 0:
         return k, v
-    kd, vd = K.unpack_blocks(K.pack_blocks(k[:, :, :n], v[:, :, :n], bits=2, dtype=dtype), D=k.shape[-1],
-                             bits=2, dtype=dtype)
+    kd, vd = K.unpack_blocks(K.pack_blocks(k[:, :, :n], v[:, :, :n], bits=bits, dtype=dtype), D=k.shape[-1],
+                             bits=bits, dtype=dtype)
     return np.concatenate([kd, k[:, :, n:]], axis=2), np.concatenate([vd, v[:, :, n:]], axis=2)
 
 
@@ -133,6 +133,47 @@ def test_attention_over_the_cache(dev, dtype, H, H_kv):
     assert np.abs(outp.float().cpu().numpy() - wp).max() <= 2e-2
     outl = lean.compute_attention(torch.from_numpy(qp).to(dev).to(TDT[dtype]), layer_idx=0)
     assert torch.equal(outl, outp)
+
+
+@pytest.mark.parametrize("dtype,bits", [("float16", 8), ("bfloat16", 4), ("bfloat16", 8)])
+def test_wider_codes_blocks_and_attention(dev, dtype, bits):
+    """4- and 8-bit caches (from_memory_ratio 4 and 2, as the reference maps
+    them): blocks and the returned cache bit-exact over updates; decode (over
+    the dequantised blocks: the fused kernel reads 2-bit blocks) and T_q > 1
+    against the float64 closed form."""
+    from halo_amd.kivi_cache import KIVICache
+    rng = np.random.default_rng(11)
+    B, H, H_kv, D = 1, 8, 2, 128
+    sizes = [200, 1, 63, 1, 40]
+    T = sum(sizes)
+    k = _rows(rng, (B, H_kv, T, D), dtype)
+    v = _rows(rng, (B, H_kv, T, D), dtype)
+    kg = torch.from_numpy(k).to(dev).to(TDT[dtype])
+    vg = torch.from_numpy(v).to(dev).to(TDT[dtype])
+    cache = KIVICache.from_memory_ratio(memory_ratio=16 // bits, residual_length=32)
+    assert cache.bits == bits
+    t = 0
+    for n in sizes:
+        kk, vv = cache.update(kg[:, :, t:t + n], vg[:, :, t:t + n], layer_idx=0)
+        t += n
+        n_seen = max(0, (t - 32) // 32 * 32)
+        assert cache._n_seen[0] == n_seen
+        if n_seen:
+            assert np.array_equal(cache.blocks(0).cpu().numpy(),
+                                  K.pack_blocks(k[:, :, :n_seen], v[:, :, :n_seen], bits=bits, dtype=dtype))
+        wk, wv = _deq(k[:, :, :t], v[:, :, :t], n_seen, dtype, bits)
+        assert np.array_equal(kk.float().cpu().numpy(), wk)
+        assert np.array_equal(vv.float().cpu().numpy(), wv)
+    scale = 1 / math.sqrt(D)
+    q = _rows(rng, (B, H, 1, D), dtype)
+    out, lse = cache.compute_attention(torch.from_numpy(q).to(dev).to(TDT[dtype]), layer_idx=0, return_lse=True)
+    ro, rl = A.attention_f64(q[:, :, 0], wk, wv, scale=scale)
+    assert np.abs(out[:, :, 0].float().cpu().numpy() - ro).max() <= 2e-2
+    assert np.abs(lse[:, :, 0].cpu().numpy() - rl).max() <= 2e-2
+    qp = _rows(rng, (B, H, 16, D), dtype)
+    outp = cache.compute_attention(torch.from_numpy(qp).to(dev).to(TDT[dtype]), layer_idx=0)
+    wp, _ = A.prefill_f64(qp, wk, wv, scale=scale, q_start=T - 16)
+    assert np.abs(outp.float().cpu().numpy() - wp).max() <= 2e-2
 
 
 def _tiny_models(dev, dtype):

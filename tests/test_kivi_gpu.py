@@ -1,4 +1,4 @@
-"""GPU parity of the KIVI 2/4-bit cold format: packed blocks and dequantised
+"""GPU parity of the KIVI 2/4/8-bit cold format: packed blocks and dequantised
 values bit-exact with the oracle; decode attention over quantised blocks
 plus unquantised recent rows within the 16-bit tolerance of the float64
 closed form over the dequantised cache."""
@@ -35,7 +35,8 @@ def _edge_cases(k, v):
 
 
 @pytest.mark.parametrize("dtype,bits,D", [("float16", 2, 128), ("bfloat16", 2, 128), ("float16", 4, 64),
-                                          ("float16", 2, 256)])
+                                          ("float16", 2, 256), ("float16", 8, 128), ("bfloat16", 8, 64),
+                                          ("bfloat16", 8, 256), ("float16", 4, 256)])
 def test_quantize_and_dequantize_bitexact(dev, dtype, bits, D):
     from halo_amd import kivi
     x = decode_inputs(4, B=1, H=4, H_kv=2, T=256, D=D, dtype=dtype, n_planted=2, sigma=10.0)

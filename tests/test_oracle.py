@@ -316,8 +316,9 @@ def test_kivi_roundtrip_bound():
     assert (np.abs(x - dq) <= bound + 1e-5).all()
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_kivi_codes_match_torch_ops(dtype):
+def test_kivi_codes_match_torch_ops(dtype, bits):
     """Per-op rounding in the storage dtype equals torch's evaluation of the
     reference expression (baselines/kivi_cache.py:64-78) on the same values."""
     torch = pytest.importorskip("torch")
@@ -327,11 +328,12 @@ def test_kivi_codes_match_torch_ops(dtype):
     x[0, 0, 0, :32] = 0.5                       # a constant group
     xt = torch.from_numpy(x).to(tdt)
     xe = xt.float().numpy()
-    codes, s, z = KV.quantize_last_axis(xe, bits=2, group_size=32, dtype=dtype)
+    codes, s, z = KV.quantize_last_axis(xe, bits=bits, group_size=32, dtype=dtype)
+    qmax = (1 << bits) - 1
     xg = xt.view(2, 3, 64, 4, 32)
     mn, mx = xg.amin(-1, keepdim=True), xg.amax(-1, keepdim=True)
-    ts = (mx - mn).clamp_min(1e-8) / 3
-    tq = ((xg - mn) / ts).round().clamp(0, 3)
+    ts = (mx - mn).clamp_min(1e-8) / qmax
+    tq = ((xg - mn) / ts).round().clamp(0, qmax)
     tq = torch.nan_to_num(tq, nan=0.0).to(torch.uint8)
     assert np.array_equal(codes, tq.numpy())
     assert np.array_equal(s, ts.float().numpy())

@@ -164,6 +164,10 @@ class HALOCacheChunked(HALOCache):
         k, _ = self._get_layer_kv(layer_idx)
         return (cold.rows if cold is not None else 0) + self._rows(k)
 
+    def get_max_cache_shape(self, layer_idx: int = 0):
+        """No static upper bound (halo/kv_cache_chunked.py:566-568)."""
+        return None
+
     def reset(self) -> None:
         if self._cold and torch.cuda.is_available():
             # decode launches read the pinned chunks in place: they must be

@@ -311,3 +311,9 @@ def test_scorer_jaccard_extremes(small_config):
     assert s.jaccard(a, torch.tensor([5, 6, 7, 8])) == pytest.approx(0.0)
     assert s.jaccard(torch.tensor([], dtype=torch.long), torch.tensor([], dtype=torch.long)) == pytest.approx(1.0)
     assert s.jaccard(a, torch.tensor([3, 4, 5])) == pytest.approx(2 / 5)
+
+
+def test_chunked_cache_has_no_static_bound():
+    """halo/kv_cache_chunked.py:566-568: get_max_cache_shape is None."""
+    from halo_amd.kv_cache_chunked import HALOCacheChunked
+    assert HALOCacheChunked().get_max_cache_shape() is None

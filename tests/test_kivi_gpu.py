@@ -22,15 +22,21 @@ def _gpu(a, dtype, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(TDT[dtype])
 
 
-def _edge_cases(k, v):
+def _edge_cases(k, v, bits=2):
     """Plant the edge groups of the format: a constant K channel group (zero
-    range: fp16 scale 0), a constant V token group, +/- extremes."""
+    range: fp16 scale 0), a constant V token group, +/- extremes, and a K
+    and a V group of ties (range qmax, half-integer values: the quotient
+    lands exactly on .5)."""
     k = k.copy()
     v = v.copy()
     k[0, 0, 0:32, 5] = 0.75          # constant K group (per channel, 32 tokens)
     v[0, 0, 3, 32:64] = -1.5         # constant V group (per token, 32 channels)
     k[0, -1, 40, 7] = 60.0           # large outlier
     v[0, -1, 70, v.shape[-1] - 5] = -60.0
+    qmax = (1 << bits) - 1
+    ties = np.minimum(np.array([0.0, float(qmax)] + [0.5 + j for j in range(30)], np.float32), qmax)
+    k[0, 0, 64:96, 9] = ties         # K channel group of ties
+    v[0, -1, 100, 0:32] = ties       # V token group of ties
     return k, v
 
 
@@ -40,7 +46,7 @@ def _edge_cases(k, v):
 def test_quantize_and_dequantize_bitexact(dev, dtype, bits, D):
     from halo_amd import kivi
     x = decode_inputs(4, B=1, H=4, H_kv=2, T=256, D=D, dtype=dtype, n_planted=2, sigma=10.0)
-    k, v = _edge_cases(x.k, x.v)
+    k, v = _edge_cases(x.k, x.v, bits)
     from oracle.inputs import round_to
     k, v = round_to(k, dtype), round_to(v, dtype)
     blocks = kivi.quantize(_gpu(k, dtype, dev), _gpu(v, dtype, dev), bits=bits)

@@ -365,6 +365,38 @@ def test_kivi_round_half_even_boundary():
     assert s.item() == 1.0 and codes[0, 0, :4].tolist() == [0, 0, 2, 3]
 
 
+def _tie_group(bits: int) -> np.ndarray:
+    """A 32-element group whose range is qmax (scale 1) holding half-integer
+    values, so (x - zero) / scale lands exactly on .5 for most of them (all
+    values exact in fp16 and bf16)."""
+    qmax = (1 << bits) - 1
+    g = np.array([0.0, float(qmax)] + [0.5 + j for j in range(30)], np.float32)
+    return np.minimum(g, qmax)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_kivi_ties_match_torch_ops(dtype, bits):
+    """Codes whose quotient is exactly k + 0.5 (and ties created by the
+    division, scale 2): the oracle against torch's evaluation of the
+    reference expression (baselines/kivi_cache.py:64-69), round half to even."""
+    torch = pytest.importorskip("torch")
+    tdt = getattr(torch, dtype)
+    qmax = (1 << bits) - 1
+    g1 = _tie_group(bits)
+    g2 = np.minimum(np.array([0.0, 2.0 * qmax] + [1.0 + 2 * j for j in range(30)], np.float32), 2.0 * qmax)
+    x = np.stack([g1, g2, -g1, g1 + 7.0])[None, None].astype(np.float32)    # (1, 1, 4, 32)
+    xt = torch.from_numpy(x).to(tdt)
+    xe = xt.float().numpy()
+    codes, s, z = KV.quantize_last_axis(xe, bits=bits, group_size=32, dtype=dtype)
+    mn, mx = xt.amin(-1, keepdim=True), xt.amax(-1, keepdim=True)
+    ts = (mx - mn).clamp_min(1e-8) / qmax
+    tq = torch.nan_to_num(((xt - mn) / ts).round().clamp(0, qmax), nan=0.0).to(torch.uint8)
+    assert np.array_equal(codes.reshape(tq.shape), tq.numpy())
+    ties = ((xe[0, 0, 0] - xe[0, 0, 0].min()) % 1.0) == 0.5
+    assert ties.sum() == min(qmax, 30)          # every half-integer below qmax is a tie
+
+
 def test_kivi_per_channel_k_groups_tokens():
     rng = np.random.default_rng(4)
     k = rng.standard_normal((1, 2, 64, 8)).astype(np.float32)

@@ -2,8 +2,8 @@
 
 Mirrors the reference's kernel tests (tests/test_triton_chunked.py:72-312)
 at the reference tolerances (rel-L2 1e-4 fp32 / 5e-3 bf16) and the
-north-star ones (max-abs 1e-5 fp32 outputs and LSE, 2e-2 bf16), calling the
-HIP path through the C-ABI.
+stricter max-abs ones of this path (1e-5 fp32 outputs and LSE, 2e-2 bf16),
+calling the HIP path through the C-ABI.
 """
 from __future__ import annotations
 

@@ -301,6 +301,45 @@ def kernel_level_c2(torch, layers, qs, *, scale, reps, with_scorer=True):
     return attn_avg, score_avg
 
 
+def bench_measured_peaks(torch, dev) -> dict:
+    """What this GPU reaches on plain work, beside the published peaks the
+    rooflines use: a 1 GiB device-to-device copy (bytes read + written), a
+    256 MiB pinned host-to-device copy (the host link) and square bf16 GEMMs
+    (torch.mm, library MFMA kernels; 8192^3 and 16384^3)."""
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+    n = 1 << 30
+    a = torch.ones(n, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    t_copy = timed(lambda: b.copy_(a), 10)
+    del a, b
+    h = torch.ones(256 << 20, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    t_h2d = timed(lambda: d.copy_(h, non_blocking=True), 5)
+    del h, d
+    gemm = {}
+    for m in (8192, 16384):
+        x = torch.randn((m, m), device=dev, dtype=torch.bfloat16)
+        y = torch.randn((m, m), device=dev, dtype=torch.bfloat16).contiguous()
+        z = torch.empty((m, m), device=dev, dtype=torch.bfloat16)
+        gemm[f"{m}^3"] = 2 * m ** 3 / timed(lambda: torch.mm(x, y, out=z), 10) / 1e12
+        del x, y, z
+    torch.cuda.empty_cache()
+    return {"hbm_copy_gbps": 2 * n / t_copy / 1e9, "host_to_device_gbps": (256 << 20) / t_h2d / 1e9,
+            "bf16_gemm_tflops": max(gemm.values()), "bf16_gemm_tflops_by_shape": gemm,
+            "note": "1 GiB device copy (read + write bytes), 256 MiB pinned H2D copy, bf16 torch.mm (square, "
+                    "best shape); the rooflines' peaks are the published 8 TB/s and 2.5 PFLOP/s"}
+
+
 def bench_prefill_c3(torch, dev, *, reps: int):
     """Chunked causal prefill, Llama-3-8B GQA shape: a 4096-token query block
     attends 28 prior chunks of 1024 rows plus itself (causal), bf16 MFMA.
@@ -747,7 +786,7 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None, help="rows per attention work item (default: planner)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill (MFMA), ragged-batch and KIVI measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin", "model", "long"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c4host", "c5", "dropin", "model", "long", "peaks"], default=None,
                     help="run one leg alone (C2 kernel level, chunked prefill, ragged batch, KIVI, drop-in) and print its reading")
     ap.add_argument("--unfused", action="store_true",
                     help="kernel-level leg: select with the standalone scorer kernel instead of in the attention kernel")
@@ -786,7 +825,8 @@ def main() -> int:
                "c3": lambda: bench_prefill_c3(torch, dev, reps=max(1, args.steps)),
                "c4": lambda: bench_ragged_c4(torch, dev, steps=max(1, args.steps)),
                "c5": lambda: bench_kivi_c5(torch, dev, steps=max(1, args.steps)),
-               "dropin": dropin}[args.only]
+               "dropin": dropin,
+               "peaks": lambda: bench_measured_peaks(torch, dev)}[args.only]
         print(json.dumps({"leg": args.only, **leg()}), flush=True)
         return 0
     n_cold = T // chunk - n_hot
@@ -942,6 +982,7 @@ def main() -> int:
         leg("ragged_c4_host_tier", "ragged host-tier leg", lambda: bench_ragged_c4_host(torch, dev, steps=40))
         leg("model_decode", "model decode leg", lambda: bench_model_decode(torch, dev))
         leg("long_context_128k", "long-context leg", lambda: bench_long_context(torch, dev))
+        leg("measured_peaks", "measured peaks", lambda: bench_measured_peaks(torch, dev))
         result["extra"] = extra
     if not args.no_cpu_baseline:
         log("cpu baseline")

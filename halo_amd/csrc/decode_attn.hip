@@ -1145,11 +1145,21 @@ __device__ __forceinline__ void plain_rows_mfma(const DecodeParams& P, const Pla
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const bool valid = nb * 16 + kg * 4 + c < nrows;
-            sv[nb][c] = valid ? sc[nb][c] * P.scale2 : -INFINITY;
-            bm = fmaxf(bm, sv[nb][c]);
-          }
+          for (int c = 0; c < 4; ++c) sv[nb][c] = sc[nb][c] * P.scale2;
+        if (nrows < TILE) {  // a short tile (the slice's last): mask rows past it
+          // The empty volatile asm keeps this a real (wave-uniform) branch
+          // instead of compares and selects on every tile.
+          asm volatile("");
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (nb * 16 + kg * 4 + c >= nrows) sv[nb][c] = -INFINITY;
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) bm = fmaxf(bm, sv[nb][c]);
         bm = rows4_max(bm);
         const float m_new = fmaxf(m_lane, bm);
         const float ms = (m_new == -INFINITY) ? 0.f : m_new;
@@ -1840,6 +1850,10 @@ decode_attn_kivi_kernel(DecodeParams P) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) sv[pb][nb][c] = __builtin_fmaf(sc[pb][nb][c], cs, zs[pb][c]);
     if (nrw[0] < 32 || nrw[1] < 32) {  // a short block (the run's last): mask rows past it
+      // The empty volatile asm keeps this a real (wave-uniform) branch: the
+      // compiler would otherwise turn the rare mask into compares and
+      // selects that every pair executes.
+      asm volatile("");
 #pragma unroll
       for (int pb = 0; pb < 2; ++pb)
 #pragma unroll

@@ -70,7 +70,7 @@ class StagingDesc(ctypes.Structure):
         ("write_allocate", _i32), ("fill_mode", _i32), ("track_busy", _i32), ("sels_per_layer", _i32),
         ("residency", _c_void_p), ("feedback", _c_void_p), ("slot_addr", _c_void_p), ("chunk_addr", _c_void_p),
         ("chunk_nbytes", _c_void_p), ("n_cold_per_unit", _c_void_p), ("copy_stream", _c_void_p),
-        ("urgent_stream", _c_void_p),
+        ("urgent_stream", _c_void_p), ("copy_stream2", _c_void_p),
     ]
 
 

@@ -28,7 +28,9 @@
 //
 // Ordering (no kernel observes a change while it runs):
 //  * a fill copies a chunk into a slot that no residency entry names, on a
-//    copy stream, followed by an event;
+//    copy stream, followed by an event (each slot has its own event, and a
+//    filling slot is never evicted or refilled, so fills on different copy
+//    streams need no order among themselves);
 //  * a fill is committed (its residency entry stored on the compute stream)
 //    before the next launches of its layer once its event has completed --
 //    or at once after a compute-stream wait for the event when it is urgent
@@ -66,7 +68,8 @@ struct halo_staging {
   bool wa = false, kernel_fills = false, track_busy = false;
   int32_t* dev_i32 = nullptr;  // residency (U * n) then the write-allocate slot per layer (L)
   const float* feedback = nullptr;
-  hipStream_t copy = nullptr, urgent = nullptr;
+  hipStream_t copy = nullptr, urgent = nullptr, copy2 = nullptr;
+  uint32_t fill_seq = 0;  // regular DMA fills issued (alternates the copy streams)
   std::vector<uint64_t> dst, src;       // (U, S, 2) slot K/V, (U, n, 2) chunk K/V addresses
   std::vector<int64_t> nbytes;          // (U, n) bytes per K (or V) tensor
   std::vector<int32_t> ncold;           // (U) cold chunks of each unit (<= n)
@@ -343,6 +346,9 @@ int account(halo_staging* h, const float* fb, int lo, int hi, hipStream_t comput
 
 int issue(halo_staging* h, const Pending& p) {
   hipStream_t s = (p.urgent && h->urgent != nullptr) ? h->urgent : h->copy;
+  // DMA fills alternate between the two copy streams (two engines overlap
+  // each copy's start-up)
+  if (s == h->copy && h->copy2 != nullptr && !h->kernel_fills && (h->fill_seq++ & 1)) s = h->copy2;
   const size_t sk = ((size_t)p.unit * h->S + p.slot) * 2, ck = ((size_t)p.unit * h->n + p.chunk) * 2;
   const int64_t nb = h->nbytes[(size_t)p.unit * h->n + p.chunk];
   halo_fill f;
@@ -503,6 +509,7 @@ extern "C" int halo_staging_create(const halo_staging_desc* d, halo_staging** ou
   h->feedback = d->feedback;
   h->copy = static_cast<hipStream_t>(d->copy_stream);
   h->urgent = static_cast<hipStream_t>(d->urgent_stream);
+  h->copy2 = static_cast<hipStream_t>(d->copy_stream2);
   const size_t L = h->L, U = h->U, n = h->n, S = h->S;
   h->dst.assign(d->slot_addr, d->slot_addr + U * S * 2);
   h->src.assign(d->chunk_addr, d->chunk_addr + U * n * 2);

@@ -558,7 +558,14 @@ int halo_store_i32(int32_t* base, int64_t n_elems, const int64_t* idx, const int
  *   chunk_nbytes:(U, n_cold) bytes of one chunk's K (= its V);
  *   n_cold_per_unit: (U) cold chunks of each unit (NULL: n_cold each);
  *   copy_stream / urgent_stream: where fills run (urgent: fills the next
- *                launch of their layer waits for; NULL = copy_stream).
+ *                launch of their layer waits for; NULL = copy_stream);
+ *   copy_stream2: NULL, or a second stream for the other fills: copies then
+ *                alternate between copy_stream and copy_stream2, so two DMA
+ *                engines overlap each copy's start-up (4 MiB host-to-device
+ *                pieces with an event after each: 56 GB/s over two streams
+ *                against 46 GB/s on one); fills then land sooner but leave
+ *                less of the link to chunks read in place.  Fill mode 1
+ *                (copy kernels) keeps to copy_stream.
  * keep in [top_k, n_slots] best-scoring chunks per unit are staged; at most
  * max_inflight fills in flight; `spare` slots per unit kept free;
  * `ring` feedback entries in flight (>= segments per step + 1);
@@ -577,6 +584,7 @@ typedef struct halo_staging_desc {
   const int32_t* n_cold_per_unit;
   void* copy_stream;
   void* urgent_stream;
+  void* copy_stream2;
 } halo_staging_desc;
 
 /* Counters of a staging cache; ns_* are host nanoseconds spent planning

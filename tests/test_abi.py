@@ -53,11 +53,12 @@ def test_select_cfg_layout_matches_header():
 
 
 def test_staging_structs_match_header():
-    """halo_staging_desc: 12 int32 then 8 pointers (112 bytes);
+    """halo_staging_desc: 12 int32 then 9 pointers (120 bytes);
     halo_staging_stats: 14 int64."""
     from halo_amd import _native as nat
-    assert ctypes.sizeof(nat.StagingDesc) == 112
+    assert ctypes.sizeof(nat.StagingDesc) == 120
     assert nat.StagingDesc.residency.offset == 48 and nat.StagingDesc.urgent_stream.offset == 104
+    assert nat.StagingDesc.copy_stream2.offset == 112
     assert ctypes.sizeof(nat.StagingStats) == 112 and nat.StagingStats.evictions_while_busy.offset == 80
 
 

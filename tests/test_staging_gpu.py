@@ -204,6 +204,8 @@ def test_staging_validates_its_inputs(dev):
         ColdStaging(hbm, n_slots=4)              # cold chunks in HBM, not pinned host memory
     with pytest.raises(AssertionError):
         ColdStaging(staged, n_slots=4, keep=2)   # keep below top_k
+    with pytest.raises(AssertionError):
+        ColdStaging(staged, n_slots=4, copy_streams=3)
 
 
 @pytest.mark.parametrize("write_allocate", [True, False])
@@ -254,12 +256,14 @@ def test_write_allocate_commits_the_rows_read_in_place(dev, write_allocate):
             assert torch.equal(st._slot_v[li][s].cpu(), lay.cold[c].v), (li, s, c)
 
 
-def test_benchmark_loop_matches_all_hbm_every_step(dev):
+@pytest.mark.parametrize("copy_streams", [1, 2])
+def test_benchmark_loop_matches_all_hbm_every_step(dev, copy_streams):
     """The timed loop of the benchmark (``bench.refetch_run``: segment
     graphs, commits before each segment, feedback one segment late, fills
     and evictions planned while the next segments run, no synchronisation
     between steps), at a small scale with evictions (rho 0.8, 6 slots for
-    12 cold chunks): every step's output, LSE and picks, copied out in stream
+    12 cold chunks), with the fills on one copy stream or alternating
+    between two: every step's output, LSE and picks, copied out in stream
     order, equal those of the all-HBM layers bit for bit; fills, commits and
     evictions were issued while launches were still queued."""
     import bench
@@ -283,7 +287,7 @@ def test_benchmark_loop_matches_all_hbm_every_step(dev):
 
     # count what the runtime issues while the replay stream still has work queued
     from halo_amd.staging import ColdStaging
-    st = ColdStaging(staged, n_slots=6, keep=4, max_inflight=6, track_busy=True)
+    st = ColdStaging(staged, n_slots=6, keep=4, max_inflight=6, track_busy=True, copy_streams=copy_streams)
     bench.refetch_run(torch, staged, st, qtraj, warmup=0, steps=steps, scale=scale, label="test", segments=2,
                       record=record, lses=lses)
     torch.cuda.synchronize()

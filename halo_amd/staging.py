@@ -148,6 +148,8 @@ class ColdStaging:
             raise AssertionError(f"keep={self.keep} must be in [top_k={self.top_k}, n_slots={self.n_slots}]")
         if fill_mode not in _FILL_MODE:
             raise AssertionError("fill_mode must be 'kernel' or 'dma'")
+        if copy_streams not in (1, 2):
+            raise AssertionError(f"copy_streams must be 1 or 2, got {copy_streams}")
         self.fill_mode = fill_mode
         self.spare = int(spare)
         self._max_inflight = int(max_inflight)
@@ -243,8 +245,6 @@ class ColdStaging:
         # stream of their own, so they share the link with the prefetches
         # queued before them instead of waiting behind them
         self._urgent = torch.cuda.Stream(device=dev) if urgent_stream else None
-        if copy_streams not in (1, 2):
-            raise AssertionError(f"copy_streams must be 1 or 2, got {copy_streams}")
         self._copy2 = torch.cuda.Stream(device=dev) if copy_streams == 2 else None
         self._addr = (dst, src, nbytes, ncold)    # read at creation; kept for inspection
         d = nat.StagingDesc(n_layers=L, n_cold=n, n_slots=self.n_slots, top_k=k, keep=self.keep,
